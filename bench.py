@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-native matmul on one MI355X: weight GB/s (% of HBM peak) for the
+Q4_K GEMV 14336x4096 at M=1 (the `value`) and M=16, on seeded synthetic packed weights.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+A step is one projection call: Q8_K quantization of the activations, then the fused
+dequantize-and-multiply kernel over the packed weight. The timed region replays a HIP graph
+of exactly K captured steps (so Python launch overhead is not measured), bracketed by
+synchronizations. Each step reads a different copy of the weight (the copies together exceed
+1 GiB), so the 256 MB Infinity Cache cannot serve repeats: every weight byte comes from HBM.
+
+roofline: the matmul kernel alone, timed with a pair of HIP events around every launch on the
+launch stream (the launches are queued behind a short spin kernel so the GPU never waits for the
+host); achieved = algorithmic bytes per launch / mean launch time.
+
+cpu_baseline: the reference's own C kernel `mx_gemm` (built from its sources into
+oracle/_ref/libmx_ref.so) on the host cores, M=1, same weight, ~10 s of repeated calls.
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+N, K = 14336, 4096
+Q4_K = 12
+SEED_W, SEED_X = 2, 1002
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(m: int) -> int:
+    """Bytes one launch must move at minimum: the packed weight once, the Q8_K activations
+    (int8 values, one fp32 scale and 16 int16 sums per 256 values) and the fp32 outputs."""
+    nb = K // 256
+    return N * (K // 256) * 144 + m * (K + nb * 4 + nb * 32) + m * N * 4
+
+
+def weight_bytes() -> int:
+    return N * (K // 256) * 144
+
+
+def cpu_has_avx2() -> bool:
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    return all(f in flags for f in (" avx2", " fma", " f16c"))
+
+
+def cpu_baseline(w_np, x_np, seconds: float):
+    """Reference C kernel on the host: median call time over ~`seconds` of repeats."""
+    if not cpu_has_avx2():
+        log("host CPU lacks AVX2/FMA/F16C: no CPU baseline")
+        return None
+    from oracle.native import REF_LIB, OracleGemm, RefGemm, default_threads
+
+    threads = default_threads()
+    if REF_LIB.exists():
+        impl, kind = RefGemm(), "reference"
+    else:
+        impl, kind = OracleGemm(), "port"
+    impl.gemm(Q4_K, w_np, x_np, N, K, threads)  # warm-up (thread pool, page faults)
+    impl.gemm(Q4_K, w_np, x_np, N, K, threads)
+    times = []
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds and len(times) < 100000:
+        t0 = time.perf_counter()
+        impl.gemm(Q4_K, w_np, x_np, N, K, threads)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(weight_bytes() / med / 1e9, 2),
+        "unit": "weight GB/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": f"Q4_K 14336x4096 M=1 x {len(times)} calls of mx_gemm over "
+                  f"{time.perf_counter() - start:.1f} s, median {med * 1e3:.3f} ms/call",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=0, help="weight copies rotated (0: > 1 GiB)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the per-launch kernel timing loop (for rocprofv3 --pmc runs)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (scale for HBM counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              "(the kernels shard by output rows; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from matricxon_amd import synthetic as S
+    from matricxon_amd.gemm import HipGemm
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gemm = HipGemm.get()
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    w_np = S.packed_weight(Q4_K, N, K, seed=SEED_W)
+    w0 = torch.from_numpy(w_np).to(dev)
+    copies = args.copies or math.ceil((1 << 30) / w0.numel()) + 1
+    weights = [w0] + [w0.clone() for _ in range(copies - 1)]
+    log(f"{copies} weight copies, {copies * w0.numel() / 2**20:.0f} MiB rotated")
+
+    results = {}
+    for m in (1, 16):
+        x = torch.from_numpy(S.activations(m, K, seed=SEED_X + m)).to(dev)
+        ws = torch.empty(gemm.workspace_bytes(Q4_K, m, K), dtype=torch.uint8, device=dev)
+        y = torch.empty((m, N), dtype=torch.float32, device=dev)
+        ref_y = gemm.matmul(Q4_K, w0, x, N, K).clone()
+
+        def step(i: int) -> None:
+            gemm.quantize_into(x, ws)
+            gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
+
+        # -- per-launch kernel timing (roofline) -----------------------------------------
+        gemm.quantize_into(x, ws)
+        n_ev = max(args.steps, 50)
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+        for i in range(args.warmup):
+            gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
+        torch.cuda.synchronize()
+        if hasattr(torch.cuda, "_sleep"):
+            torch.cuda._sleep(20_000_000)  # keep the GPU busy while the launches are queued
+        for i in range(n_ev):
+            starts[i].record()
+            gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
+            ends[i].record()
+        torch.cuda.synchronize()
+        kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+        kern_mean = statistics.fmean(kern_ms)
+        log(f"M={m}: kernel mean {kern_mean * 1e3:.2f} us, median "
+            f"{statistics.median(kern_ms) * 1e3:.2f} us over {n_ev} launches")
+        if not torch.equal(y, ref_y):
+            raise SystemExit(f"M={m}: kernel-only result differs from the full call")
+        if args.kernel_only:
+            results[m] = {"kernel_us": kern_mean * 1e3}
+            continue
+
+        # -- timed region: a graph of exactly K steps ------------------------------------
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                for i in range(args.steps):
+                    step(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph.replay()  # untimed replay, checked against the eager result
+        torch.cuda.synchronize()
+        if not torch.equal(y, ref_y):
+            raise SystemExit(f"M={m}: graph replay result differs from the eager call")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        if not torch.equal(y, ref_y):
+            raise SystemExit(f"M={m}: timed replay result differs from the eager call")
+        ms_step = elapsed * 1e3 / args.steps
+        results[m] = {
+            "ms_per_step": ms_step,
+            "weight_gbs": weight_bytes() / (ms_step * 1e-3) / 1e9,
+            "rows_per_s": N / (ms_step * 1e-3),
+            "kernel_us": kern_mean * 1e3,
+            "kernel_weight_gbs": weight_bytes() / (kern_mean * 1e-3) / 1e9,
+            "kernel_alg_gbs": algorithmic_bytes(m) / (kern_mean * 1e-3) / 1e9,
+        }
+        log(f"M={m}: {ms_step * 1e3:.2f} us/step, {results[m]['weight_gbs']:.0f} weight GB/s "
+            f"(kernel {results[m]['kernel_weight_gbs']:.0f} GB/s)")
+        del graph
+
+    if args.calibrate_copy:
+        nbytes = args.calibrate_copy << 20
+        a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {nbytes} bytes read and written per copy kernel")
+
+    if args.kernel_only:
+        print(json.dumps({"kernel_only": True, **{f"m{m}": r for m, r in results.items()}}))
+        return 0
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w_np, S.activations(1, K, seed=SEED_X + 1), args.cpu_seconds)
+
+    traffic = None
+    tf = REPO / "profiles" / "q4k_gemv_14336x4096_m1_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+
+    r1, r16 = results[1], results[16]
+    line = {
+        "metric": "weight GB/s (% of HBM peak) for Q4_K GEMV 14336x4096 at M=1 and M=16",
+        "value": round(r1["weight_gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r1["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8",
+        "data": "synthetic (seeded packed Q4_K blocks, N(0,1) activations)",
+        "config": {
+            "workload": "Q4_K GEMV 14336x4096, M=1 (config 2); weights rotated over "
+                        f"{copies} HBM copies",
+            "type": "Q4_K", "N": N, "K": K, "M": 1,
+            "pct_of_hbm_peak": round(100 * r1["weight_gbs"] / HBM_PEAK_GBS, 1),
+            "rows_per_s": round(r1["rows_per_s"]),
+            "m16": {"weight_gbs": round(r16["weight_gbs"], 1),
+                    "pct_of_hbm_peak": round(100 * r16["weight_gbs"] / HBM_PEAK_GBS, 1),
+                    "ms_per_step": round(r16["ms_per_step"], 5),
+                    "kernel_us": round(r16["kernel_us"], 2),
+                    "rows_per_s": round(r16["rows_per_s"])},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(r1["kernel_alg_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r1["kernel_alg_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "gemv_kernel<Q4_K, M=1>",
+            "kernel_us": round(r1["kernel_us"], 3),
+            "bytes_per_launch": algorithmic_bytes(1),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,108 @@
+/*
+ * matricxon_amd: quantized-native matmul over packed GGUF blocks on AMD Instinct MI355X (gfx950).
+ *
+ * C ABI of libmatricxon_amd.so. Plain pointers and sizes only. All array pointers are DEVICE
+ * pointers (HBM) unless stated otherwise; `stream` is a hipStream_t (NULL = the null stream).
+ * Every call is asynchronous on `stream`, keeps no pointer after it returns and allocates no
+ * device memory: scratch space is the caller's `workspace`.
+ *
+ * Status codes (the reference's convention, app/native/src/mx_gemm.c:217-218, extended):
+ *   0  ok
+ *  -1  unsupported type or shape (the caller keeps another path; app/native/gemm.py:94-103)
+ *  -2  workspace missing or too small (the reference's "out of memory")
+ *  -3  kernel launch error (the HIP error string is available from mxa_last_error())
+ *
+ * GGML type ids (app/gguf/constants.py:24-59): Q8_0 = 8, Q4_K = 12, Q6_K = 14, IQ4_XS = 23.
+ */
+#ifndef MATRICXON_AMD_H
+#define MATRICXON_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXA_TYPE_Q8_0 8
+#define MXA_TYPE_Q4_K 12
+#define MXA_TYPE_Q6_K 14
+#define MXA_TYPE_IQ4_XS 23
+
+#define MXA_OK 0
+#define MXA_ERR_UNSUPPORTED (-1)
+#define MXA_ERR_WORKSPACE (-2)
+#define MXA_ERR_LAUNCH (-3)
+
+/* Build description for the startup log.
+ * Replaces `mx_build_info` (app/native/src/mx_gemm.c:291-314). Host-only, no GPU call. */
+const char *mxa_build_info(void);
+
+/* 1 when mxa_gemm handles (ggml_type, in_features): one of the four types and in_features a
+ * positive multiple of 256; 0 otherwise.
+ * Replaces `mx_supports` (app/native/src/mx_gemm.c:209-215). Host-only. */
+int mxa_supports(int ggml_type, int in_features);
+
+/* Bytes of one packed row of `in_features` values (0 when unsupported). Host-only. */
+size_t mxa_row_bytes(int ggml_type, int in_features);
+
+/* Workspace bytes mxa_gemm / mxa_gemm_multi need for n_tokens rows of in_features (the Q8_K
+ * activation blocks; 0 for IQ4_XS, which reads the float activations directly). Host-only. */
+size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features);
+
+/* y (n_tokens, out_features) fp32 = x (n_tokens, in_features) fp32 @ W.T, W the packed rows
+ * (out_features, row_bytes) in GGUF order. The activations are quantized to Q8_K into
+ * `workspace` first (except for IQ4_XS), exactly as the reference C kernel does.
+ * Replaces `mx_gemm` (app/native/src/mx_gemm.c:219-288) and, on the GPU, the dequantize +
+ * F.linear of `DevicePackedLinear.forward` (app/architectures/device_packed.py:53-63). */
+int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_tokens,
+             int out_features, int in_features, void *workspace, size_t workspace_bytes,
+             void *stream);
+
+/* mxa_gemm without its first step: `workspace` already holds the Q8_K activations of x
+ * (written by mxa_quantize_q8_k for the same n_tokens and in_features), so only the matmul
+ * kernel runs. `x` is read only for IQ4_XS (float activations) and may be NULL otherwise.
+ * The reference has no separate entry: this is the second half of `mx_gemm`
+ * (app/native/src/mx_gemm.c:252-284), for callers that quantize once for several weights. */
+int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_tokens,
+                 int out_features, int in_features, const void *workspace,
+                 size_t workspace_bytes, void *stream);
+
+/* Up to 4 packed weights sharing one input (q/k/v, gate/up): one activation quantization, then
+ * each weight's output columns written after the previous weight's, y (n_tokens, sum outs).
+ * `types`, `ws` (device pointers) and `outs` are HOST arrays of n entries.
+ * Replaces `mx_gemm_multi` (app/native/src/mx_gemm_multi.c:123-176); unlike the reference it
+ * also accepts prefill-sized n_tokens (the reference returns -1 there). */
+int mxa_gemm_multi(int n, const int *types, const void *const *ws, const int *outs,
+                   const float *x, float *y, int n_tokens, int in_features, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/* Q8_K activation quantization of x (n_tokens, in_features) into the workspace layout
+ * q int8 (n_tokens, K) | d fp32 (n_tokens, K/256) | bsums int16 (n_tokens, K/256, 16), each
+ * part starting on a 256-byte boundary (see mxa_workspace_bytes).
+ * Replaces `mx_quantize_row_q8_k` (app/native/src/mx_common.c:42-69). */
+int mxa_quantize_q8_k(const float *x, int n_tokens, int in_features, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* Bit-exact dequantization of n_blocks packed blocks to fp32 (block_size values each).
+ * Replaces `TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:323-325), itself a
+ * mirror of the numpy `QuantStrategy.dequantize`. */
+int mxa_dequantize(int ggml_type, const void *blocks, long long n_blocks, float *out,
+                   void *stream);
+
+/* Rows `rows[0..n_rows)` (device int32 indices into the n_src_rows packed rows of `w`) of a
+ * packed matrix with row_width values per row, dequantized bit-exactly to out (n_rows,
+ * row_width) fp32; an index outside [0, n_src_rows) gives a row of NaN.
+ * Replaces `mx_dequant_rows` (app/native/src/mx_dequant_rows.c:253-281) and the per-lookup
+ * dequant of `DevicePackedEmbedding.forward` (app/architectures/device_packed.py:81-84). */
+int mxa_dequant_rows(int ggml_type, const void *w, long long n_src_rows, const int32_t *rows,
+                     int n_rows, int row_width, float *out, void *stream);
+
+/* Text of the last HIP error seen by this library on the calling thread ("" if none). */
+const char *mxa_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MATRICXON_AMD_H */

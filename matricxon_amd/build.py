@@ -1,0 +1,66 @@
+"""Builds libmatricxon_amd.so in-tree from csrc/*.hip with hipcc for gfx950.
+
+    python -m matricxon_amd.build
+
+The library is written to matricxon_amd/libmatricxon_amd.so through a temp file and a rename,
+so a concurrently starting process never loads a half-written file (the pattern of the
+reference's loader, app/native/library.py:70-91).
+"""
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+LIB_NAME = "libmatricxon_amd.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    # every float rounding step is explicit in the sources (bit-exact dequant and folds)
+    "-ffp-contract=off",
+    # no packed-FP32 instructions (v_pk_*_f32) anywhere in the device code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found (ROCm is required to build matricxon_amd)")
+    return path
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False) -> Path:
+    """Compiles every csrc/*.hip into LIB_PATH; raises RuntimeError with the compiler output on
+    failure."""
+    fd, tmp = tempfile.mkstemp(dir=PKG_DIR, suffix=".so.tmp")
+    os.close(fd)
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *map(str, sources())]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        Path(tmp).unlink(missing_ok=True)
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
+    os.chmod(tmp, 0o755)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,180 @@
+// extern "C" entry points of libmatricxon_amd.so (declared in include/matricxon_amd.h):
+// argument checks, workspace layout, kernel dispatch, status codes.
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/matricxon_amd.h"
+#include "mxa_kernels.hpp"
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+int check_launch() {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return MXA_OK;
+  snprintf(g_last_error, sizeof g_last_error, "%s", hipGetErrorString(e));
+  return MXA_ERR_LAUNCH;
+}
+
+bool known_type(int t) {
+  return t == MXA_TYPE_Q8_0 || t == MXA_TYPE_Q4_K || t == MXA_TYPE_Q6_K || t == MXA_TYPE_IQ4_XS;
+}
+
+int block_elems(int t) { return t == MXA_TYPE_Q8_0 ? 32 : 256; }
+
+int block_bytes(int t) {
+  switch (t) {
+    case MXA_TYPE_Q8_0: return 34;
+    case MXA_TYPE_Q4_K: return 144;
+    case MXA_TYPE_Q6_K: return 210;
+    case MXA_TYPE_IQ4_XS: return 136;
+    default: return 0;
+  }
+}
+
+bool needs_q8k(int t) { return t != MXA_TYPE_IQ4_XS; }
+
+mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
+  mxa::Act act;
+  act.q = a ? a->q : nullptr;
+  act.d = a ? a->d : nullptr;
+  act.bsums = a ? a->bsums : nullptr;
+  act.x = x;
+  act.k = k;
+  act.nb = k / mxa::QK;
+  return act;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mxa_build_info(void) {
+  return "matricxon_amd gfx950: q8k-quantize, bit-exact dequant (Q8_0/Q4_K/Q6_K/IQ4_XS), "
+         "dot4 decode GEMV (M<=16 per pass)";
+}
+
+int mxa_supports(int ggml_type, int in_features) {
+  return known_type(ggml_type) && in_features > 0 && in_features % mxa::QK == 0;
+}
+
+size_t mxa_row_bytes(int ggml_type, int in_features) {
+  if (!mxa_supports(ggml_type, in_features)) return 0;
+  return (size_t)(in_features / block_elems(ggml_type)) * block_bytes(ggml_type);
+}
+
+size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features) {
+  if (!mxa_supports(ggml_type, in_features) || n_tokens <= 0) return 0;
+  return needs_q8k(ggml_type) ? mxa::act_bytes(n_tokens, in_features) : 0;
+}
+
+int mxa_quantize_q8_k(const float* x, int n_tokens, int in_features, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  if (x == nullptr || n_tokens <= 0 || in_features <= 0 || in_features % mxa::QK != 0)
+    return MXA_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+    return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, in_features);
+  mxa::launch_quantize_q8k(x, a, n_tokens, in_features, (hipStream_t)stream);
+  return check_launch();
+}
+
+int mxa_gemm(int ggml_type, const void* w, const float* x, float* y, int n_tokens,
+             int out_features, int in_features, void* workspace, size_t workspace_bytes,
+             void* stream) {
+  const int outs[1] = {out_features};
+  const int types[1] = {ggml_type};
+  const void* ws[1] = {w};
+  return mxa_gemm_multi(1, types, ws, outs, x, y, n_tokens, in_features, workspace,
+                        workspace_bytes, stream);
+}
+
+int mxa_gemm_q8k(int ggml_type, const void* w, const float* x, float* y, int n_tokens,
+                 int out_features, int in_features, const void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (!mxa_supports(ggml_type, in_features) || w == nullptr || y == nullptr || n_tokens <= 0 ||
+      out_features <= 0)
+    return MXA_ERR_UNSUPPORTED;
+  mxa::ActBuffers buf{};
+  const mxa::ActBuffers* abuf = nullptr;
+  if (needs_q8k(ggml_type)) {
+    if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+      return MXA_ERR_WORKSPACE;
+    buf = mxa::act_layout((void*)workspace, n_tokens, in_features);
+    abuf = &buf;
+  } else if (x == nullptr) {
+    return MXA_ERR_UNSUPPORTED;
+  }
+  const mxa::Act act = make_act(x, abuf, in_features);
+  const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
+  mxa::launch_gemv(ggml_type, (const uint8_t*)w, rb, act, y, out_features, n_tokens,
+                   out_features, (hipStream_t)stream);
+  return check_launch();
+}
+
+int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* outs,
+                   const float* x, float* y, int n_tokens, int in_features, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr)
+    return MXA_ERR_UNSUPPORTED;
+  if (x == nullptr || y == nullptr || n_tokens <= 0) return MXA_ERR_UNSUPPORTED;
+  bool any_q8k = false;
+  long long total = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!mxa_supports(types[i], in_features) || ws[i] == nullptr || outs[i] <= 0)
+      return MXA_ERR_UNSUPPORTED;
+    any_q8k |= needs_q8k(types[i]);
+    total += outs[i];
+  }
+  hipStream_t s = (hipStream_t)stream;
+  mxa::ActBuffers buf{};
+  const mxa::ActBuffers* abuf = nullptr;
+  if (any_q8k) {
+    if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+      return MXA_ERR_WORKSPACE;
+    buf = mxa::act_layout(workspace, n_tokens, in_features);
+    abuf = &buf;
+    mxa::launch_quantize_q8k(x, buf, n_tokens, in_features, s);
+    const int st = check_launch();
+    if (st != MXA_OK) return st;
+  }
+  const mxa::Act act = make_act(x, abuf, in_features);
+  long long col = 0;
+  for (int i = 0; i < n; ++i) {
+    const long long rb = (long long)mxa_row_bytes(types[i], in_features);
+    mxa::launch_gemv(types[i], (const uint8_t*)ws[i], rb, act, y + col, total, n_tokens, outs[i],
+                     s);
+    const int st = check_launch();
+    if (st != MXA_OK) return st;
+    col += outs[i];
+  }
+  return MXA_OK;
+}
+
+int mxa_dequantize(int ggml_type, const void* blocks, long long n_blocks, float* out,
+                   void* stream) {
+  if (!known_type(ggml_type) || blocks == nullptr || out == nullptr || n_blocks <= 0)
+    return MXA_ERR_UNSUPPORTED;
+  if (mxa::launch_dequant(ggml_type, (const uint8_t*)blocks, nullptr, 0, 0, 1, n_blocks, out,
+                          (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
+int mxa_dequant_rows(int ggml_type, const void* w, long long n_src_rows, const int32_t* rows,
+                     int n_rows, int row_width, float* out, void* stream) {
+  if (!mxa_supports(ggml_type, row_width) || w == nullptr || rows == nullptr || out == nullptr ||
+      n_rows <= 0 || n_src_rows <= 0)
+    return MXA_ERR_UNSUPPORTED;
+  const int bpr = row_width / block_elems(ggml_type);
+  const long long rb = (long long)mxa_row_bytes(ggml_type, row_width);
+  if (mxa::launch_dequant(ggml_type, (const uint8_t*)w, rows, n_src_rows, rb, bpr,
+                          (long long)n_rows * bpr, out, (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
+const char* mxa_last_error(void) { return g_last_error; }
+
+}  // extern "C"

@@ -1,0 +1,51 @@
+// Host-visible kernel launchers shared between the kernel files and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mxa_device.hpp"
+
+namespace mxa {
+
+// Device layout of the Q8_K activations inside the caller's workspace (each part 256-B aligned):
+// q int8 (M, K) | d float (M, K/256) | bsums int16 (M, K/256, 16).
+struct ActBuffers {
+  int8_t* q;
+  float* d;
+  int16_t* bsums;
+};
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+inline size_t act_bytes(int m_rows, int k) {
+  const size_t nb = (size_t)k / QK;
+  return align256((size_t)m_rows * k) + align256((size_t)m_rows * nb * 4) +
+         align256((size_t)m_rows * nb * 16 * 2);
+}
+
+inline ActBuffers act_layout(void* ws, int m_rows, int k) {
+  const size_t nb = (size_t)k / QK;
+  uint8_t* p = (uint8_t*)ws;
+  ActBuffers a;
+  a.q = (int8_t*)p;
+  p += align256((size_t)m_rows * k);
+  a.d = (float*)p;
+  p += align256((size_t)m_rows * nb * 4);
+  a.bsums = (int16_t*)p;
+  return a;
+}
+
+void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
+                         hipStream_t stream);
+
+int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long n_src_rows,
+                   long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
+                   hipStream_t stream);
+
+// y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of one packed weight.
+int launch_gemv(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
+}  // namespace mxa

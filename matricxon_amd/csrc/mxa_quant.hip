@@ -1,0 +1,209 @@
+// Q8_K activation quantization and bit-exact dequantization of packed GGUF blocks.
+//
+// Compiled with -ffp-contract=off: every float multiply and subtract below rounds on its own,
+// in the order the reference's numpy dequantizers use, so results are bit-identical to them.
+#include "mxa_kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mxa {
+
+// One wave per (row m, 256-value block b); lane l owns elements 4l..4l+3. Restates
+// mx_quantize_row_q8_k (app/native/src/mx_common.c:42-69): amax over the block; an all-zero block
+// gives q = 0, bsums = 0, d = 0; otherwise iscale = 127/amax and d = amax/127 are correctly
+// rounded divisions, q = clamp(round-half-even(x * iscale), +-127) (lrintf in the default
+// rounding mode is v_rndne_f32), bsums are the sums of q over 16 values.
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
+                                                           int8_t* __restrict__ q,
+                                                           float* __restrict__ d,
+                                                           int16_t* __restrict__ bsums, int m_rows,
+                                                           int k, int nb) {
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wave >= m_rows * nb) return;
+  const int m = wave / nb, b = wave - m * nb;
+  const size_t base = (size_t)m * k + (size_t)b * QK + 4 * lane;
+  const float4 v = *(const float4*)(x + base);
+  // fmaxf ignores a NaN operand and the running maximum starts at 0, as the reference's
+  // `ax > amax ? ax : amax` from 0: a NaN input never becomes amax.
+  float amax = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+  if (amax != 0.0f) {
+    const float iscale = 127.0f / amax;
+    q0 = (int)fminf(fmaxf(rintf(v.x * iscale), -127.0f), 127.0f);
+    q1 = (int)fminf(fmaxf(rintf(v.y * iscale), -127.0f), 127.0f);
+    q2 = (int)fminf(fmaxf(rintf(v.z * iscale), -127.0f), 127.0f);
+    q3 = (int)fminf(fmaxf(rintf(v.w * iscale), -127.0f), 127.0f);
+  }
+  const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
+                          ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
+  *(uint32_t*)(q + base) = packed;
+  const int s = quad_sum(q0 + q1 + q2 + q3);
+  if ((lane & 3) == 0) bsums[((size_t)m * nb + b) * 16 + (lane >> 2)] = (int16_t)s;
+  if (lane == 0) d[(size_t)m * nb + b] = amax / 127.0f;
+}
+
+void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
+                         hipStream_t stream) {
+  const int nb = k / QK;
+  const int waves = m_rows * nb;
+  const int grid = (waves + 3) / 4;
+  hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, stream, x, a.q, a.d, a.bsums,
+                     m_rows, k, nb);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dequantization. Each thread writes 8 consecutive values of one block (Q8_0: 4 threads per
+// 32-value block; the 256-value types: 32 threads per block). Blocks come either straight from a
+// flat block array, or (row gather) from whole packed rows picked by an index list; an index
+// outside [0, n_src_rows) yields NaN values instead of a read.
+
+struct DequantSrc {
+  const uint8_t* base;
+  const int32_t* rows;  // null: flat block array
+  long long n_src_rows;
+  long long row_bytes;
+  int blocks_per_row;
+};
+
+template <int TYPE>
+struct Geo;
+template <>
+struct Geo<T_Q8_0> {
+  static constexpr int kElems = 32, kBytes = 34;
+};
+template <>
+struct Geo<T_Q4_K> {
+  static constexpr int kElems = 256, kBytes = 144;
+};
+template <>
+struct Geo<T_Q6_K> {
+  static constexpr int kElems = 256, kBytes = 210;
+};
+template <>
+struct Geo<T_IQ4_XS> {
+  static constexpr int kElems = 256, kBytes = 136;
+};
+
+// The 8 values of elements e0..e0+7 of one block at `blk` (byte-granular reads: the dequant
+// kernels are not on the matmul path and must accept any block alignment).
+template <int TYPE>
+__device__ __forceinline__ void dequant8(const uint8_t* __restrict__ blk, int e0, float* v);
+
+template <>
+__device__ __forceinline__ void dequant8<T_Q8_0>(const uint8_t* __restrict__ blk, int e0, float* v) {
+  const float d = half_to_float(blk[0] | (blk[1] << 8));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)blk[2 + e0 + i] * d;
+}
+
+template <>
+__device__ __forceinline__ void dequant8<T_Q4_K>(const uint8_t* __restrict__ blk, int e0, float* v) {
+  // value = (d * sc) * q - (dmin * m)   (app/gguf/dequant/kquants.py:57-61)
+  const float d = half_to_float(blk[0] | (blk[1] << 8));
+  const float dmin = half_to_float(blk[2] | (blk[3] << 8));
+  const int c = e0 >> 6, hi = (e0 >> 5) & 1, l0 = e0 & 31;
+  const int j = 2 * c + hi;
+  const uint8_t* s = blk + 4;
+  const int sc = j < 4 ? (s[j] & 63) : ((s[j + 4] & 15) | ((s[j - 4] >> 6) << 4));
+  const int mn = j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+  const float ds = d * (float)sc;
+  const float dm = dmin * (float)mn;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint8_t byte = blk[16 + 32 * c + l0 + i];
+    const int u = hi ? (byte >> 4) : (byte & 15);
+    v[i] = ds * (float)u - dm;
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant8<T_Q6_K>(const uint8_t* __restrict__ blk, int e0, float* v) {
+  // value = (d * sc) * (u - 32)   (app/gguf/dequant/kquants.py:144-159)
+  const float d = half_to_float(blk[208] | (blk[209] << 8));
+  const int h = e0 >> 7, g = (e0 >> 5) & 3, l0 = e0 & 31;
+  const float ds = d * (float)(int8_t)blk[192 + (e0 >> 4)];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int l = l0 + i;
+    const uint8_t qlb = blk[64 * h + ((g & 1) ? 32 : 0) + l];
+    const int nib = (g & 2) ? (qlb >> 4) : (qlb & 15);
+    const int u = nib | (((blk[128 + 32 * h + l] >> (2 * g)) & 3) << 4);
+    v[i] = ds * ((float)u - 32.0f);
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant8<T_IQ4_XS>(const uint8_t* __restrict__ blk, int e0,
+                                                   float* v) {
+  // value = (d * (ls - 32)) * grid[idx]   (app/gguf/dequant/iq_ternary.py:78-89)
+  const float d = half_to_float(blk[0] | (blk[1] << 8));
+  const int ib = e0 >> 5, hi = (e0 >> 4) & 1, l0 = e0 & 15;
+  const int sh = blk[2] | (blk[3] << 8);
+  const int ls = ((blk[4 + (ib >> 1)] >> (4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+  const float dl = d * (float)(ls - 32);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint8_t byte = blk[8 + 16 * ib + l0 + i];
+    const int idx = hi ? (byte >> 4) : (byte & 15);
+    const uint32_t g = iq4_grid_word(idx >> 2);
+    v[i] = dl * (float)(int8_t)(uint8_t)(g >> (8 * (idx & 3)));
+  }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void dequant_kernel(DequantSrc src, long long n_blocks,
+                                                      float* __restrict__ out) {
+  constexpr int kThreads = Geo<TYPE>::kElems / 8;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long g = t / kThreads;
+  if (g >= n_blocks) return;
+  const int e0 = (int)(t - g * kThreads) * 8;
+  float v[8];
+  bool ok = true;
+  const uint8_t* blk;
+  if (src.rows != nullptr) {
+    const long long r = g / src.blocks_per_row;
+    const long long bi = g - r * src.blocks_per_row;
+    const long long row = src.rows[r];
+    ok = row >= 0 && row < src.n_src_rows;
+    blk = src.base + (ok ? row : 0) * src.row_bytes + bi * Geo<TYPE>::kBytes;
+  } else {
+    blk = src.base + g * Geo<TYPE>::kBytes;
+  }
+  if (ok) {
+    dequant8<TYPE>(blk, e0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_nanf("");
+  }
+  float4* o = (float4*)(out + g * Geo<TYPE>::kElems + e0);
+  o[0] = make_float4(v[0], v[1], v[2], v[3]);
+  o[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+template <int TYPE>
+static void launch_dequant_t(const DequantSrc& src, long long n_blocks, float* out,
+                             hipStream_t stream) {
+  const long long threads = n_blocks * (Geo<TYPE>::kElems / 8);
+  const long long grid = (threads + 255) / 256;
+  hipLaunchKernelGGL(dequant_kernel<TYPE>, dim3((unsigned)grid), dim3(256), 0, stream, src,
+                     n_blocks, out);
+}
+
+int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long n_src_rows,
+                   long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
+                   hipStream_t stream) {
+  const DequantSrc src{base, rows, n_src_rows, row_bytes, blocks_per_row};
+  switch (type) {
+    case T_Q8_0: launch_dequant_t<T_Q8_0>(src, n_blocks, out, stream); return 0;
+    case T_Q4_K: launch_dequant_t<T_Q4_K>(src, n_blocks, out, stream); return 0;
+    case T_Q6_K: launch_dequant_t<T_Q6_K>(src, n_blocks, out, stream); return 0;
+    case T_IQ4_XS: launch_dequant_t<T_IQ4_XS>(src, n_blocks, out, stream); return 0;
+    default: return -1;
+  }
+}
+
+}  // namespace mxa

@@ -1,0 +1,128 @@
+"""Drop-in replacements for the reference's packed GPU modules
+(app/architectures/device_packed.py:14-89) that compute with the HIP kernels instead of
+dequantizing with torch ops and calling `F.linear`.
+
+* `DevicePackedLinear(packed, in_features, ggml_type, bias=None, dtype=torch.bfloat16)`: same
+  constructor, attributes (`out_features`, `in_features`, non-persistent `packed` buffer,
+  `bias`) and `forward(x: (..., K)) -> (..., N)` in `dtype`, as the reference's
+  (device_packed.py:22-63). The weight is never dequantized: one fused quantized matmul per call.
+* `DevicePackedEmbedding(packed, embedding_dim, ggml_type, dtype)`: a lookup dequantizes only
+  the rows it needs (device_packed.py:66-84); `as_linear` is the tied lm_head over the same
+  bytes (device_packed.py:86-89).
+* `upload_packed(raw, n_rows, device)`: (n_rows, row_bytes) uint8 device copy of packed bytes
+  (device_packed.py:14-19).
+* `HipDequantizer`: the `TorchDequantizer` interface (torch_dequant.py:310-325) on the kernels.
+
+Only Q8_0, Q4_K, Q6_K and IQ4_XS (with in_features % 256 == 0) are computed here; a loader
+asks `HipDequantizer.supports` / `HipGemm.supports` and keeps the reference module for the rest.
+"""
+
+import warnings
+
+import numpy as np
+import torch
+from torch import nn
+
+from matricxon_amd.gemm import HipGemm
+from matricxon_amd.quant_types import GEOMETRY
+
+
+def upload_packed(raw, n_rows: int, device: torch.device) -> torch.Tensor:
+    """`(n_rows, row_bytes)` uint8 copy of packed bytes on `device` (never aliases `raw`)."""
+    if isinstance(raw, torch.Tensor):
+        flat = raw.reshape(-1).to(torch.uint8)
+    else:
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            flat = torch.frombuffer(memoryview(np.ascontiguousarray(raw)).cast("B"),
+                                    dtype=torch.uint8)
+    return flat.reshape(n_rows, -1).to(device, copy=True)
+
+
+class HipDequantizer:
+    """Which quant types dequantize on the device with the HIP kernels, and their geometry."""
+
+    @staticmethod
+    def supports(ggml_type: int) -> bool:
+        return int(ggml_type) in GEOMETRY
+
+    @staticmethod
+    def geometry(ggml_type: int) -> tuple[int, int]:
+        """`(block_size, type_size)` of `ggml_type`."""
+        return GEOMETRY[int(ggml_type)]
+
+    @staticmethod
+    def dequantize(blocks: torch.Tensor, ggml_type: int) -> torch.Tensor:
+        return HipGemm.get().dequantize(blocks, ggml_type)
+
+
+class DevicePackedLinear(nn.Module):
+    """`nn.Linear` whose weight stays quantized in device memory and is multiplied in place by
+    the fused HIP kernels: x is quantized to Q8_K (IQ4_XS: kept in float32) and multiplied
+    against the packed blocks with float32 accumulation, as the reference's native C kernel does
+    (app/native/src/mx_gemm.c:219-288)."""
+
+    def __init__(
+        self,
+        packed: torch.Tensor,
+        in_features: int,
+        ggml_type: int,
+        bias: torch.Tensor | None = None,
+        dtype: torch.dtype = torch.bfloat16,
+    ) -> None:
+        super().__init__()
+        gemm = HipGemm.get()
+        if not gemm.supports(int(ggml_type), in_features):
+            raise ValueError(
+                f"no HIP kernel for GGML type {int(ggml_type)} with in_features={in_features}"
+            )
+        self.out_features = packed.shape[0]
+        self.in_features = in_features
+        self._ggml_type = int(ggml_type)
+        self._dtype = dtype
+        self._type_size = HipDequantizer.geometry(ggml_type)[1]
+        self._gemm = gemm
+        self.register_buffer("packed", packed, persistent=False)
+        self.bias = None if bias is None else nn.Parameter(bias.to(packed.device, dtype))
+
+    @property
+    def ggml_type(self) -> int:
+        return self._ggml_type
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # The reference casts x to the layer dtype before its matmul (device_packed.py:54).
+        x = x.to(self._dtype)
+        lead = x.shape[:-1]
+        y = self._gemm.matmul(self._ggml_type, self.packed, x.reshape(-1, self.in_features),
+                              self.out_features, self.in_features)
+        y = y.to(self._dtype).reshape(*lead, self.out_features)
+        return y if self.bias is None else y + self.bias
+
+
+class DevicePackedEmbedding(nn.Module):
+    """Packed token-embedding table on the device: a lookup dequantizes only the rows it needs.
+    `as_linear` is the tied lm_head over the same bytes (no second copy)."""
+
+    def __init__(
+        self, packed: torch.Tensor, embedding_dim: int, ggml_type: int, dtype: torch.dtype
+    ) -> None:
+        super().__init__()
+        gemm = HipGemm.get()
+        if not gemm.supports_dequant_rows(int(ggml_type), embedding_dim):
+            raise ValueError(f"no HIP row dequantizer for GGML type {int(ggml_type)}")
+        self.num_embeddings = packed.shape[0]
+        self.embedding_dim = embedding_dim
+        self.dtype = dtype
+        self._ggml_type = int(ggml_type)
+        self._type_size = HipDequantizer.geometry(ggml_type)[1]
+        self._gemm = gemm
+        self.register_buffer("packed", packed, persistent=False)
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        rows = self._gemm.dequant_rows(self._ggml_type, self.packed, ids.reshape(-1),
+                                       self.embedding_dim)
+        return rows.reshape(*ids.shape, self.embedding_dim).to(self.dtype)
+
+    def as_linear(self) -> DevicePackedLinear:
+        return DevicePackedLinear(self.packed, self.embedding_dim, self._ggml_type,
+                                  dtype=self.dtype)

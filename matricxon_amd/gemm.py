@@ -1,0 +1,255 @@
+"""Python face of the HIP quantized matmul (libmatricxon_amd.so): y = x @ W.T for a packed GGUF
+weight W that stays packed in device memory.
+
+`HipGemm` mirrors the reference's `NativeGemm` (app/native/gemm.py:22-212): `configure` /
+`active` / `supports` / `matmul` / `supports_dequant_rows` / `dequant_rows` / `take_stats`, with
+the same argument meaning and the same error behaviour (a nonzero library status becomes a
+`RuntimeError` naming the status and the type). The differences are the ones the device imposes:
+the packed weight is a device uint8 tensor instead of an mmap'd memoryview, x and y live on that
+device, and the call is asynchronous on torch's current HIP stream (no host sync).
+"""
+
+import logging
+
+import torch
+
+from matricxon_amd import _lib
+from matricxon_amd.quant_types import GEOMETRY
+
+logger = logging.getLogger(__name__)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device_tensor(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a tensor on a HIP device, got {getattr(t, 'device', t)}")
+
+
+class HipGemm:
+    _active: "HipGemm | None" = None
+
+    def __init__(self) -> None:
+        self._lib = _lib.load()
+        self.build_info = self._lib.mxa_build_info().decode()
+        self._calls = 0
+        self._fallback_types_logged: set[int] = set()
+
+    # -- lifecycle (NativeGemm.configure / active, app/native/gemm.py:63-84) --------------------
+    @classmethod
+    def configure(cls, backend: str = "hip") -> None:
+        """Loads the library once at startup. Unlike the reference's C build there is no fallback
+        to hide a failure behind: a missing library raises `LibraryMissingError`."""
+        cls._active = None
+        if backend != "hip":
+            return
+        cls._active = cls()
+        logger.info("HIP quantized kernels enabled: %s", cls._active.build_info)
+
+    @classmethod
+    def active(cls) -> "HipGemm | None":
+        return cls._active
+
+    @classmethod
+    def get(cls) -> "HipGemm":
+        """The configured instance, configuring on first use."""
+        if cls._active is None:
+            cls.configure("hip")
+        return cls._active
+
+    # -- capability queries ---------------------------------------------------------------------
+    def supports(self, ggml_type: int, in_features: int) -> bool:
+        supported = bool(self._lib.mxa_supports(int(ggml_type), int(in_features)))
+        if not supported and int(ggml_type) not in self._fallback_types_logged:
+            self._fallback_types_logged.add(int(ggml_type))
+            logger.info("no HIP kernel for GGML type %d (in_features=%d)", int(ggml_type),
+                        in_features)
+        return supported
+
+    def supports_dequant_rows(self, ggml_type: int, row_width: int) -> bool:
+        return bool(self._lib.mxa_supports(int(ggml_type), int(row_width)))
+
+    def row_bytes(self, ggml_type: int, in_features: int) -> int:
+        return int(self._lib.mxa_row_bytes(int(ggml_type), int(in_features)))
+
+    def workspace_bytes(self, ggml_type: int, n_tokens: int, in_features: int) -> int:
+        return int(self._lib.mxa_workspace_bytes(int(ggml_type), int(n_tokens), int(in_features)))
+
+    # -- stats (NativeGemm.record / take_stats, app/native/gemm.py:161-171) ---------------------
+    def record(self, seconds: float = 0.0) -> None:
+        self._calls += 1
+
+    def take_stats(self) -> tuple[int, float]:
+        """(calls, 0.0) since the last call: launches are asynchronous, so host time is not the
+        kernel time; per-kernel time comes from HIP events or rocprofv3."""
+        stats = (self._calls, 0.0)
+        self._calls = 0
+        return stats
+
+    # -- compute --------------------------------------------------------------------------------
+    def _check(self, status: int, what: str, ggml_type: int) -> None:
+        if status != 0:
+            detail = self._lib.mxa_last_error().decode()
+            raise RuntimeError(
+                f"{what} failed with status {status} for type {ggml_type}"
+                + (f": {detail}" if detail else "")
+            )
+
+    def _check_packed(self, ggml_type: int, packed: torch.Tensor, out_features: int,
+                      in_features: int) -> None:
+        _require_device_tensor("packed", packed)
+        expected = (out_features, self.row_bytes(ggml_type, in_features))
+        if packed.dtype != torch.uint8 or tuple(packed.shape) != expected:
+            raise ValueError(
+                f"packed must be uint8 {expected} for type {ggml_type}, got "
+                f"{packed.dtype} {tuple(packed.shape)}"
+            )
+        if not packed.is_contiguous():
+            raise ValueError("packed rows must be contiguous")
+
+    def matmul(self, ggml_type: int, packed: torch.Tensor, x: torch.Tensor, out_features: int,
+               in_features: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """`x`: (n_tokens, in_features), any float dtype, on packed's device. Returns
+        (n_tokens, out_features) float32 (written into `out` when given)."""
+        ggml_type = int(ggml_type)
+        if not self.supports(ggml_type, in_features):
+            raise RuntimeError(f"mxa_gemm failed with status -1 for type {ggml_type}")
+        self._check_packed(ggml_type, packed, out_features, in_features)
+        x32 = x.detach().reshape(-1, in_features).to(device=packed.device,
+                                                     dtype=torch.float32).contiguous()
+        n_tokens = x32.shape[0]
+        if out is None:
+            out = torch.empty((n_tokens, out_features), dtype=torch.float32, device=packed.device)
+        elif out.shape != (n_tokens, out_features) or out.dtype != torch.float32 or \
+                not out.is_contiguous() or out.device != packed.device:
+            raise ValueError("out must be a contiguous float32 (n_tokens, out_features) tensor")
+        if n_tokens == 0:
+            return out
+        ws_bytes = self.workspace_bytes(ggml_type, n_tokens, in_features)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=packed.device)
+        status = self._lib.mxa_gemm(ggml_type, packed.data_ptr(), x32.data_ptr(), out.data_ptr(),
+                                    n_tokens, out_features, in_features, ws.data_ptr(), ws_bytes,
+                                    _stream(packed.device))
+        self._check(status, "mxa_gemm", ggml_type)
+        self._calls += 1
+        return out
+
+    def matmul_q8k(self, ggml_type: int, packed: torch.Tensor, workspace: torch.Tensor,
+                   x: torch.Tensor | None, out: torch.Tensor, n_tokens: int, out_features: int,
+                   in_features: int) -> torch.Tensor:
+        """The matmul kernel alone on activations already quantized into `workspace` (by
+        `quantize_into`); `x` (float32, contiguous) is read only for IQ4_XS."""
+        ggml_type = int(ggml_type)
+        status = self._lib.mxa_gemm_q8k(ggml_type, packed.data_ptr(),
+                                        None if x is None else x.data_ptr(), out.data_ptr(),
+                                        n_tokens, out_features, in_features,
+                                        workspace.data_ptr(), workspace.numel(),
+                                        _stream(packed.device))
+        self._check(status, "mxa_gemm_q8k", ggml_type)
+        return out
+
+    def quantize_into(self, x: torch.Tensor, workspace: torch.Tensor) -> None:
+        """Q8_K activations of x (M, K) float32 contiguous into `workspace` (uint8, at least
+        `workspace_bytes(Q4_K, M, K)` bytes)."""
+        m, k = x.shape
+        status = self._lib.mxa_quantize_q8_k(x.data_ptr(), m, k, workspace.data_ptr(),
+                                             workspace.numel(), _stream(x.device))
+        self._check(status, "mxa_quantize_q8_k", 15)
+
+    def matmul_multi(self, items: list[tuple[int, torch.Tensor, int]],
+                     x: torch.Tensor) -> list[torch.Tensor]:
+        """`items`: (ggml_type, packed, out_features) per weight sharing input `x`
+        (n_tokens, in_features): one activation quantization, one float32 output per weight,
+        as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them."""
+        import ctypes
+
+        if not 1 <= len(items) <= 4:
+            raise ValueError("matmul_multi takes 1 to 4 weights")
+        in_features = x.shape[-1]
+        device = items[0][1].device
+        for t, p, o in items:
+            if not self.supports(t, in_features):
+                raise RuntimeError(f"mxa_gemm_multi failed with status -1 for type {t}")
+            self._check_packed(int(t), p, o, in_features)
+            if p.device != device:
+                raise ValueError("all packed weights must be on one device")
+        x32 = x.detach().reshape(-1, in_features).to(device=device, dtype=torch.float32).contiguous()
+        n_tokens = x32.shape[0]
+        outs = [int(o) for _, _, o in items]
+        y = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
+        ws_bytes = max(self.workspace_bytes(int(t), n_tokens, in_features) for t, _, _ in items)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+        n = len(items)
+        types = (ctypes.c_int * n)(*[int(t) for t, _, _ in items])
+        ptrs = (ctypes.c_void_p * n)(*[p.data_ptr() for _, p, _ in items])
+        couts = (ctypes.c_int * n)(*outs)
+        status = self._lib.mxa_gemm_multi(n, types, ptrs, couts, x32.data_ptr(), y.data_ptr(),
+                                          n_tokens, in_features, ws.data_ptr(), ws_bytes,
+                                          _stream(device))
+        self._check(status, "mxa_gemm_multi", int(items[0][0]))
+        self._calls += 1
+        return list(torch.split(y, outs, dim=-1))
+
+    def quantize_q8_k(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Q8_K activations of x (M, K) float32 on the device: (q int8 (M, K), d float32
+        (M, K/256), bsums int16 (M, K/256, 16))."""
+        _require_device_tensor("x", x)
+        x32 = x.detach().to(torch.float32).contiguous()
+        m, k = x32.shape
+        if k % 256 != 0 or m == 0:
+            raise ValueError("x must be (M, K) with M > 0 and K a multiple of 256")
+        nb = k // 256
+        ws_bytes = self.workspace_bytes(12, m, k)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+        status = self._lib.mxa_quantize_q8_k(x32.data_ptr(), m, k, ws.data_ptr(), ws_bytes,
+                                             _stream(x.device))
+        self._check(status, "mxa_quantize_q8_k", 15)
+
+        def al(n: int) -> int:
+            return (n + 255) & ~255
+
+        q = ws[: m * k].view(torch.int8).reshape(m, k)
+        off = al(m * k)
+        d = ws[off : off + m * nb * 4].view(torch.float32).reshape(m, nb)
+        off += al(m * nb * 4)
+        bs = ws[off : off + m * nb * 32].view(torch.int16).reshape(m, nb, 16)
+        return q, d, bs
+
+    def dequantize(self, blocks: torch.Tensor, ggml_type: int) -> torch.Tensor:
+        """`TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:323-325): blocks
+        (n_blocks, type_size) uint8 on the device -> (n_blocks * block_size,) float32,
+        bit-exact."""
+        ggml_type = int(ggml_type)
+        _require_device_tensor("blocks", blocks)
+        block, size = GEOMETRY[ggml_type]
+        blocks = blocks.reshape(-1, size).contiguous()
+        n_blocks = blocks.shape[0]
+        out = torch.empty(n_blocks * block, dtype=torch.float32, device=blocks.device)
+        if n_blocks == 0:
+            return out
+        status = self._lib.mxa_dequantize(ggml_type, blocks.data_ptr(), n_blocks, out.data_ptr(),
+                                          _stream(blocks.device))
+        self._check(status, "mxa_dequantize", ggml_type)
+        return out
+
+    def dequant_rows(self, ggml_type: int, packed: torch.Tensor, row_indices: torch.Tensor,
+                     row_width: int) -> torch.Tensor:
+        """Rows `row_indices` of the packed (n_rows, row_bytes) matrix, dequantized bit-exactly
+        to (len(row_indices), row_width) float32 (NativeGemm.dequant_rows,
+        app/native/gemm.py:111-132, on the device)."""
+        ggml_type = int(ggml_type)
+        if not self.supports_dequant_rows(ggml_type, row_width):
+            raise RuntimeError(f"mxa_dequant_rows failed with status -1 for type {ggml_type}")
+        self._check_packed(ggml_type, packed, packed.shape[0], row_width)
+        idx = row_indices.detach().reshape(-1).to(device=packed.device,
+                                                  dtype=torch.int32).contiguous()
+        out = torch.empty((idx.shape[0], row_width), dtype=torch.float32, device=packed.device)
+        if idx.shape[0] == 0:
+            return out
+        status = self._lib.mxa_dequant_rows(ggml_type, packed.data_ptr(), packed.shape[0],
+                                            idx.data_ptr(), idx.shape[0], row_width,
+                                            out.data_ptr(), _stream(packed.device))
+        self._check(status, "mxa_dequant_rows", ggml_type)
+        return out

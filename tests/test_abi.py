@@ -1,0 +1,97 @@
+"""The C ABI without a GPU: the library loads next to torch's HIP runtime, exports every symbol
+include/matricxon_amd.h declares, and its host-only queries and argument checks behave (no
+kernel is launched by anything here)."""
+
+import ctypes
+import re
+
+import pytest
+
+from tests.conftest import REPO
+
+HEADER = REPO / "include" / "matricxon_amd.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(mxa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from matricxon_amd import _lib
+
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib) -> None:
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    from matricxon_amd._lib import EXPORTS
+
+    assert sorted(EXPORTS) == names
+
+
+def test_only_torch_hip_runtime_is_mapped(lib) -> None:
+    import torch
+
+    maps = open("/proc/self/maps").read()
+    hip = set(re.findall(r"/\S*libamdhip64\S*", maps))
+    assert len(hip) == 1 and str(REPO) not in next(iter(hip))
+    assert any(p.startswith(str(REPO / "matricxon_amd")) for p in
+               re.findall(r"/\S*libmatricxon_amd\S*", maps))
+    assert torch.__file__
+
+
+def test_supports_and_sizes(lib) -> None:
+    assert lib.mxa_supports(12, 3072) == 1
+    assert lib.mxa_supports(12, 3000) == 0
+    assert lib.mxa_supports(10, 3072) == 0  # Q2_K: not one of the four types
+    assert lib.mxa_supports(8, 256) == 1 and lib.mxa_supports(8, 224) == 0
+    assert lib.mxa_row_bytes(12, 4096) == 2304
+    assert lib.mxa_row_bytes(14, 4096) == 3360
+    assert lib.mxa_row_bytes(8, 4096) == 4352
+    assert lib.mxa_row_bytes(23, 4096) == 2176
+    assert lib.mxa_row_bytes(14, 14336) == 11760
+    # Q8_K workspace: q (M*K) | d (M*nb*4) | bsums (M*nb*32), each 256-aligned
+    assert lib.mxa_workspace_bytes(12, 16, 4096) == 65536 + 1024 + 8192
+    assert lib.mxa_workspace_bytes(12, 1, 256) == 256 + 256 + 256
+    assert lib.mxa_workspace_bytes(23, 16, 4096) == 0  # IQ4_XS reads float activations
+
+
+def test_argument_errors_return_status_without_launching(lib) -> None:
+    vp = ctypes.c_void_p
+    # unsupported type / shape -> -1
+    assert lib.mxa_gemm(10, vp(1), vp(1), vp(1), 1, 4, 4096, vp(1), 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 1, 4, 4000, vp(1), 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, None, vp(1), vp(1), 1, 4, 4096, vp(1), 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 0, 4, 4096, vp(1), 1 << 20, None) == -1
+    # workspace too small -> -2
+    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 16, 4, 4096, vp(1), 1000, None) == -2
+    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 16, 4, 4096, None, 1 << 20, None) == -2
+    assert lib.mxa_quantize_q8_k(vp(1), 2, 512, vp(1), 10, None) == -2
+    assert lib.mxa_dequantize(11, vp(1), 4, vp(1), None) == -1
+    assert lib.mxa_dequant_rows(12, vp(1), 10, vp(1), 2, 300, vp(1), None) == -1
+    n = 5
+    types = (ctypes.c_int * n)(*([12] * n))
+    assert lib.mxa_gemm_multi(n, types, vp(1), vp(1), vp(1), vp(1), 1, 4096, vp(1), 1 << 20,
+                              None) == -1
+    assert lib.mxa_last_error() == b""
+
+
+def test_build_info(lib) -> None:
+    assert b"gfx950" in lib.mxa_build_info()
+
+
+def test_modules_fail_loudly_off_gpu() -> None:
+    """No CPU fallback: host tensors are rejected before anything is launched."""
+    import torch
+
+    from matricxon_amd.gemm import HipGemm
+
+    g = HipGemm.get()
+    w = torch.zeros((4, 288), dtype=torch.uint8)
+    with pytest.raises(ValueError, match="HIP device"):
+        g.matmul(12, w, torch.zeros(1, 512), 4, 512)

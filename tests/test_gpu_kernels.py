@@ -1,0 +1,194 @@
+"""GPU parity of the HIP kernels against the CPU oracle (oracle/), through the C ABI.
+
+Bars: dequantized values bit-exact; matmul outputs within rel-L2 <= 1e-4 and
+max|diff| <= 2e-3 * max|ref| of the reference C kernel semantics. K-quant and Q8_0 outputs are
+additionally checked for bit-equality with the oracle: integer block dots are exact and the
+kernels fold blocks in the oracle's order with the oracle's fused steps, so any difference there
+is a bug, not rounding. IQ4_XS (float activations, a sequential fp32 chain in the reference) is
+held to the tolerance only.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from matricxon_amd import synthetic as S
+from oracle import dequant as D
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [D.Q8_0, D.Q4_K, D.Q6_K, D.IQ4_XS]
+REL_L2 = 1e-4
+MAX_REL = 2e-3
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_within_tolerance(got: np.ndarray, want: np.ndarray) -> None:
+    got = got.astype(np.float64)
+    want = want.astype(np.float64)
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    mx = np.abs(got - want).max()
+    assert rel <= REL_L2, f"rel-L2 {rel:.3e}"
+    assert mx <= MAX_REL * np.abs(want).max(), f"max|diff| {mx:.3e} vs max|ref| {np.abs(want).max():.3e}"
+
+
+def check_gemm(gpu, oracle, ggml_type, w, x, n, k, exact=True):
+    y = host(gpu.matmul(ggml_type, dev(w), dev(x), n, k))
+    want = oracle.gemm(ggml_type, w, x, n, k)
+    assert y.shape == want.shape
+    assert_within_tolerance(y, want)
+    if exact and ggml_type != D.IQ4_XS:
+        diff = np.nonzero(bits(y) != bits(want))
+        assert diff[0].size == 0, f"{diff[0].size} outputs differ from the oracle, first at {diff[0][0]},{diff[1][0]}"
+    return y
+
+
+# ---------------------------------------------------------------------------- dequantization
+
+
+def test_half_decoding_all_patterns(gpu) -> None:
+    h = np.arange(1 << 16, dtype=np.uint16)
+    hf = h.view(np.float16)
+    h = h[~np.isinf(hf) & ~np.isnan(hf)]
+    blocks = np.zeros((h.size, 34), dtype=np.uint8)
+    blocks[:, 0:2] = h.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2] = 1
+    got = host(gpu.dequantize(dev(blocks), D.Q8_0)).reshape(-1, 32)[:, 0]
+    assert np.array_equal(bits(got), bits(h.view(np.float16).astype(np.float32)))
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+def test_dequantize_bit_exact(gpu, ggml_type) -> None:
+    w = S.packed_weight(ggml_type, 96, 2048, seed=300 + ggml_type)
+    blocks = w.reshape(-1, D.GEOMETRY[ggml_type][1])
+    # force f16-subnormal and zero scales into a few blocks
+    off = {D.Q8_0: 0, D.Q4_K: 0, D.Q6_K: 208, D.IQ4_XS: 0}[ggml_type]
+    blocks[::7, off : off + 2] = np.frombuffer(np.uint16(0x0003).tobytes(), dtype=np.uint8)
+    blocks[1::11, off : off + 2] = 0
+    got = host(gpu.dequantize(dev(blocks), ggml_type))
+    assert np.array_equal(bits(got), bits(D.dequantize(ggml_type, blocks)))
+
+
+def test_dequantize_q6_k_wide_scales(gpu) -> None:
+    w = S.packed_weight(D.Q6_K, 32, 1024, seed=5, sc_low=-128, sc_high=127)
+    got = host(gpu.dequantize(dev(w), D.Q6_K))
+    assert np.array_equal(bits(got), bits(D.dequantize(D.Q6_K, w)))
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+def test_dequant_rows_gather(gpu, ggml_type) -> None:
+    n, k = 50, 1024
+    w = S.packed_weight(ggml_type, n, k, seed=17)
+    rows = np.array([3, 0, 49, 3, 17, 60, -1], dtype=np.int32)
+    got = host(gpu.dequant_rows(ggml_type, dev(w), dev(rows), k))
+    full = D.dequantize_matrix(ggml_type, w, n, k)
+    for i, r in enumerate(rows):
+        if 0 <= r < n:
+            assert np.array_equal(bits(got[i]), bits(full[r]))
+        else:
+            assert np.all(np.isnan(got[i]))
+
+
+# ---------------------------------------------------------------------------- Q8_K quantizer
+
+
+@pytest.mark.parametrize("shape", [(1, 256), (3, 4096), (16, 14336), (5, 1024)])
+def test_quantize_q8_k_exact(gpu, oracle, shape) -> None:
+    x = S.activations(*shape, seed=shape[0] * 7)
+    x[0, :256] = 0.0  # an all-zero block
+    if shape[1] >= 512:
+        x[0, 256:512] = np.linspace(-127, 127, 256, dtype=np.float32) + 0.5  # ties
+    q, d, bs = (host(t) for t in gpu.quantize_q8_k(dev(x)))
+    wq, wd, wbs = oracle.quantize_q8_k(x)
+    assert np.array_equal(q, wq)
+    assert np.array_equal(bits(d), bits(wd))
+    assert np.array_equal(bs, wbs)
+
+
+def test_quantize_q8_k_nan_element(gpu, oracle) -> None:
+    x = S.activations(1, 256, seed=3)
+    x[0, 7] = np.nan
+    q, d, _ = (host(t) for t in gpu.quantize_q8_k(dev(x)))
+    wq, wd, _ = oracle.quantize_q8_k(x)
+    assert np.array_equal(q, wq) and np.array_equal(d, wd)
+
+
+# ---------------------------------------------------------------------------- matmul
+
+SHAPES = [(7, 512, 1), (7, 512, 3), (16, 1024, 2), (33, 1536, 5), (100, 4096, 16), (1, 256, 1),
+          (17, 768, 17), (40, 2048, 33), (129, 14336, 4)]
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("n,k,m", SHAPES)
+def test_gemm_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None:
+    w = S.packed_weight(ggml_type, n, k, seed=n * 31 + m)
+    x = S.activations(m, k, seed=m * 13 + k)
+    check_gemm(gpu, oracle, ggml_type, w, x, n, k)
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+def test_gemm_exact_on_integer_activations(gpu, ggml_type) -> None:
+    n, k = 7, 512
+    w = S.packed_weight(ggml_type, n, k, seed=ggml_type)
+    x = S.integer_activations(3, k, seed=1)
+    want = x.astype(np.float64) @ D.dequantize_matrix(ggml_type, w, n, k).astype(np.float64).T
+    got = host(gpu.matmul(ggml_type, dev(w), dev(x), n, k)).astype(np.float64)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-4 * np.abs(want).max())
+
+
+def test_gemm_q6_k_wide_scales(gpu, oracle) -> None:
+    w = S.packed_weight(D.Q6_K, 48, 2048, seed=5, sc_low=-128, sc_high=127)
+    check_gemm(gpu, oracle, D.Q6_K, w, S.activations(6, 2048, seed=6), 48, 2048)
+
+
+def test_gemm_odd_q6_k_row_alignment(gpu, oracle) -> None:
+    """K = 256 x odd: Q6_K rows of 210 x odd bytes start on 2-byte boundaries."""
+    w = S.packed_weight(D.Q6_K, 23, 768, seed=9)
+    check_gemm(gpu, oracle, D.Q6_K, w, S.activations(3, 768, seed=2), 23, 768)
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+def test_decode_rows_equal_prefill_rows(gpu, ggml_type) -> None:
+    """tests/unit/test_native_gemm.py:177-189 of the reference, on the GPU: a token's output must
+    not depend on whether it was computed alone or in a batch."""
+    n, k = 9, 768
+    w = dev(S.packed_weight(ggml_type, n, k, seed=77))
+    x = S.activations(6, k, seed=5)
+    batch = host(gpu.matmul(ggml_type, w, dev(x), n, k))
+    for t in range(6):
+        alone = host(gpu.matmul(ggml_type, w, dev(x[t : t + 1]), n, k))
+        assert np.array_equal(bits(alone[0]), bits(batch[t]))
+
+
+def test_gemm_multi_equals_separate_calls(gpu) -> None:
+    k = 1024
+    items = [(D.Q4_K, 64), (D.Q4_K, 16), (D.Q6_K, 16)]
+    ws = [dev(S.packed_weight(t, o, k, seed=i)) for i, (t, o) in enumerate(items)]
+    x = dev(S.activations(3, k, seed=11))
+    multi = gpu.matmul_multi([(t, w, o) for (t, o), w in zip(items, ws)], x)
+    for (t, o), w, y in zip(items, ws, multi):
+        assert torch.equal(y, gpu.matmul(t, w, x, o, k))
+
+
+def test_unsupported_shapes_fail_loudly(gpu) -> None:
+    w = dev(S.packed_weight(D.Q4_K, 4, 512, seed=1))
+    x = dev(S.activations(1, 512, seed=1))
+    with pytest.raises(RuntimeError, match="status -1"):
+        gpu.matmul(10, w, x, 4, 512)  # Q2_K has no kernel here
+    with pytest.raises(ValueError):
+        gpu.matmul(D.Q4_K, w, x, 5, 512)  # wrong row count
+    with pytest.raises(ValueError):
+        gpu.matmul(D.Q4_K, w.cpu(), x, 4, 512)  # host tensor
