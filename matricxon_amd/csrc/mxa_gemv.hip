@@ -3,8 +3,13 @@
 //
 // Work split. A workgroup (4 waves) owns 16 consecutive weight rows. In every wave, lane
 // (r = lane / 4, j = lane % 4) handles quarter j of row r's blocks; the 4 waves take the blocks of
-// the row in turn (block b goes to wave b % 4), so the whole workgroup streams its rows' bytes
-// with 16-byte loads, each wave issuing the loads of 4 blocks before it computes any of them.
+// the row in turn (block b goes to wave b % 4), so the workgroup streams its rows' bytes with
+// 16-byte loads. Each wave issues the loads of its next group of 4 blocks before it computes the
+// current group, and the first group's loads go out before anything else, so the weight stream
+// starts at the first instruction.
+//
+// Activations. The workgroup copies the Q8_K activations of a chunk of blocks (int8 values,
+// bsums, scales; raw floats for IQ4_XS) into LDS once; every lane then reads them from LDS.
 //
 // Numerics (the reference C kernel's, app/native/src/mx_gemm.c:241-261): K-quant and Q8_0 rows
 // use Q8_K activations and exact integer block dots (v_dot4_i32_i8, then a 4-lane integer
@@ -20,12 +25,27 @@ namespace {
 
 constexpr int kRows = 16;   // weight rows per workgroup
 constexpr int kWaves = 4;   // waves per workgroup
-constexpr int kGroup = 4;   // blocks a wave loads before computing them
+constexpr int kGroup = 4;   // blocks a wave loads ahead of computing them
+constexpr int kThreads = 64 * kWaves;
 
-template <int MAXM>
+// LDS bytes per (activation row, block) staged for a type, and the chunk of blocks staged per
+// pass so the staged activations take at most 16 KB.
+template <int TYPE>
+struct Stage {
+  static constexpr int kBytes = TYPE == T_IQ4_XS ? QK * 4 : QK + 32 + 4;
+};
+template <int TYPE, int MAXM>
 struct Chunk {
-  // blocks per LDS pass, so that the per-block partials take at most 16 KB
-  static constexpr int value = MAXM <= 4 ? 64 : (MAXM == 8 ? 32 : 16);
+  static constexpr int raw = 16384 / (MAXM * Stage<TYPE>::kBytes);
+  static constexpr int value = raw < 1 ? 1 : raw;
+};
+
+// Activations of one chunk in LDS: row m, block bb (0..kChunk) of the chunk.
+struct LdsAct {
+  const int8_t* q;       // q[(m * chunk + bb) * 256 + e]
+  const int16_t* bsums;  // bsums[(m * chunk + bb) * 16 + s]
+  const float* x;        // x[(m * chunk + bb) * 256 + e]  (IQ4_XS)
+  int chunk;
 };
 
 // 16 bytes at a 2-byte aligned address: one aligned 16-byte load (plus one dword when the
@@ -71,7 +91,7 @@ struct Ops<T_Q4_K> {
   }
   // V[m] = d * sumi - dmin * summ (mx_dot_k_ssse3.c:150-154), fused as the oracle does.
   template <int MAXM>
-  __device__ static void compute(const Lane& L, const Act& act, int b, int j, int M, float* V,
+  __device__ static void compute(const Lane& L, const LdsAct& a, int bb, int j, int M, float* V,
                                  float& D) {
     const float d = half_to_float(L.hdr.x), dmin = half_to_float(L.hdr.x >> 16);
     const K4Scales s = k4_scales(L.hdr.y, L.hdr.z, L.hdr.w);
@@ -83,7 +103,8 @@ struct Ops<T_Q4_K> {
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
       if (m < M) {
-        const int8_t* q8 = act.q + (size_t)m * act.k + (size_t)b * QK + 64 * j;
+        const int blk = m * a.chunk + bb;
+        const int8_t* q8 = a.q + blk * QK + 64 * j;
         const i32x4a4 x0 = ld16s(q8), x1 = ld16s(q8 + 16), x2 = ld16s(q8 + 32), x3 = ld16s(q8 + 48);
         const int xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         const int xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
@@ -93,8 +114,7 @@ struct Ops<T_Q4_K> {
           sl = sdot4(q[i] & 0x0F0F0F0Fu, (uint32_t)xl[i], sl);
           sh = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, (uint32_t)xh[i], sh);
         }
-        const u32x2a4 bs =
-            ld8((const uint8_t*)(act.bsums + ((size_t)m * act.nb + b) * 16 + 4 * j));
+        const u32x2a4 bs = *(const u32x2a4*)(a.bsums + blk * 16 + 4 * j);
         int sumi = sc0 * sl + sc1 * sh;
         int summ = mn0 * (lo16(bs.x) + hi16(bs.x)) + mn1 * (lo16(bs.y) + hi16(bs.y));
         sumi = quad_sum(sumi);
@@ -104,9 +124,7 @@ struct Ops<T_Q4_K> {
     }
     D = 0.0f;
   }
-  __device__ static float fold(float acc, const Act& act, int m, int b, float v, float) {
-    return fmaf(act.d[(size_t)m * act.nb + b], v, acc);
-  }
+  __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
 };
 
 // ---- Q6_K: {u8 ql[128], u8 qh[64], i8 scales[16], f16 d}, 210 bytes ------------------------
@@ -133,7 +151,7 @@ struct Ops<T_Q6_K> {
   }
   // V[m] = sumi = sum_s sc_s * sum((u - 32) * q8)  (mx_dot_k_ssse3.c:196-205)
   template <int MAXM>
-  __device__ static void compute(const Lane& L, const Act& act, int b, int j, int M, float* V,
+  __device__ static void compute(const Lane& L, const LdsAct& a, int bb, int j, int M, float* V,
                                  float& D) {
     const int h = j >> 1, jo = j & 1;
     const uint32_t Sa = h ? L.S.z : L.S.x, Sb = h ? L.S.w : L.S.y;
@@ -156,9 +174,9 @@ struct Ops<T_Q6_K> {
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
       if (m < M) {
-        const int8_t* q8 = act.q + (size_t)m * act.k + (size_t)b * QK + 128 * h + 16 * jo;
-        const u32x4a4 bw =
-            ld16((const uint8_t*)(act.bsums + ((size_t)m * act.nb + b) * 16 + 8 * h));
+        const int blk = m * a.chunk + bb;
+        const int8_t* q8 = a.q + blk * QK + 128 * h + 16 * jo;
+        const u32x4a4 bw = *(const u32x4a4*)(a.bsums + blk * 16 + 8 * h);
         const uint32_t bwv[4] = {bw.x, bw.y, bw.z, bw.w};
         int sumi = 0;
 #pragma unroll
@@ -178,8 +196,8 @@ struct Ops<T_Q6_K> {
     D = half_to_float(L.d);
   }
   // acc += (y.d * d) * sumi  (mx_dot_k_ssse3.c:206)
-  __device__ static float fold(float acc, const Act& act, int m, int b, float v, float d) {
-    return fmaf(act.d[(size_t)m * act.nb + b] * d, v, acc);
+  __device__ static float fold(float acc, float xd, float v, float d) {
+    return fmaf(xd * d, v, acc);
   }
 };
 
@@ -205,7 +223,7 @@ struct Ops<T_Q8_0> {
   }
   // V[m] = block_sum: sum over k = 0..7 of d_k * sum(qs * q8), in k order (mx_dot_q8_0.c:8-18)
   template <int MAXM>
-  __device__ static void compute(const Lane& L, const Act& act, int b, int j, int M, float* V,
+  __device__ static void compute(const Lane& L, const LdsAct& a, int bb, int j, int M, float* V,
                                  float& D) {
     const float d0 = half_to_float(L.w[0]), d1 = half_to_float(L.w[8] >> 16);
     uint32_t qa[8], qb[8];
@@ -220,7 +238,7 @@ struct Ops<T_Q8_0> {
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
       if (m < M) {
-        const int8_t* q8 = act.q + (size_t)m * act.k + (size_t)b * QK + 64 * j;
+        const int8_t* q8 = a.q + (m * a.chunk + bb) * QK + 64 * j;
         const i32x4a4 x0 = ld16s(q8), x1 = ld16s(q8 + 16), x2 = ld16s(q8 + 32), x3 = ld16s(q8 + 48);
         const int xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         const int xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
@@ -241,9 +259,7 @@ struct Ops<T_Q8_0> {
     }
     D = 0.0f;
   }
-  __device__ static float fold(float acc, const Act& act, int m, int b, float v, float) {
-    return fmaf(act.d[(size_t)m * act.nb + b], v, acc);
-  }
+  __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
 };
 
 // ---- IQ4_XS: {f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]}, 136 bytes --------------------
@@ -267,7 +283,7 @@ struct Ops<T_IQ4_XS> {
   // V[m] = sum over the block of x * (dl * grid) as dl * (sum x * grid) per sub-block
   // (mx_dot_f32.c:42-55 up to the order of the float additions).
   template <int MAXM>
-  __device__ static void compute(const Lane& L, const Act& act, int b, int j, int M, float* V,
+  __device__ static void compute(const Lane& L, const LdsAct& a, int bb, int j, int M, float* V,
                                  float& D) {
     const float d = half_to_float(L.hdr.x);
     const uint32_t sh = L.hdr.x >> 16, sl = L.hdr.y;
@@ -284,7 +300,7 @@ struct Ops<T_IQ4_XS> {
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
       if (m < M) {
-        const float* xs = act.x + (size_t)m * act.k + (size_t)b * QK + 64 * j;
+        const float* xs = a.x + (m * a.chunk + bb) * QK + 64 * j;
         float p[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -292,15 +308,15 @@ struct Ops<T_IQ4_XS> {
           for (int i = 0; i < 4; ++i) {
             const float4 xl = *(const float4*)(xs + 32 * t + 4 * i);
             const float4 xh = *(const float4*)(xs + 32 * t + 16 + 4 * i);
-            const uint32_t a = gl[4 * t + i], c = gh[4 * t + i];
-            p[t] = fmaf(xl.x, sbyte_f<0>(a), p[t]);
-            p[t] = fmaf(xl.y, sbyte_f<1>(a), p[t]);
-            p[t] = fmaf(xl.z, sbyte_f<2>(a), p[t]);
-            p[t] = fmaf(xl.w, sbyte_f<3>(a), p[t]);
-            p[t] = fmaf(xh.x, sbyte_f<0>(c), p[t]);
-            p[t] = fmaf(xh.y, sbyte_f<1>(c), p[t]);
-            p[t] = fmaf(xh.z, sbyte_f<2>(c), p[t]);
-            p[t] = fmaf(xh.w, sbyte_f<3>(c), p[t]);
+            const uint32_t g0 = gl[4 * t + i], g1 = gh[4 * t + i];
+            p[t] = fmaf(xl.x, sbyte_f<0>(g0), p[t]);
+            p[t] = fmaf(xl.y, sbyte_f<1>(g0), p[t]);
+            p[t] = fmaf(xl.z, sbyte_f<2>(g0), p[t]);
+            p[t] = fmaf(xl.w, sbyte_f<3>(g0), p[t]);
+            p[t] = fmaf(xh.x, sbyte_f<0>(g1), p[t]);
+            p[t] = fmaf(xh.y, sbyte_f<1>(g1), p[t]);
+            p[t] = fmaf(xh.z, sbyte_f<2>(g1), p[t]);
+            p[t] = fmaf(xh.w, sbyte_f<3>(g1), p[t]);
           }
         }
         V[m] = quad_sum(fmaf(dl1, p[1], dl0 * p[0]));
@@ -308,58 +324,138 @@ struct Ops<T_IQ4_XS> {
     }
     D = 0.0f;
   }
-  __device__ static float fold(float acc, const Act&, int, int, float v, float) { return acc + v; }
+  __device__ static float fold(float acc, float, float v, float) { return acc + v; }
 };
 
-template <int TYPE, int MAXM>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w,
+template <int TYPE, int MAXM, bool PIPE>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* w,
                                                    long long row_bytes, Act act,
                                                    float* __restrict__ y, long long ldy, int M,
                                                    int N) {
   using O = Ops<TYPE>;
-  constexpr int kChunk = Chunk<MAXM>::value;
+  constexpr int kChunk = Chunk<TYPE, MAXM>::value;
+  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
+  constexpr int kQBytes = kChunk * (kFloatAct ? QK * 4 : QK);  // staged bytes per row m
+  constexpr int kQLoads = (kQBytes + kThreads * 16 - 1) / (kThreads * 16);
+  constexpr int kBLoads = kFloatAct ? 0 : (kChunk * 32 + kThreads * 16 - 1) / (kThreads * 16);
+  __shared__ __align__(16) int8_t Xq[kFloatAct ? 16 : MAXM * kChunk * QK];
+  __shared__ __align__(16) int16_t Xb[kFloatAct ? 8 : MAXM * kChunk * 16];
+  __shared__ float Xd[kFloatAct ? 1 : MAXM * kChunk];
+  __shared__ __align__(16) float Xf[kFloatAct ? MAXM * kChunk * QK : 4];
   __shared__ float Vs[MAXM][kChunk][kRows];
   __shared__ float Ds[O::kHasD ? kChunk : 1][kRows];
 
   const int n0 = xcd_tile(blockIdx.x, gridDim.x) * kRows;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int r = lane >> 2, j = lane & 3;
   const int n = min(n0 + r, N - 1);  // rows past N recompute row N-1; never stored
   const uint8_t* row = w + (size_t)n * row_bytes;
   const int nb = act.nb;
-  const int fr = threadIdx.x & (kRows - 1), fm = threadIdx.x >> 4;
+  const int fr = tid & (kRows - 1), fm = tid >> 4;
+  const LdsAct la{Xq, Xb, Xf, kChunk};
   float acc = 0.0f;
 
   for (int c0 = 0; c0 < nb; c0 += kChunk) {
     const int cn = min(kChunk, nb - c0);
-    for (int g0 = wave; g0 < cn; g0 += kWaves * kGroup) {
-      typename O::Lane L[kGroup];
+    // this wave's blocks of the chunk are bb = wave + kWaves * i, i < mine
+    const int mine = cn > wave ? (cn - wave + kWaves - 1) / kWaves : 0;
+    // Every load below is unconditional, at an address clamped into its buffer (a clamped
+    // activation piece is stored twice to the same place; a clamped weight block is loaded and
+    // not used), so the compiler issues them back to back without branches.
+
+    // 1. this chunk's activations (all M rows) into registers, before the weight loads, so
+    //    that waiting for them (loads retire in order) never waits for HBM.
+    const int q_per_m = cn * (kFloatAct ? QK * 4 : QK);
+    const uint8_t* q_src = kFloatAct ? (const uint8_t*)(act.x + (size_t)c0 * QK)
+                                     : (const uint8_t*)(act.q + (size_t)c0 * QK);
+    const size_t q_row = (size_t)act.k * (kFloatAct ? 4 : 1);
+    u32x4a4 sq[MAXM][kQLoads];
+    u32x4a4 sb[MAXM][kBLoads > 0 ? kBLoads : 1];
+    float sd[MAXM];
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        const int bb = g0 + u * kWaves;
-        if (bb < cn) L[u] = O::load(row, c0 + bb, j);
+    for (int m = 0; m < MAXM; ++m) {
+      const int mc = min(m, M - 1);
+#pragma unroll
+      for (int t = 0; t < kQLoads; ++t)
+        sq[m][t] = ld16(q_src + mc * q_row + min(tid * 16 + t * kThreads * 16, q_per_m - 16));
+      if constexpr (!kFloatAct) {
+#pragma unroll
+        for (int t = 0; t < kBLoads; ++t)
+          sb[m][t] = ld16((const uint8_t*)act.bsums + ((size_t)mc * nb + c0) * 32 +
+                          min(tid * 16 + t * kThreads * 16, cn * 32 - 16));
+        sd[m] = act.d[(size_t)mc * nb + c0 + min(tid, cn - 1)];
+      }
+    }
+
+    // 2. the weight loads of this wave's first group of blocks
+    typename O::Lane cur[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u)
+      cur[u] = O::load(row, c0 + min(wave + kWaves * u, cn - 1), j);
+
+    // keep every load above issued before the first wait below (the scheduler would otherwise
+    // interleave the LDS stores, and their waits, with the weight loads)
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. activations into LDS, laid out [m][block of the chunk][...]
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int mc = min(m, M - 1);
+#pragma unroll
+      for (int t = 0; t < kQLoads; ++t) {
+        const int o = min(tid * 16 + t * kThreads * 16, q_per_m - 16);
+        uint8_t* dst = kFloatAct ? (uint8_t*)Xf + mc * kQBytes + o : (uint8_t*)Xq + mc * kQBytes + o;
+        *(u32x4a4*)dst = sq[m][t];
+      }
+      if constexpr (!kFloatAct) {
+#pragma unroll
+        for (int t = 0; t < kBLoads; ++t)
+          *(u32x4a4*)((uint8_t*)Xb + mc * kChunk * 32 +
+                      min(tid * 16 + t * kThreads * 16, cn * 32 - 16)) = sb[m][t];
+        Xd[mc * kChunk + min(tid, cn - 1)] = sd[m];
+      }
+    }
+    __syncthreads();
+
+    // 4. compute, one group of kGroup blocks at a time; the first group runs on every path (so
+    //    its loads stay above the barrier), and with PIPE the next group's weight loads are in
+    //    flight while a group is computed
+    for (int g = 0;; g += kGroup) {
+      typename O::Lane nxt[PIPE ? kGroup : 1];
+      if constexpr (PIPE) {
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u)
+          nxt[u] = O::load(row, c0 + min(wave + kWaves * (g + kGroup + u), cn - 1), j);
       }
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
-        const int bb = g0 + u * kWaves;
-        if (bb < cn) {
-          float V[MAXM];
-          float D;
-          O::template compute<MAXM>(L[u], act, c0 + bb, j, M, V, D);
-          if (j == 0) {
+        // computed on every path (on a clamped, valid block past `mine`) so that the compiler
+        // keeps the weight loads where they are issued; only the store is conditional
+        const int bb = wave + kWaves * (g + u);
+        const int bbc = min(bb, cn - 1);
+        float V[MAXM];
+        float D;
+        O::template compute<MAXM>(cur[u], la, bbc, j, M, V, D);
+        if (j == 0 && g + u < mine) {
 #pragma unroll
-            for (int m = 0; m < MAXM; ++m)
-              if (m < M) Vs[m][bb][r] = V[m];
-            if (O::kHasD) Ds[O::kHasD ? bb : 0][r] = D;
-          }
+          for (int m = 0; m < MAXM; ++m)
+            if (m < M) Vs[m][bb][r] = V[m];
+          if (O::kHasD) Ds[O::kHasD ? bb : 0][r] = D;
         }
+      }
+      if (!PIPE || g + kGroup >= mine) break;  // without PIPE a wave owns one group (launch_m)
+      if constexpr (PIPE) {
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) cur[u] = nxt[u];
       }
     }
     __syncthreads();
     if (fm < M) {
 #pragma unroll 8
       for (int bb = 0; bb < cn; ++bb)
-        acc = O::fold(acc, act, fm, c0 + bb, Vs[fm][bb][fr], Ds[O::kHasD ? bb : 0][fr]);
+        acc = O::fold(acc, kFloatAct ? 0.0f : Xd[kFloatAct ? 0 : fm * kChunk + bb], Vs[fm][bb][fr],
+                      Ds[O::kHasD ? bb : 0][fr]);
     }
     __syncthreads();
   }
@@ -370,8 +466,14 @@ template <int TYPE, int MAXM>
 void launch_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
               int M, int N, hipStream_t stream) {
   const int tiles = (N + kRows - 1) / kRows;
-  hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM>), dim3(tiles), dim3(256), 0, stream, w, row_bytes,
-                     act, y, ldy, M, N);
+  // Without the prefetch buffer a wave must own at most kGroup blocks of every chunk.
+  const int chunk = min(act.nb, Chunk<TYPE, MAXM>::value);
+  if (chunk <= kWaves * kGroup)
+    hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM, false>), dim3(tiles), dim3(kThreads), 0, stream,
+                       w, row_bytes, act, y, ldy, M, N);
+  else
+    hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM, true>), dim3(tiles), dim3(kThreads), 0, stream,
+                       w, row_bytes, act, y, ldy, M, N);
 }
 
 template <int TYPE>

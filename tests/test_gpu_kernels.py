@@ -28,7 +28,7 @@ def dev(a: np.ndarray) -> torch.Tensor:
 
 def host(t: torch.Tensor) -> np.ndarray:
     torch.cuda.synchronize()
-    return t.cpu().numpy()
+    return t.detach().cpu().numpy()
 
 
 def bits(a: np.ndarray) -> np.ndarray:
