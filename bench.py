@@ -4,8 +4,9 @@ Q4_K GEMV 14336x4096 at M=1 (the `value`) and M=16, on seeded synthetic packed w
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
-A step is one projection call: Q8_K quantization of the activations, then the fused
-dequantize-and-multiply kernel over the packed weight. The timed region replays a HIP graph
+A step is one projection call through the public entry point `mxa_gemm`: Q8_K quantization of
+the activations and the fused dequantize-and-multiply over the packed weight (for M <= 4 both in
+one kernel; for M = 16 a quantization kernel, then the matmul kernel). The timed region replays a HIP graph
 of exactly K captured steps (so Python launch overhead is not measured), bracketed by
 synchronizations. Each step reads a different copy of the weight (the copies together exceed
 1 GiB), so the 256 MB Infinity Cache cannot serve repeats: every weight byte comes from HBM.
@@ -138,23 +139,33 @@ def main() -> int:
         y = torch.empty((m, N), dtype=torch.float32, device=dev)
         ref_y = gemm.matmul(Q4_K, w0, x, N, K).clone()
 
+        fused = ws.numel() == 0  # up to 4 rows the matmul kernel quantizes x itself
+
         def step(i: int) -> None:
-            gemm.quantize_into(x, ws)
-            gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
+            """One projection call through the public entry point (mxa_gemm)."""
+            gemm.matmul(Q4_K, weights[i % copies], x, N, K, out=y)
+
+        def kernel(i: int) -> None:
+            """The dominant kernel alone: the matmul kernel on quantized activations."""
+            if fused:
+                gemm.matmul(Q4_K, weights[i % copies], x, N, K, out=y)
+            else:
+                gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
 
         # -- per-launch kernel timing (roofline) -----------------------------------------
-        gemm.quantize_into(x, ws)
+        if not fused:
+            gemm.quantize_into(x, ws)
         n_ev = max(args.steps, 50)
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
         ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
         for i in range(args.warmup):
-            gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
+            kernel(i)
         torch.cuda.synchronize()
         if hasattr(torch.cuda, "_sleep"):
             torch.cuda._sleep(20_000_000)  # keep the GPU busy while the launches are queued
         for i in range(n_ev):
             starts[i].record()
-            gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
+            kernel(i)
             ends[i].record()
         torch.cuda.synchronize()
         kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
@@ -259,7 +270,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(r1["kernel_alg_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "gemv_kernel<Q4_K, M=1>",
+            "kernel": "gemv_kernel<Q4_K, M=1, fused Q8_K>",
             "kernel_us": round(r1["kernel_us"], 3),
             "bytes_per_launch": algorithmic_bytes(1),
         },

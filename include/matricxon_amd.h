@@ -46,13 +46,15 @@ int mxa_supports(int ggml_type, int in_features);
 /* Bytes of one packed row of `in_features` values (0 when unsupported). Host-only. */
 size_t mxa_row_bytes(int ggml_type, int in_features);
 
-/* Workspace bytes mxa_gemm / mxa_gemm_multi need for n_tokens rows of in_features (the Q8_K
- * activation blocks; 0 for IQ4_XS, which reads the float activations directly). Host-only. */
+/* Workspace bytes mxa_gemm / mxa_gemm_multi need for n_tokens rows of in_features: the Q8_K
+ * activation blocks, or 0 when none are needed (IQ4_XS reads the float activations; up to 4
+ * rows, the matmul kernel quantizes them in on-chip memory itself). Host-only. */
 size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features);
 
 /* y (n_tokens, out_features) fp32 = x (n_tokens, in_features) fp32 @ W.T, W the packed rows
- * (out_features, row_bytes) in GGUF order. The activations are quantized to Q8_K into
- * `workspace` first (except for IQ4_XS), exactly as the reference C kernel does.
+ * (out_features, row_bytes) in GGUF order. The activations are quantized to Q8_K exactly as the
+ * reference C kernel does (except IQ4_XS, which uses them as floats): into `workspace` first,
+ * or, for n_tokens <= 4, inside the matmul kernel (one launch, no workspace).
  * Replaces `mx_gemm` (app/native/src/mx_gemm.c:219-288) and, on the GPU, the dequantize +
  * F.linear of `DevicePackedLinear.forward` (app/architectures/device_packed.py:53-63). */
 int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_tokens,

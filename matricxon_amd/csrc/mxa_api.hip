@@ -35,6 +35,9 @@ int block_bytes(int t) {
 
 bool needs_q8k(int t) { return t != MXA_TYPE_IQ4_XS; }
 
+// Up to this many activation rows the matmul kernel quantizes x itself (no workspace).
+bool fused_quant(int n_tokens) { return n_tokens <= mxa::kFusedQuantMaxRows; }
+
 mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
   mxa::Act act;
   act.q = a ? a->q : nullptr;
@@ -66,7 +69,8 @@ size_t mxa_row_bytes(int ggml_type, int in_features) {
 
 size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features) {
   if (!mxa_supports(ggml_type, in_features) || n_tokens <= 0) return 0;
-  return needs_q8k(ggml_type) ? mxa::act_bytes(n_tokens, in_features) : 0;
+  return needs_q8k(ggml_type) && !fused_quant(n_tokens) ? mxa::act_bytes(n_tokens, in_features)
+                                                        : 0;
 }
 
 int mxa_quantize_q8_k(const float* x, int n_tokens, int in_features, void* workspace,
@@ -130,7 +134,7 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
   hipStream_t s = (hipStream_t)stream;
   mxa::ActBuffers buf{};
   const mxa::ActBuffers* abuf = nullptr;
-  if (any_q8k) {
+  if (any_q8k && !fused_quant(n_tokens)) {
     if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
       return MXA_ERR_WORKSPACE;
     buf = mxa::act_layout(workspace, n_tokens, in_features);

@@ -16,6 +16,8 @@
 // reduction); IQ4_XS uses the raw float activations. The per-block float results go to LDS and
 // one thread per (row, activation row) folds them over the blocks in order 0..nb-1 with the same
 // fused multiply-adds as the CPU oracle, so K-quant and Q8_0 outputs equal it bit for bit.
+#include <type_traits>
+
 #include "mxa_kernels.hpp"
 
 #pragma clang fp contract(off)
@@ -64,6 +66,20 @@ __device__ __forceinline__ u32x4a4 ld16_a2(const uint8_t* p) {
   r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
   r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
   return r;
+}
+
+// Maximum over each row of 16 lanes: quad butterflies, then the half-row and row mirrors.
+__device__ __forceinline__ float row16_max(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                 decltype(ctrl)::value, 0xF, 0xF,
+                                                                 false));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+  return v;
 }
 
 __device__ __forceinline__ int lo16(uint32_t w) { return (int16_t)(w & 0xFFFFu); }
@@ -327,13 +343,17 @@ struct Ops<T_IQ4_XS> {
   __device__ static float fold(float acc, float, float v, float) { return acc + v; }
 };
 
-template <int TYPE, int MAXM, bool PIPE>
+// FUSEQ: the workgroup quantizes the float activations to Q8_K itself (16 lanes per 256-value
+// block, the arithmetic of quantize_q8k_kernel), instead of reading them from the workspace; for
+// M <= 4 this saves a kernel launch per projection.
+template <int TYPE, int MAXM, bool PIPE, bool FUSEQ>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* w,
                                                    long long row_bytes, Act act,
                                                    float* __restrict__ y, long long ldy, int M,
                                                    int N) {
   using O = Ops<TYPE>;
-  constexpr int kChunk = Chunk<TYPE, MAXM>::value;
+  static_assert(!FUSEQ || (TYPE != T_IQ4_XS && MAXM <= 4), "fused quantization: M <= 4");
+  constexpr int kChunk = FUSEQ ? 16 / MAXM : Chunk<TYPE, MAXM>::value;
   constexpr bool kFloatAct = TYPE == T_IQ4_XS;
   constexpr int kQBytes = kChunk * (kFloatAct ? QK * 4 : QK);  // staged bytes per row m
   constexpr int kQLoads = (kQBytes + kThreads * 16 - 1) / (kThreads * 16);
@@ -373,8 +393,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* w,
     u32x4a4 sq[MAXM][kQLoads];
     u32x4a4 sb[MAXM][kBLoads > 0 ? kBLoads : 1];
     float sd[MAXM];
+    // FUSEQ: lanes 16g..16g+15 own row m = g / kChunk, block bb = g % kChunk; lane part p of the
+    // group holds elements 16p..16p+15 of that block
+    const int fq_g = tid >> 4, fq_p = tid & 15;
+    const int fq_m = min(fq_g / kChunk, M - 1), fq_bb = min(fq_g % kChunk, cn - 1);
+    float4 fx[FUSEQ ? 4 : 1];
+    if constexpr (FUSEQ) {
+      const float* src = act.x + (size_t)fq_m * act.k + (size_t)(c0 + fq_bb) * QK + 16 * fq_p;
 #pragma unroll
-    for (int m = 0; m < MAXM; ++m) {
+      for (int i = 0; i < 4; ++i) fx[i] = *(const float4*)(src + 4 * i);
+    }
+#pragma unroll
+    for (int m = 0; m < (FUSEQ ? 0 : MAXM); ++m) {
       const int mc = min(m, M - 1);
 #pragma unroll
       for (int t = 0; t < kQLoads; ++t)
@@ -399,8 +429,36 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* w,
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. activations into LDS, laid out [m][block of the chunk][...]
+    if constexpr (FUSEQ) {
+      // Q8_K of this lane's 16 values (app/native/src/mx_common.c:42-69, as quantize_q8k_kernel)
+      const float v[16] = {fx[0].x, fx[0].y, fx[0].z, fx[0].w, fx[1].x, fx[1].y, fx[1].z, fx[1].w,
+                           fx[2].x, fx[2].y, fx[2].z, fx[2].w, fx[3].x, fx[3].y, fx[3].z, fx[3].w};
+      float amax = 0.0f;
 #pragma unroll
-    for (int m = 0; m < MAXM; ++m) {
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      amax = row16_max(amax);
+      int q[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q[i] = 0;
+      if (amax != 0.0f) {
+        const float iscale = 127.0f / amax;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = (int)fminf(fmaxf(rintf(v[i] * iscale), -127.0f), 127.0f);
+      }
+      int bsum = 0;
+      u32x4a4 packed;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        packed[i] = (uint32_t)(q[4 * i] & 0xFF) | ((uint32_t)(q[4 * i + 1] & 0xFF) << 8) |
+                    ((uint32_t)(q[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * i + 3] & 0xFF) << 24);
+        bsum += q[4 * i] + q[4 * i + 1] + q[4 * i + 2] + q[4 * i + 3];
+      }
+      *(u32x4a4*)(Xq + fq_m * kQBytes + fq_bb * QK + 16 * fq_p) = packed;
+      Xb[(fq_m * kChunk + fq_bb) * 16 + fq_p] = (int16_t)bsum;
+      if (fq_p == 0) Xd[fq_m * kChunk + fq_bb] = amax / 127.0f;
+    }
+#pragma unroll
+    for (int m = 0; m < (FUSEQ ? 0 : MAXM); ++m) {
       const int mc = min(m, M - 1);
 #pragma unroll
       for (int t = 0; t < kQLoads; ++t) {
@@ -462,23 +520,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* w,
   if (fm < M && n0 + fr < N) y[(size_t)fm * ldy + n0 + fr] = acc;
 }
 
-template <int TYPE, int MAXM>
+template <int TYPE, int MAXM, bool FUSEQ>
 void launch_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
               int M, int N, hipStream_t stream) {
   const int tiles = (N + kRows - 1) / kRows;
   // Without the prefetch buffer a wave must own at most kGroup blocks of every chunk.
-  const int chunk = min(act.nb, Chunk<TYPE, MAXM>::value);
+  const int chunk = min(act.nb, FUSEQ ? 16 / MAXM : Chunk<TYPE, MAXM>::value);
   if (chunk <= kWaves * kGroup)
-    hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM, false>), dim3(tiles), dim3(kThreads), 0, stream,
-                       w, row_bytes, act, y, ldy, M, N);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM, false, FUSEQ>), dim3(tiles), dim3(kThreads), 0,
+                       stream, w, row_bytes, act, y, ldy, M, N);
   else
-    hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM, true>), dim3(tiles), dim3(kThreads), 0, stream,
-                       w, row_bytes, act, y, ldy, M, N);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, MAXM, true, FUSEQ>), dim3(tiles), dim3(kThreads), 0,
+                       stream, w, row_bytes, act, y, ldy, M, N);
+}
+
+template <int TYPE, int MAXM>
+void launch_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+              int M, int N, hipStream_t stream) {
+  launch_m<TYPE, MAXM, false>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
 template <int TYPE>
 void launch_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                  int M, int N, hipStream_t stream) {
+  if constexpr (TYPE != T_IQ4_XS) {
+    if (act.q == nullptr) {
+      // fused quantization (the caller checked M <= 4 and passed the float activations)
+      if (M == 1) launch_m<TYPE, 1, true>(w, row_bytes, act, y, ldy, M, N, stream);
+      else if (M == 2) launch_m<TYPE, 2, true>(w, row_bytes, act, y, ldy, M, N, stream);
+      else launch_m<TYPE, 4, true>(w, row_bytes, act, y, ldy, M, N, stream);
+      return;
+    }
+  }
   for (int m0 = 0; m0 < M; m0 += 16) {
     const int mm = min(16, M - m0);
     Act a = act;

@@ -44,7 +44,12 @@ int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long
                    long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
                    hipStream_t stream);
 
-// y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of one packed weight.
+// Activation rows up to which the matmul kernels quantize x themselves (no workspace).
+constexpr int kFusedQuantMaxRows = 4;
+
+// y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of one packed weight. A K-quant or
+// Q8_0 weight with act.q == nullptr (only for m_rows <= kFusedQuantMaxRows) quantizes act.x in
+// the kernel.
 int launch_gemv(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
 

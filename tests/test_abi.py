@@ -57,7 +57,8 @@ def test_supports_and_sizes(lib) -> None:
     assert lib.mxa_row_bytes(14, 14336) == 11760
     # Q8_K workspace: q (M*K) | d (M*nb*4) | bsums (M*nb*32), each 256-aligned
     assert lib.mxa_workspace_bytes(12, 16, 4096) == 65536 + 1024 + 8192
-    assert lib.mxa_workspace_bytes(12, 1, 256) == 256 + 256 + 256
+    assert lib.mxa_workspace_bytes(12, 5, 256) == 1280 + 256 + 256
+    assert lib.mxa_workspace_bytes(12, 4, 4096) == 0  # quantized inside the matmul kernel
     assert lib.mxa_workspace_bytes(23, 16, 4096) == 0  # IQ4_XS reads float activations
 
 
@@ -71,6 +72,7 @@ def test_argument_errors_return_status_without_launching(lib) -> None:
     # workspace too small -> -2
     assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 16, 4, 4096, vp(1), 1000, None) == -2
     assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 16, 4, 4096, None, 1 << 20, None) == -2
+    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 5, 4, 4096, vp(1), 1000, None) == -2
     assert lib.mxa_quantize_q8_k(vp(1), 2, 512, vp(1), 10, None) == -2
     assert lib.mxa_dequantize(11, vp(1), 4, vp(1), None) == -1
     assert lib.mxa_dequant_rows(12, vp(1), 10, vp(1), 2, 300, vp(1), None) == -1
