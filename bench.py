@@ -118,7 +118,7 @@ def main() -> int:
     import torch
 
     from matricxon_amd import synthetic as S
-    from matricxon_amd.gemm import HipGemm
+    from matricxon_amd.gemm import HipGemm, q8k_bytes
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -135,11 +135,11 @@ def main() -> int:
     results = {}
     for m in (1, 16):
         x = torch.from_numpy(S.activations(m, K, seed=SEED_X + m)).to(dev)
-        ws = torch.empty(gemm.workspace_bytes(Q4_K, m, K), dtype=torch.uint8, device=dev)
+        ws = torch.empty(q8k_bytes(m, K), dtype=torch.uint8, device=dev)
         y = torch.empty((m, N), dtype=torch.float32, device=dev)
         ref_y = gemm.matmul(Q4_K, w0, x, N, K).clone()
 
-        fused = ws.numel() == 0  # up to 4 rows the matmul kernel quantizes x itself
+        fused = gemm.workspace_bytes(Q4_K, m, K) == 0  # the matmul kernel quantizes x itself
 
         def step(i: int) -> None:
             """One projection call through the public entry point (mxa_gemm)."""

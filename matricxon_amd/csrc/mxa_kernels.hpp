@@ -53,4 +53,15 @@ constexpr int kFusedQuantMaxRows = 4;
 int launch_gemv(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Matrix-core kernel for batched decode: Q4_K, 1 <= m_rows <= 16, on Q8_K activations already
+// in the workspace.
+bool mfma_decode_supported(int type, int m_rows);
+int launch_mfma_decode(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                       long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
+// The matmul for any m_rows: picks the kernel (matrix-core decode, or the dot4 GEMV in passes of
+// up to 16 rows).
+int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 }  // namespace mxa

@@ -23,6 +23,17 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _al256(n: int) -> int:
+    return (n + 255) & ~255
+
+
+def q8k_bytes(m: int, k: int) -> int:
+    """Bytes of the Q8_K activation layout mxa_quantize_q8_k writes for (m, k) floats:
+    q int8 (m, k) | d float32 (m, k/256) | bsums int16 (m, k/256, 16), each 256-byte aligned."""
+    nb = k // 256
+    return _al256(m * k) + _al256(m * nb * 4) + _al256(m * nb * 32)
+
+
 def _require_device_tensor(name: str, t: torch.Tensor) -> None:
     if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
         raise ValueError(f"{name} must be a tensor on a HIP device, got {getattr(t, 'device', t)}")
@@ -152,7 +163,7 @@ class HipGemm:
 
     def quantize_into(self, x: torch.Tensor, workspace: torch.Tensor) -> None:
         """Q8_K activations of x (M, K) float32 contiguous into `workspace` (uint8, at least
-        `workspace_bytes(Q4_K, M, K)` bytes)."""
+        `q8k_bytes(M, K)` bytes)."""
         m, k = x.shape
         status = self._lib.mxa_quantize_q8_k(x.data_ptr(), m, k, workspace.data_ptr(),
                                              workspace.numel(), _stream(x.device))
@@ -201,19 +212,16 @@ class HipGemm:
         if k % 256 != 0 or m == 0:
             raise ValueError("x must be (M, K) with M > 0 and K a multiple of 256")
         nb = k // 256
-        ws_bytes = self.workspace_bytes(12, m, k)
+        ws_bytes = q8k_bytes(m, k)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
         status = self._lib.mxa_quantize_q8_k(x32.data_ptr(), m, k, ws.data_ptr(), ws_bytes,
                                              _stream(x.device))
         self._check(status, "mxa_quantize_q8_k", 15)
 
-        def al(n: int) -> int:
-            return (n + 255) & ~255
-
         q = ws[: m * k].view(torch.int8).reshape(m, k)
-        off = al(m * k)
+        off = _al256(m * k)
         d = ws[off : off + m * nb * 4].view(torch.float32).reshape(m, nb)
-        off += al(m * nb * 4)
+        off += _al256(m * nb * 4)
         bs = ws[off : off + m * nb * 32].view(torch.int16).reshape(m, nb, 16)
         return q, d, bs
 
