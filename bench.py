@@ -11,9 +11,12 @@ of exactly K captured steps (so Python launch overhead is not measured), bracket
 synchronizations. Each step reads a different copy of the weight (the copies together exceed
 1 GiB), so the 256 MB Infinity Cache cannot serve repeats: every weight byte comes from HBM.
 
-roofline: the matmul kernel alone, timed with a pair of HIP events around every launch on the
-launch stream (the launches are queued behind a short spin kernel so the GPU never waits for the
-host); achieved = algorithmic bytes per launch / mean launch time.
+roofline: the dominant kernel is the M=1 matmul kernel (it also quantizes x): every M=1 step is
+exactly one launch of it, so its average launch duration is the time between two HIP events
+recorded on the replay stream around the timed graph replay, divided by K (gaps between
+launches included); achieved = algorithmic bytes per launch / that duration. For M=16 the
+matmul kernel alone (activations quantized beforehand) is timed the same way in a graph of its
+own.
 
 cpu_baseline: the reference's own C kernel `mx_gemm` (built from its sources into
 oracle/_ref/libmx_ref.so) on the host cores, M=1, same weight, ~10 s of repeated calls.
@@ -146,74 +149,78 @@ def main() -> int:
             gemm.matmul(Q4_K, weights[i % copies], x, N, K, out=y)
 
         def kernel(i: int) -> None:
-            """The dominant kernel alone: the matmul kernel on quantized activations."""
+            """The matmul kernel alone (for M <= 4 the same call as `step`)."""
             if fused:
                 gemm.matmul(Q4_K, weights[i % copies], x, N, K, out=y)
             else:
                 gemm.matmul_q8k(Q4_K, weights[i % copies], ws, None, y, m, N, K)
 
-        # -- per-launch kernel timing (roofline) -----------------------------------------
         if not fused:
             gemm.quantize_into(x, ws)
-        n_ev = max(args.steps, 50)
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-        for i in range(args.warmup):
-            kernel(i)
-        torch.cuda.synchronize()
-        if hasattr(torch.cuda, "_sleep"):
-            torch.cuda._sleep(20_000_000)  # keep the GPU busy while the launches are queued
-        for i in range(n_ev):
-            starts[i].record()
-            kernel(i)
-            ends[i].record()
-        torch.cuda.synchronize()
-        kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-        kern_mean = statistics.fmean(kern_ms)
-        log(f"M={m}: kernel mean {kern_mean * 1e3:.2f} us, median "
-            f"{statistics.median(kern_ms) * 1e3:.2f} us over {n_ev} launches")
-        if not torch.equal(y, ref_y):
-            raise SystemExit(f"M={m}: kernel-only result differs from the full call")
-        if args.kernel_only:
-            results[m] = {"kernel_us": kern_mean * 1e3}
+        if args.kernel_only:  # eager launches only, for counter-collection runs
+            for i in range(args.steps):
+                kernel(i)
+            torch.cuda.synchronize()
+            if not torch.equal(y, ref_y):
+                raise SystemExit(f"M={m}: kernel-only result differs from the full call")
+            results[m] = {"launches": args.steps}
             continue
 
+        def capture(fn):
+            for i in range(args.warmup):
+                fn(i)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    for i in range(args.steps):
+                        fn(i)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            graph.replay()  # untimed replay, checked against the eager result
+            torch.cuda.synchronize()
+            if not torch.equal(y, ref_y):
+                raise SystemExit(f"M={m}: graph replay result differs from the eager call")
+            return graph
+
+        def timed(graph):
+            """Host seconds and HIP-event milliseconds of one replay of K captured steps."""
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t0
+            if not torch.equal(y, ref_y):
+                raise SystemExit(f"M={m}: timed replay result differs from the eager call")
+            return elapsed, e0.elapsed_time(e1)
+
         # -- timed region: a graph of exactly K steps ------------------------------------
-        for i in range(args.warmup):
-            step(i)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(graph, stream=s):
-                for i in range(args.steps):
-                    step(i)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        graph.replay()  # untimed replay, checked against the eager result
-        torch.cuda.synchronize()
-        if not torch.equal(y, ref_y):
-            raise SystemExit(f"M={m}: graph replay result differs from the eager call")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        graph.replay()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        if not torch.equal(y, ref_y):
-            raise SystemExit(f"M={m}: timed replay result differs from the eager call")
+        graph = capture(step)
+        elapsed, ev_ms = timed(graph)
+        del graph
         ms_step = elapsed * 1e3 / args.steps
+        kern_us = ev_ms * 1e3 / args.steps
+        if not fused:  # the matmul kernel alone in a graph of its own
+            graph = capture(kernel)
+            _, ev_ms = timed(graph)
+            del graph
+            kern_us = ev_ms * 1e3 / args.steps
         results[m] = {
             "ms_per_step": ms_step,
             "weight_gbs": weight_bytes() / (ms_step * 1e-3) / 1e9,
             "rows_per_s": N / (ms_step * 1e-3),
-            "kernel_us": kern_mean * 1e3,
-            "kernel_weight_gbs": weight_bytes() / (kern_mean * 1e-3) / 1e9,
-            "kernel_alg_gbs": algorithmic_bytes(m) / (kern_mean * 1e-3) / 1e9,
+            "kernel_us": kern_us,
+            "kernel_weight_gbs": weight_bytes() / (kern_us * 1e-6) / 1e9,
+            "kernel_alg_gbs": algorithmic_bytes(m) / (kern_us * 1e-6) / 1e9,
         }
-        log(f"M={m}: {ms_step * 1e3:.2f} us/step, {results[m]['weight_gbs']:.0f} weight GB/s "
-            f"(kernel {results[m]['kernel_weight_gbs']:.0f} GB/s)")
-        del graph
+        log(f"M={m}: {ms_step * 1e3:.2f} us/step, {results[m]['weight_gbs']:.0f} weight GB/s; "
+            f"matmul kernel {kern_us:.2f} us/launch (HIP events over the replay), "
+            f"{results[m]['kernel_alg_gbs']:.0f} GB/s algorithmic")
 
     if args.calibrate_copy:
         nbytes = args.calibrate_copy << 20
@@ -270,7 +277,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(r1["kernel_alg_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "gemv_kernel<Q4_K, M=1, fused Q8_K>",
+            "kernel": "gemv_pipe_kernel<Q4_K, M=1, fused Q8_K>",
             "kernel_us": round(r1["kernel_us"], 3),
             "bytes_per_launch": algorithmic_bytes(1),
         },

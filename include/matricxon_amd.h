@@ -6,6 +6,9 @@
  * Every call is asynchronous on `stream`, keeps no pointer after it returns and allocates no
  * device memory: scratch space is the caller's `workspace`.
  *
+ * Alignment: packed weights start on a 4-byte boundary; float activations `x` and `workspace`
+ * on a 16-byte boundary (every allocation of the HIP allocator is); otherwise -1.
+ *
  * Status codes (the reference's convention, app/native/src/mx_gemm.c:217-218, extended):
  *   0  ok
  *  -1  unsupported type or shape (the caller keeps another path; app/native/gemm.py:94-103)

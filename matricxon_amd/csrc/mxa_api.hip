@@ -35,6 +35,9 @@ int block_bytes(int t) {
 
 bool needs_q8k(int t) { return t != MXA_TYPE_IQ4_XS; }
 
+// The kernels read packed blocks as dwords and activations / workspace as 16-byte vectors.
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
 // Up to this many activation rows the matmul kernel quantizes x itself (no workspace).
 bool fused_quant(int n_tokens) { return n_tokens <= mxa::kFusedQuantMaxRows; }
 
@@ -75,7 +78,8 @@ size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features) {
 
 int mxa_quantize_q8_k(const float* x, int n_tokens, int in_features, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  if (x == nullptr || n_tokens <= 0 || in_features <= 0 || in_features % mxa::QK != 0)
+  if (x == nullptr || n_tokens <= 0 || in_features <= 0 || in_features % mxa::QK != 0 ||
+      !aligned(x, 16) || !aligned(workspace, 16))
     return MXA_ERR_UNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
     return MXA_ERR_WORKSPACE;
@@ -98,7 +102,7 @@ int mxa_gemm_q8k(int ggml_type, const void* w, const float* x, float* y, int n_t
                  int out_features, int in_features, const void* workspace,
                  size_t workspace_bytes, void* stream) {
   if (!mxa_supports(ggml_type, in_features) || w == nullptr || y == nullptr || n_tokens <= 0 ||
-      out_features <= 0)
+      out_features <= 0 || !aligned(w, 4) || !aligned(x, 16) || !aligned(workspace, 16))
     return MXA_ERR_UNSUPPORTED;
   mxa::ActBuffers buf{};
   const mxa::ActBuffers* abuf = nullptr;
@@ -122,11 +126,13 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
                    size_t workspace_bytes, void* stream) {
   if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr)
     return MXA_ERR_UNSUPPORTED;
-  if (x == nullptr || y == nullptr || n_tokens <= 0) return MXA_ERR_UNSUPPORTED;
+  if (x == nullptr || y == nullptr || n_tokens <= 0 || !aligned(x, 16) || !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
   bool any_q8k = false;
   long long total = 0;
   for (int i = 0; i < n; ++i) {
-    if (!mxa_supports(types[i], in_features) || ws[i] == nullptr || outs[i] <= 0)
+    if (!mxa_supports(types[i], in_features) || ws[i] == nullptr || outs[i] <= 0 ||
+        !aligned(ws[i], 4))
       return MXA_ERR_UNSUPPORTED;
     any_q8k |= needs_q8k(types[i]);
     total += outs[i];

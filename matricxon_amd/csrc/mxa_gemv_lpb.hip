@@ -1,0 +1,863 @@
+// Decode GEMV, lane-per-block form: y[m, n] = sum_k x[m, k] * W[n, k] for up to 4 activation rows.
+//
+// Memory. A wave owns R consecutive weight rows (R * nb <= 64 blocks; one row per pass of 64 blocks
+// when nb > 64). Those rows are one contiguous byte range, which the wave copies into its own LDS
+// region with global_load_lds_dwordx4: every instruction moves 1 KB of consecutive bytes (16 per
+// lane), the fully coalesced pattern that keeps HBM streaming. All of a wave's copies are issued
+// at its first instruction, before anything waits.
+//
+// Compute. Lane i of the wave then owns block i of that range (row i / nb, block i % nb) and reads
+// it from LDS: no cross-lane reduction, and LDS absorbs the blocks' alignment (Q6_K's 210-byte
+// blocks are read as dwords and realigned with v_alignbyte). The workgroup quantizes the float
+// activations to Q8_K once into LDS (the arithmetic of quantize_q8k_kernel; IQ4_XS keeps floats).
+//
+// Numerics (app/native/src/mx_gemm.c:241-261): exact integer block dots, then the per-block float
+// value goes to a wave-private LDS buffer and one lane per (row, activation row) folds the blocks
+// in order 0..nb-1 with the CPU oracle's fused multiply-adds: results equal it bit for bit (IQ4_XS:
+// float activations, within tolerance).
+#include "mxa_kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mxa {
+namespace {
+
+constexpr int kWaveLanes = 64;
+constexpr int kActPad = 16;  // LDS bytes of padding after each staged 256-value activation block
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+template <int TYPE>
+struct Lpb;
+
+// NW dwords of LDS from byte `off` of the 4-byte aligned `base` (off 2-byte aligned at worst).
+// LDS addresses stay base + integer offset throughout this file: an LDS pointer that passes
+// through an integer cast becomes a flat pointer, and flat loads are counted by vmcnt too.
+template <int NW>
+__device__ __forceinline__ void lds_words(const uint8_t* base, int off, uint32_t* w) {
+  const uint32_t* p = (const uint32_t*)(base + (off & ~3));
+  const uint32_t sh = (uint32_t)(off & 3);
+  uint32_t raw[NW + 1];
+#pragma unroll
+  for (int i = 0; i < NW + 1; ++i) raw[i] = p[i];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+}
+
+// Activations of one 256-value block of row m in LDS: q8 values, 16 bsums, scale (or 256 floats).
+struct ActBlock {
+  const int8_t* q;
+  const int16_t* bsums;
+  float d;
+  const float* x;
+};
+
+template <>
+struct Lpb<T_Q4_K> {
+  static constexpr int kBytes = 144;
+  static constexpr bool kHasD = false;
+  // value: fmaf(d, sumi, -(dmin * summ))   (mx_dot_k_ssse3.c:150-154)
+  template <int MAXM>
+  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+    const uint8_t* blk = wb + off;  // 4-byte aligned
+    const u32x4a4 h = *(const u32x4a4*)blk;
+    uint32_t q[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x4a4 v = *(const u32x4a4*)(blk + 16 + 16 * i);
+      q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
+    }
+    const float d = half_to_float(h.x), dmin = half_to_float(h.x >> 16);
+    const K4Scales s = k4_scales(h.y, h.z, h.w);
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      if (m < M) {
+        // X[sb]: sum of the 32 activations of sub-block sb (its two 16-value bsums)
+        const u32x4a4 b0 = *(const u32x4a4*)a[m].bsums, b1 = *(const u32x4a4*)(a[m].bsums + 8);
+        const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        int X[8];
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) X[sb] = (int)(int16_t)(bw[sb] & 0xFFFFu) + (int)(int16_t)(bw[sb] >> 16);
+        // High nibbles h as signed bytes 16 h - 128 ((w & 0xF0) ^ 0x80, one bit operation):
+        // sum(h * x) = (sum((16 h - 128) * x) + 128 X) / 16, exactly. 16 * sumi stays below 2^29.
+        int sumi16 = 0, summ = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          int lo = 0, hs = 0;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const i32x4a4 xl = *(const i32x4a4*)(a[m].q + 64 * c + 16 * i);
+            const i32x4a4 xh = *(const i32x4a4*)(a[m].q + 64 * c + 32 + 16 * i);
+            const int xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t w = q[8 * c + 4 * i + k];
+              lo = sdot4(w & 0x0F0F0F0Fu, (uint32_t)xlv[k], lo);
+              hs = sdot4((w & 0xF0F0F0F0u) ^ 0x80808080u, (uint32_t)xhv[k], hs);
+            }
+          }
+          // 24-bit multiplies (full rate): |lo| < 2^16, |hs + 128 X| < 2^20, scales < 64
+          sumi16 += 16 * __mul24((int)k4_pick(s.sc_lo, s.sc_hi, 2 * c), lo) +
+                    __mul24((int)k4_pick(s.sc_lo, s.sc_hi, 2 * c + 1), hs + 128 * X[2 * c + 1]);
+        }
+        const int sumi = sumi16 >> 4;  // exact: a multiple of 16
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) summ += (int)k4_pick(s.mn_lo, s.mn_hi, sb) * X[sb];
+        V[m] = fmaf(d, (float)sumi, -(dmin * (float)summ));
+      }
+    }
+    D = 0.0f;
+  }
+  __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
+};
+
+template <>
+struct Lpb<T_Q6_K> {
+  static constexpr int kBytes = 210;
+  static constexpr bool kHasD = true;
+  // value: sumi = sum_s sc_s * sum((u - 32) * q8); fold (y.d * d) * sumi   (mx_dot_k_ssse3.c:167-209)
+  template <int MAXM>
+  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+    uint32_t w[53];  // bytes 0..211: ql 0..127, qh 128..191, scales 192..207, d 208..209
+    lds_words<53>(wb, off, w);
+    int sumi[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) sumi[m] = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint32_t U[8];  // codes u = q + 32 of elements 128h + 32g + 4i .. +3
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t l = w[16 * h + ((g & 1) ? 8 : 0) + i], qh = w[32 + 8 * h + i];
+          U[i] = g == 0 ? q6_codes<0>(l, qh) : g == 1 ? q6_codes<1>(l, qh)
+               : g == 2 ? q6_codes<2>(l, qh) : q6_codes<3>(l, qh);
+        }
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m) {
+          if (m < M) {
+            const uint32_t bwd = *(const uint32_t*)(a[m].bsums + 8 * h + 2 * g);
+#pragma unroll
+            for (int half16 = 0; half16 < 2; ++half16) {  // sub-block 8h + 2g + half16
+              const i32x4a4 x = *(const i32x4a4*)(a[m].q + 128 * h + 32 * g + 16 * half16);
+              int sdot = 0;
+              sdot = sdot4(U[4 * half16 + 0], (uint32_t)x.x, sdot);
+              sdot = sdot4(U[4 * half16 + 1], (uint32_t)x.y, sdot);
+              sdot = sdot4(U[4 * half16 + 2], (uint32_t)x.z, sdot);
+              sdot = sdot4(U[4 * half16 + 3], (uint32_t)x.w, sdot);
+              const int sbi = 8 * h + 2 * g + half16;
+              const int sc = (int)(int8_t)(uint8_t)(w[48 + (sbi >> 2)] >> (8 * (sbi & 3)));
+              const int bs = half16 ? (int)(int16_t)(bwd >> 16) : (int)(int16_t)(bwd & 0xFFFFu);
+              sumi[m] += __mul24(sc, sdot - 32 * bs);  // |sc| < 2^7, |sdot - 32 bs| < 2^18
+            }
+          }
+        }
+      }
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) V[m] = (float)sumi[m];
+    D = half_to_float(w[52]);
+  }
+  __device__ static float fold(float acc, float xd, float v, float d) { return fmaf(xd * d, v, acc); }
+};
+
+template <>
+struct Lpb<T_Q8_0> {
+  static constexpr int kBytes = 272;  // eight 34-byte blocks
+  static constexpr bool kHasD = false;
+  // value: block_sum = sum_k d_k * sum(qs * q8) in k order (mx_dot_q8_0.c:8-18)
+  template <int MAXM>
+  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+    const uint8_t* blk = wb + off;  // 4-byte aligned
+    float bs[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) bs[m] = 0.0f;
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {  // pairs of 34-byte blocks: 68 bytes, 17 words
+      uint32_t w[17];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4a4 v = *(const u32x4a4*)(blk + 68 * pr + 16 * i);
+        w[4 * i] = v.x, w[4 * i + 1] = v.y, w[4 * i + 2] = v.z, w[4 * i + 3] = v.w;
+      }
+      w[16] = *(const uint32_t*)(blk + 68 * pr + 64);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {  // block k = 2pr + e: d then 32 qs
+        const int k = 2 * pr + e;
+        const float dk = e == 0 ? half_to_float(w[0]) : half_to_float(w[8] >> 16);
+        uint32_t qs[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          qs[i] = e == 0 ? __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2) : w[9 + i];
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m) {
+          if (m < M) {
+            const i32x4a4 x0 = *(const i32x4a4*)(a[m].q + 32 * k);
+            const i32x4a4 x1 = *(const i32x4a4*)(a[m].q + 32 * k + 16);
+            int p = 0;
+            p = sdot4(qs[0], (uint32_t)x0.x, p);
+            p = sdot4(qs[1], (uint32_t)x0.y, p);
+            p = sdot4(qs[2], (uint32_t)x0.z, p);
+            p = sdot4(qs[3], (uint32_t)x0.w, p);
+            p = sdot4(qs[4], (uint32_t)x1.x, p);
+            p = sdot4(qs[5], (uint32_t)x1.y, p);
+            p = sdot4(qs[6], (uint32_t)x1.z, p);
+            p = sdot4(qs[7], (uint32_t)x1.w, p);
+            bs[m] = fmaf(dk, (float)p, bs[m]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) V[m] = bs[m];
+    D = 0.0f;
+  }
+  __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
+};
+
+template <>
+struct Lpb<T_IQ4_XS> {
+  static constexpr int kBytes = 136;
+  static constexpr bool kHasD = false;
+  // value: sum over sub-blocks of dl * sum(x * grid) (mx_dot_f32.c:42-55 up to float order), in
+  // the order every IQ4_XS kernel here uses, so a token's result does not depend on the batch:
+  // p = sequential fmaf over a sub-block's 16 low-nibble / 16 high-nibble elements four at a
+  // time, quarters fmaf(dl1, p1, dl0 * p0), block (q0 + q1) + (q2 + q3), rows sum blocks in order
+  template <int MAXM>
+  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+    const uint8_t* blk = wb + off;  // 4-byte aligned
+    uint32_t w[34];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) {
+      const u32x2a4 v = *(const u32x2a4*)(blk + 8 * i);
+      w[2 * i] = v.x, w[2 * i + 1] = v.y;
+    }
+    const float d = half_to_float(w[0]);
+    const uint32_t sh = w[0] >> 16, sl = w[1];
+    float dl[8];
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+      const int ls = (int)(((sl >> (4 * ib)) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+      dl[ib] = d * (float)(ls - 32);
+    }
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      if (m < M) {
+        float L[4];  // 64-element quarters: fmaf(dl[2j+1], p[2j+1], dl[2j] * p[2j])
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float p[2];
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ib = 2 * j + t;
+            p[t] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t qw = w[2 + 4 * ib + i];
+              const uint32_t gl = iq4_lookup4(qw & 0x0F0F0F0Fu), gh = iq4_lookup4((qw >> 4) & 0x0F0F0F0Fu);
+              const float4 xl = *(const float4*)(a[m].x + 32 * ib + 4 * i);
+              const float4 xh = *(const float4*)(a[m].x + 32 * ib + 16 + 4 * i);
+              p[t] = fmaf(xl.x, sbyte_f<0>(gl), p[t]);
+              p[t] = fmaf(xl.y, sbyte_f<1>(gl), p[t]);
+              p[t] = fmaf(xl.z, sbyte_f<2>(gl), p[t]);
+              p[t] = fmaf(xl.w, sbyte_f<3>(gl), p[t]);
+              p[t] = fmaf(xh.x, sbyte_f<0>(gh), p[t]);
+              p[t] = fmaf(xh.y, sbyte_f<1>(gh), p[t]);
+              p[t] = fmaf(xh.z, sbyte_f<2>(gh), p[t]);
+              p[t] = fmaf(xh.w, sbyte_f<3>(gh), p[t]);
+            }
+          }
+          L[j] = fmaf(dl[2 * j + 1], p[1], dl[2 * j] * p[0]);
+        }
+        V[m] = (L[0] + L[1]) + (L[2] + L[3]);
+      }
+    }
+    D = 0.0f;
+  }
+  __device__ static float fold(float acc, float, float v, float) { return acc + v; }
+};
+
+// 16-lane maximum (lanes 16g..16g+15): quad butterflies, then the half-row and row mirrors.
+__device__ __forceinline__ float max16(float v) {
+#define MXA_DPP_MAX(ctrl) \
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)))
+  MXA_DPP_MAX(0xB1);
+  MXA_DPP_MAX(0x4E);
+  MXA_DPP_MAX(0x141);
+  MXA_DPP_MAX(0x140);
+#undef MXA_DPP_MAX
+  return v;
+}
+
+// LDS layout of a workgroup (dynamic shared memory):
+//   [act]  per activation row m and staged block bb: 256 q8 + kActPad | ... then bsums (32 B each)
+//          and scales (4 B each); IQ4_XS: 1024 B of floats + kActPad per block
+//   [wave] per wave: the weight bytes region (reg_bytes), then V / D buffers
+struct Geometry {
+  int rows_per_wave;    // R
+  int blocks_per_pass;  // blocks of one row in a pass (nb when R > 1)
+  int reg_bytes;        // weight region per wave
+  int act_blocks;       // activation blocks staged per pass
+};
+
+template <int TYPE, int MAXM, bool FUSEQ>
+__global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict__ w,
+                                                       long long row_bytes, Act act,
+                                                       float* __restrict__ y, long long ldy,
+                                                       int M, int N, Geometry geo) {
+  using L = Lpb<TYPE>;
+  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
+  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+  const int R = geo.rows_per_wave, bpp = geo.blocks_per_pass, nb = act.nb;
+  const int ab = geo.act_blocks;  // == bpp
+  uint8_t* act_q = smem;                                        // [MAXM][ab][kActBlk]
+  int16_t* act_bs = (int16_t*)(smem + MAXM * ab * kActBlk);      // [MAXM][ab][16]
+  float* act_d = (float*)(act_bs + MAXM * ab * 16);              // [MAXM][ab]
+  uint8_t* region = smem + ((MAXM * ab * (kActBlk + 32 + 4) + 15) & ~15);
+  const int wave_bytes = geo.reg_bytes + MAXM * 64 * 4 * 2;  // weights, then V and D (64 each)
+  uint8_t* wreg = region + wave * wave_bytes;
+  float* Vbuf = (float*)(wreg + geo.reg_bytes);                 // [MAXM][64]
+  float* Dbuf = Vbuf + MAXM * 64;                                // [64]
+
+  const int tile_rows = R * nw;
+  const int n_wave0 = xcd_tile(blockIdx.x, gridDim.x) * tile_rows + wave * R;  // first row of the wave
+  const uint8_t* w_end = w + (size_t)N * row_bytes;
+  // (row, activation row) pairs f = lane + 64 j (j < MAXM): row f % R, activation row f / R;
+  // R * M <= 64 * MAXM. Several passes happen only when R == 1.
+  float acc[MAXM];
+#pragma unroll
+  for (int j = 0; j < MAXM; ++j) acc[j] = 0.0f;
+
+  for (int c0 = 0; c0 < nb; c0 += bpp) {
+    const int cb = min(bpp, nb - c0);  // blocks of each row in this pass
+    // 1. the wave's bytes: R rows x cb blocks, one contiguous range when cb == nb (else R == 1)
+    const int nrows = max(0, min(R, N - n_wave0));
+    const uint8_t* src0 = w + (size_t)min(n_wave0, N - 1) * row_bytes + (size_t)c0 * L::kBytes;
+    const uintptr_t s_al = (uintptr_t)src0 & ~(uintptr_t)15;
+    const int mis = (int)((uintptr_t)src0 - s_al);
+    const int span = (cb == nb ? nrows * (int)row_bytes : cb * L::kBytes);
+    const int n_ins = (mis + span + 1023) >> 10;
+    // copies are whole aligned 16-byte chunks: the first and last may extend past the matrix,
+    // but a 16-byte aligned chunk holding one of its bytes never leaves that byte's page
+    const uintptr_t last = ((uintptr_t)w_end - 1) & ~(uintptr_t)15;
+    for (int t = 0; t < n_ins; ++t) {
+      const uintptr_t a = min(s_al + (uintptr_t)(t * 1024 + lane * 16), last);
+      __builtin_amdgcn_global_load_lds((const void*)a, (lds_void*)(wreg + t * 1024), 16, 0, 0);
+    }
+
+    // 2. activations of the pass into LDS (all M rows), quantized here when FUSEQ
+    if constexpr (FUSEQ) {
+      // 16 lanes per (m, block); lane part p holds values 16p..16p+15
+      for (int g = tid >> 4; g < M * cb; g += blockDim.x >> 4) {
+        const int m = g / cb, bb = g - m * cb, p = tid & 15;
+        const float* src = act.x + (size_t)m * act.k + (size_t)(c0 + bb) * QK + 16 * p;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 f = *(const float4*)(src + 4 * i);
+          v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = max16(amax);
+        int q[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = 0;
+        if (amax != 0.0f) {
+          const float iscale = 127.0f / amax;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) q[i] = (int)fminf(fmaxf(rintf(v[i] * iscale), -127.0f), 127.0f);
+        }
+        u32x4a4 packed;
+        int bsum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          packed[i] = (uint32_t)(q[4 * i] & 0xFF) | ((uint32_t)(q[4 * i + 1] & 0xFF) << 8) |
+                      ((uint32_t)(q[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * i + 3] & 0xFF) << 24);
+          bsum += q[4 * i] + q[4 * i + 1] + q[4 * i + 2] + q[4 * i + 3];
+        }
+        *(u32x4a4*)(act_q + (m * ab + bb) * kActBlk + 16 * p) = packed;
+        act_bs[(m * ab + bb) * 16 + p] = (int16_t)bsum;
+        if (p == 0) act_d[m * ab + bb] = amax / 127.0f;
+      }
+    } else if constexpr (kFloatAct) {
+      for (int i = tid; i < M * cb * 64; i += blockDim.x) {  // 16-byte pieces of float rows
+        const int m = i / (cb * 64), o = i - m * cb * 64, bb = o >> 6, pc = o & 63;
+        *(u32x4a4*)(act_q + (m * ab + bb) * kActBlk + 16 * pc) =
+            ld16((const uint8_t*)(act.x + (size_t)m * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
+      }
+    } else {
+      for (int i = tid; i < M * cb * 16; i += blockDim.x) {  // 16-byte pieces of q8 rows
+        const int m = i / (cb * 16), o = i - m * cb * 16, bb = o >> 4, pc = o & 15;
+        *(u32x4a4*)(act_q + (m * ab + bb) * kActBlk + 16 * pc) =
+            ld16((const uint8_t*)(act.q + (size_t)m * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
+      }
+      for (int i = tid; i < M * cb * 2; i += blockDim.x) {
+        const int m = i / (cb * 2), o = i - m * cb * 2, bb = o >> 1, hf = o & 1;
+        *(u32x4a4*)(act_bs + (m * ab + bb) * 16 + 8 * hf) =
+            ld16((const uint8_t*)(act.bsums + ((size_t)m * nb + c0 + bb) * 16) + 16 * hf);
+      }
+      for (int i = tid; i < M * cb; i += blockDim.x) {
+        const int m = i / cb, bb = i - m * cb;
+        act_d[m * ab + bb] = act.d[(size_t)m * nb + c0 + bb];
+      }
+    }
+    // weight bytes landed (global_load_lds completes into LDS before vmcnt drops), activations
+    // written: one barrier for the workgroup
+    __builtin_amdgcn_s_waitcnt(0x3F70);  // vmcnt(0)
+    __syncthreads();
+
+    // 3. lane -> block
+    const int fb = min(lane, nrows * cb - 1);
+    const int r = fb / cb, b = fb - r * cb;
+    if (nrows > 0) {
+      const int boff = mis + (cb == nb ? r * (int)row_bytes : 0) + b * L::kBytes;
+      ActBlock ablk[MAXM];
+#pragma unroll
+      for (int m = 0; m < MAXM; ++m) {
+        const int mc = min(m, M - 1);
+        ablk[m].q = (const int8_t*)(act_q + (mc * ab + b) * kActBlk);
+        ablk[m].bsums = act_bs + (mc * ab + b) * 16;
+        ablk[m].d = 0.0f;
+        ablk[m].x = (const float*)(act_q + (mc * ab + b) * kActBlk);
+      }
+      float V[MAXM], D;
+      L::template compute<MAXM>(wreg, boff, ablk, M, V, D);
+      if (lane < nrows * cb) {
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m)
+          if (m < M) Vbuf[m * 64 + lane] = V[m];
+        if (L::kHasD) Dbuf[lane] = D;
+      }
+      __builtin_amdgcn_wave_barrier();
+      // 4. fold this pass's blocks of each pair, in order
+#pragma unroll
+      for (int j = 0; j < MAXM; ++j) {
+        const int f = lane + 64 * j, fr = f % R, fm = f / R;
+        if (f < R * M && fr < nrows) {
+          const int base = fr * cb;
+          for (int bb = 0; bb < cb; ++bb) {
+            const float xd = kFloatAct ? 0.0f : act_d[fm * ab + bb];
+            acc[j] = L::fold(acc[j], xd, Vbuf[fm * 64 + base + bb], L::kHasD ? Dbuf[base + bb] : 0.0f);
+          }
+        }
+      }
+    }
+    __syncthreads();  // before the next pass overwrites LDS
+  }
+#pragma unroll
+  for (int j = 0; j < MAXM; ++j) {
+    const int f = lane + 64 * j, fr = f % R, fm = f / R;
+    if (f < R * M && fr < N - n_wave0) y[(size_t)fm * ldy + n_wave0 + fr] = acc[j];
+  }
+}
+
+template <int TYPE, int MAXM, bool FUSEQ>
+int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+               int M, int N, hipStream_t stream) {
+  using L = Lpb<TYPE>;
+  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
+  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  const int nb = act.nb;
+  Geometry geo;
+  // blocks staged per pass: a wave's 64 lanes, and (float activations, 1 KB per block and row)
+  // at most ~40 KB of activations
+  const int cap = kFloatAct ? max(1, min(kWaveLanes, 40960 / (MAXM * kActBlk))) : kWaveLanes;
+  if (nb <= cap) {
+    geo.rows_per_wave = kWaveLanes / nb;
+    geo.blocks_per_pass = nb;
+  } else {
+    geo.rows_per_wave = 1;
+    geo.blocks_per_pass = cap;
+  }
+  const int pass_bytes = geo.rows_per_wave * geo.blocks_per_pass * L::kBytes;
+  geo.reg_bytes = ((pass_bytes + 15 + 1023) / 1024) * 1024;
+  geo.act_blocks = geo.blocks_per_pass;
+  const int act_lds = MAXM * geo.act_blocks * (kActBlk + 32 + 4) + 16;
+  const int wave_lds = geo.reg_bytes + MAXM * 64 * 4 * 2;
+  // two workgroups per CU (<= 80 KB each), at most 8 waves
+  int nw = (80 * 1024 - act_lds) / wave_lds;
+  nw = max(1, min(8, nw));
+  const int lds = act_lds + nw * wave_lds;
+  if (lds > 160 * 1024) return -1;
+  const int tile_rows = geo.rows_per_wave * nw;
+  const int grid = (N + tile_rows - 1) / tile_rows;
+  auto kern = gemv_lpb_kernel<TYPE, MAXM, FUSEQ>;
+  static int lds_set = 0;  // the attribute only grows; one call per instantiation and size class
+  if (lds > 64 * 1024 && lds > lds_set) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    lds_set = 160 * 1024;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, row_bytes, act, y, ldy, M, N, geo);
+  return 0;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Pipelined form (blocks per row <= 64): compute overlaps the arrival of the weight bytes.
+//
+// A workgroup has `act_waves` waves that only stage the activations and `weight_waves` waves
+// that only move and multiply weights. vmcnt (a wave's count of outstanding memory operations)
+// is per wave, but the vector-memory queue of a CU is shared and drains in order: the activation
+// waves issue their loads first and the weight waves start copying only after a barrier, so the
+// activations never wait behind weight bytes. A weight wave owns R consecutive rows, i.e. R * nb
+// consecutive blocks of one contiguous byte range, and walks them in stages of 64 blocks (one per
+// lane) through a ring of P + 1 LDS buffers: it keeps P stages of copies in flight, waits only for
+// the copies of the stage it computes next (copies complete in issue order), issues the copies
+// of the stage P ahead into the buffer it has just finished with, and computes. Copies are issued
+// only as fast as the queue drains, so a wave that tried to issue everything up front would sit
+// in the issue queue instead of computing. After its last stage one lane per (row, activation
+// row) folds the row's nb block values in order.
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63]; lgkmcnt and expcnt are not waited for.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define MXA_VM(k) \
+  case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0x0F70); break;
+#define MXA_VM8(k) MXA_VM(k) MXA_VM(k + 1) MXA_VM(k + 2) MXA_VM(k + 3) MXA_VM(k + 4) \
+  MXA_VM(k + 5) MXA_VM(k + 6) MXA_VM(k + 7)
+  switch (n) {
+    MXA_VM8(0) MXA_VM8(8) MXA_VM8(16) MXA_VM8(24) MXA_VM8(32) MXA_VM8(40) MXA_VM8(48) MXA_VM8(56)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+#undef MXA_VM8
+#undef MXA_VM
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+}
+
+constexpr int kMaxCopies = 63;  // the largest vmcnt: copies a weight wave may have outstanding
+
+// global_load_lds_dwordx4: 16 bytes per lane from `g` to LDS byte address m0 + 16 * lane. Issued
+// as inline assembly so that the compiler's own wait insertion does not see it (it would add
+// vmcnt(0) before unrelated instructions); the kernel waits for these copies itself.
+__device__ __forceinline__ void copy16_to_lds(const void* g, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr) : "memory");
+}
+
+struct PipeGeo {
+  int rows_per_wave;  // R
+  int weight_waves;
+  int act_waves;
+  int ahead;          // P: stages of copies in flight while a stage is computed
+  int buf_kb;         // KB of one stage buffer (the most copies a stage needs)
+};
+
+// Stage 64 s .. 64 s + 63 of a range of nblk blocks that starts `mis` bytes past a 16-byte
+// boundary needs this many 1 KB copies (64 blocks are a multiple of 16 bytes for every type, so
+// every stage starts `mis` bytes past a boundary too).
+template <int KB>
+__device__ __forceinline__ int stage_copies(int s, int nblk, int mis) {
+  const int nbk = min(64, nblk - 64 * s);
+  return (mis + nbk * KB + 1023) >> 10;
+}
+
+// The activation waves: M rows x nb blocks into LDS (quantized to Q8_K when FUSEQ; copied from
+// the workspace, or as floats for IQ4_XS). Executes the workgroup's first barrier once its first
+// loads are issued, and the second when everything is in LDS.
+template <int TYPE, bool FUSEQ>
+__device__ __forceinline__ void stage_activations(const Act& act, int M, int aw, int na, int lane,
+                                                  uint8_t* act_q, int16_t* act_bs, float* act_d) {
+  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
+  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  const int nb = act.nb, total = M * nb;
+  if constexpr (FUSEQ) {
+    // 16 lanes per (m, block): lane part p holds values 16p..16p+15; kBatch groups per lane are
+    // loaded before any is quantized
+    constexpr int kBatch = 4;
+    const int per = 4 * na, p = lane & 15;
+    float4 v[kBatch][4];
+    auto load = [&](int g0) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = min(g0 + i * per, total - 1);
+        const int m = g / nb, b = g - m * nb;
+        const float* src = act.x + (size_t)m * act.k + (size_t)b * QK + 16 * p;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[i][q] = *(const float4*)(src + 4 * q);
+      }
+    };
+    int gw = 4 * aw;  // the wave's first group (its lanes 16r.. take group gw + r); gw < total
+    int g0 = gw + (lane >> 4);
+    load(g0);
+    __builtin_amdgcn_s_barrier();  // first barrier: these loads are queued ahead of any copy
+    for (;;) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = g0 + i * per;
+        if (g < total) {  // uniform over the 16 lanes of the group
+          const int m = g / nb, b = g - m * nb;
+          const float x[16] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w, v[i][1].x, v[i][1].y,
+                               v[i][1].z, v[i][1].w, v[i][2].x, v[i][2].y, v[i][2].z, v[i][2].w,
+                               v[i][3].x, v[i][3].y, v[i][3].z, v[i][3].w};
+          float amax = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[e]));
+          amax = max16(amax);
+          int q[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) q[e] = 0;
+          if (amax != 0.0f) {
+            const float iscale = 127.0f / amax;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) q[e] = (int)fminf(fmaxf(rintf(x[e] * iscale), -127.0f), 127.0f);
+          }
+          u32x4a4 packed;
+          int bsum = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            packed[e] = (uint32_t)(q[4 * e] & 0xFF) | ((uint32_t)(q[4 * e + 1] & 0xFF) << 8) |
+                        ((uint32_t)(q[4 * e + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * e + 3] & 0xFF) << 24);
+            bsum += q[4 * e] + q[4 * e + 1] + q[4 * e + 2] + q[4 * e + 3];
+          }
+          *(u32x4a4*)(act_q + (m * nb + b) * kActBlk + 16 * p) = packed;
+          act_bs[(m * nb + b) * 16 + p] = (int16_t)bsum;
+          if (p == 0) act_d[m * nb + b] = amax / 127.0f;
+        }
+      }
+      gw += per * kBatch;
+      g0 += per * kBatch;
+      if (gw >= total) break;  // wave-uniform
+      load(g0);
+    }
+  } else {
+    __builtin_amdgcn_s_barrier();  // first barrier
+    if constexpr (kFloatAct) {
+      for (int i = aw * 64 + lane; i < total * 64; i += na * 64) {  // 16-byte pieces of float rows
+        const int g = i >> 6, pc = i & 63, m = g / nb, b = g - m * nb;
+        *(u32x4a4*)(act_q + g * kActBlk + 16 * pc) =
+            ld16((const uint8_t*)(act.x + (size_t)m * act.k + (size_t)b * QK) + 16 * pc);
+      }
+    } else {
+      for (int i = aw * 64 + lane; i < total * 16; i += na * 64) {  // 16-byte pieces of q8 rows
+        const int g = i >> 4, pc = i & 15, m = g / nb, b = g - m * nb;
+        *(u32x4a4*)(act_q + g * kActBlk + 16 * pc) =
+            ld16((const uint8_t*)(act.q + (size_t)m * act.k + (size_t)b * QK) + 16 * pc);
+      }
+      for (int i = aw * 64 + lane; i < total * 2; i += na * 64)  // (m, b) bsums are contiguous
+        *(u32x4a4*)(act_bs + 8 * i) = ld16((const uint8_t*)(act.bsums + 8 * (size_t)i));
+      for (int i = aw * 64 + lane; i < total; i += na * 64) act_d[i] = act.d[i];
+    }
+  }
+  // Nothing of this wave stays outstanding (the compiler may merge the barrier below with the
+  // weight waves' one, and its wait bookkeeping would carry these loads over to them).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // second barrier: the activations are in LDS
+}
+
+template <int TYPE, int MAXM, bool FUSEQ>
+__global__ __launch_bounds__(1024) void gemv_pipe_kernel(const uint8_t* w, long long row_bytes,
+                                                         Act act, float* __restrict__ y,
+                                                         long long ldy, int M, int N, PipeGeo geo) {
+  using L = Lpb<TYPE>;
+  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
+  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar control flow
+  const int nb = act.nb, na = geo.act_waves, total = M * nb;
+  uint8_t* act_q = smem;                                    // [M * nb][kActBlk]
+  int16_t* act_bs = (int16_t*)(smem + total * kActBlk);     // [M * nb][16]
+  float* act_d = (float*)(act_bs + total * 16);             // [M * nb]
+  uint8_t* region = smem + ((total * (kActBlk + 32 + 4) + 15) & ~15);
+
+  if (wave < na) {  // activation wave
+    stage_activations<TYPE, FUSEQ>(act, M, wave, na, lane, act_q, act_bs, act_d);
+    return;
+  }
+
+  const int R = geo.rows_per_wave, P = geo.ahead, ww = wave - na;
+  const int vslots = R * nb;
+  const int buf_bytes = geo.buf_kb * 1024;
+  const int wave_bytes = (P + 1) * buf_bytes + vslots * 4 * (MAXM + 1);
+  uint8_t* wreg = region + ww * wave_bytes;
+  float* Vbuf = (float*)(wreg + (P + 1) * buf_bytes);  // [MAXM][vslots]
+  float* Dbuf = Vbuf + MAXM * vslots;                   // [vslots]
+
+  const int n0 = (xcd_tile(blockIdx.x, gridDim.x) * geo.weight_waves + ww) * R;
+  const int nrows = max(0, min(R, N - n0));
+  const int nblk = nrows * nb, stages = (nblk + 63) >> 6;
+  const uint8_t* src0 = w + (size_t)min(n0, N - 1) * row_bytes;
+  const uintptr_t s_al = (uintptr_t)src0 & ~(uintptr_t)15;
+  const int mis = (int)((uintptr_t)src0 - s_al);
+  // whole aligned 16-byte chunks: the first and last may extend past the matrix, but a 16-byte
+  // aligned chunk holding one of its bytes never leaves that byte's page
+  const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
+  const uint32_t lds_w = (uint32_t)(uintptr_t)(lds_u8*)wreg;
+  auto issue = [&](int s) {
+    const uintptr_t g = s_al + (uintptr_t)s * 64 * L::kBytes + (uintptr_t)lane * 16;
+    const uint32_t dst = lds_w + (uint32_t)((s % (P + 1)) * buf_bytes);
+    const int n = stage_copies<L::kBytes>(s, nblk, mis);
+    if (s + 1 < stages) {  // the bytes of a later stage follow: no copy passes the matrix end
+      for (int t = 0; t < n; ++t) copy16_to_lds((const void*)(g + (uintptr_t)t * 1024), dst + t * 1024);
+    } else {
+      for (int t = 0; t < n; ++t) copy16_to_lds((const void*)min(g + (uintptr_t)t * 1024, last), dst + t * 1024);
+    }
+  };
+
+  __builtin_amdgcn_s_barrier();  // first barrier: the activation loads are queued
+  for (int s = 0; s < min(P, stages); ++s) issue(s);
+  __builtin_amdgcn_s_barrier();  // second barrier: the activations are in LDS
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+
+  // lane l computes block 64 s + l of the range: block b = (64 s + l) mod nb of its row, kept
+  // incrementally (stage s + 1 adds 64 mod nb); lanes past the range end redo its last block
+  const int step = 64 % nb;
+  int b = lane % nb;
+  const int lane_off = mis + (int)__umul24(lane, L::kBytes);
+  for (int s = 0; s < stages; ++s) {
+    // copies issued after stage s: stages s + 1 .. min(s + P - 1, stages - 1)
+    int after = 0;
+    for (int k = s + 1; k <= min(s + P - 1, stages - 1); ++k) after += stage_copies<L::kBytes>(k, nblk, mis);
+    wait_vmcnt(after);
+    if (s + P < stages) issue(s + P);
+    int jl = lane, boff = lane_off, bb = b;
+    if (64 * s + 64 > nblk) {  // partial last stage
+      jl = min(lane, nblk - 1 - 64 * s);
+      boff = mis + (int)__umul24(jl, L::kBytes);
+      bb = (64 * s + jl) % nb;
+    }
+    const int aoff = (int)__umul24(bb, kActBlk);
+    ActBlock ablk[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int row = min(m, M - 1) * nb;
+      ablk[m].q = (const int8_t*)(act_q + row * kActBlk + aoff);
+      ablk[m].bsums = act_bs + row * 16 + bb * 16;
+      ablk[m].d = 0.0f;
+      ablk[m].x = (const float*)(act_q + row * kActBlk + aoff);
+    }
+    float V[MAXM], D;
+    L::template compute<MAXM>(wreg + (s % (P + 1)) * buf_bytes, boff, ablk, M, V, D);
+    b += step;
+    b = b >= nb ? b - nb : b;
+    const int j = 64 * s + jl;
+    if (jl == lane) {
+#pragma unroll
+      for (int m = 0; m < MAXM; ++m)
+        if (m < M) Vbuf[m * vslots + j] = V[m];
+      if (L::kHasD) Dbuf[j] = D;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // fold: pair f -> row f % nrows, activation row f / nrows; blocks in order
+  for (int f = lane; f < nrows * M; f += 64) {
+    const int fm = f / nrows, fr = f - fm * nrows;
+    const float* v = Vbuf + fm * vslots + fr * nb;
+    const float* dd = Dbuf + fr * nb;
+    const float* xd = act_d + fm * nb;
+    float acc = 0.0f;
+    for (int bb = 0; bb < nb; ++bb)
+      acc = L::fold(acc, kFloatAct ? 0.0f : xd[bb], v[bb], L::kHasD ? dd[bb] : 0.0f);
+    y[(size_t)fm * ldy + n0 + fr] = acc;
+  }
+}
+
+int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+// Returns -1 when the shape does not suit the pipelined form (the caller uses gemv_lpb_kernel).
+template <int TYPE, int MAXM, bool FUSEQ>
+int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+                int M, int N, hipStream_t stream) {
+  using L = Lpb<TYPE>;
+  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
+  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  constexpr int kLdsMax = 160 * 1024;
+  constexpr int kBufKb = (15 + 64 * L::kBytes + 1023) / 1024;  // copies of a full stage, worst case
+  const int nb = act.nb;
+  if (nb > kWaveLanes) return -1;
+  const int total = M * nb;
+  const int act_lds = total * (kActBlk + 32 + 4) + 16;
+  if (act_lds > 48 * 1024) return -1;
+  const int na = min(4, (total + 15) / 16);
+  const int ncu = cu_count();
+  PipeGeo geo;
+  geo.act_waves = na;
+  geo.buf_kb = kBufKb;
+  auto wave_bytes = [&](int P, int R) { return (P + 1) * kBufKb * 1024 + R * nb * 4 * (MAXM + 1); };
+  // First choice: one workgroup per CU whose waves stream all their rows (every row requested in
+  // one round). When the rows' block values do not fit beside the buffers: two workgroups per CU
+  // of about 8 stages per wave, so that one fills its pipeline while the other drains. One stage
+  // in flight per wave and as many waves as fit (up to 8, two per SIMD) measured fastest on
+  // MI355X: more copies in flight only lengthen the queue at HBM.
+  int P = 0, nw = 0, R = 0;
+  bool ok = false;
+  for (int mode = 0; mode < 4 && !ok; ++mode) {
+    const bool persistent = mode < 2;
+    P = mode % 2 == 0 ? 1 : 2;
+    const int budget = (persistent ? kLdsMax : kLdsMax / 2) - act_lds;
+    for (nw = min(16 - na, 8); nw >= 2 && !ok; --nw) {
+      R = persistent ? (int)((N + (long long)ncu * nw - 1) / ((long long)ncu * nw)) : max(1, 512 / nb);
+      ok = nw * wave_bytes(P, R) <= budget;
+      if (ok) break;
+    }
+  }
+  if (!ok || kBufKb * P > kMaxCopies) return -1;
+  geo.ahead = P;
+  geo.weight_waves = nw;
+  geo.rows_per_wave = R;
+  const int lds = act_lds + nw * wave_bytes(P, R);
+  if (lds > kLdsMax) return -1;
+  const int grid = (int)((N + (long long)nw * R - 1) / ((long long)nw * R));
+  auto kern = gemv_pipe_kernel<TYPE, MAXM, FUSEQ>;
+  static bool lds_set = false;
+  if (!lds_set) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    lds_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (nw + na)), lds, stream, w, row_bytes, act, y,
+                     ldy, M, N, geo);
+  return 0;
+}
+
+template <int TYPE, int MAXM, bool FUSEQ>
+int launch_decode(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+                  int M, int N, hipStream_t stream) {
+  if (launch_pipe<TYPE, MAXM, FUSEQ>(w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
+  return launch_lpb<TYPE, MAXM, FUSEQ>(w, row_bytes, act, y, ldy, M, N, stream);
+}
+
+template <int TYPE>
+int launch_lpb_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+                    int M, int N, hipStream_t stream) {
+  constexpr bool kQ8K = TYPE != T_IQ4_XS;
+  const bool fuse = kQ8K && act.q == nullptr;
+  if (M == 1) return fuse ? launch_decode<TYPE, 1, kQ8K>(w, row_bytes, act, y, ldy, M, N, stream)
+                          : launch_decode<TYPE, 1, false>(w, row_bytes, act, y, ldy, M, N, stream);
+  if (M == 2) return fuse ? launch_decode<TYPE, 2, kQ8K>(w, row_bytes, act, y, ldy, M, N, stream)
+                          : launch_decode<TYPE, 2, false>(w, row_bytes, act, y, ldy, M, N, stream);
+  return fuse ? launch_decode<TYPE, 4, kQ8K>(w, row_bytes, act, y, ldy, M, N, stream)
+              : launch_decode<TYPE, 4, false>(w, row_bytes, act, y, ldy, M, N, stream);
+}
+
+}  // namespace
+
+int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                    long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+  if (m_rows < 1 || m_rows > 4) return -1;
+  switch (type) {
+    case T_Q4_K: return launch_lpb_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q6_K: return launch_lpb_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q8_0: return launch_lpb_type<T_Q8_0>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_IQ4_XS: return launch_lpb_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    default: return -1;
+  }
+}
+
+}  // namespace mxa

@@ -53,6 +53,11 @@ constexpr int kFusedQuantMaxRows = 4;
 int launch_gemv(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Decode GEMV for 1 <= m_rows <= 4 with lane-per-block compute on weight rows staged into LDS
+// by coalesced copies. Same contract as launch_gemv.
+int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 // Matrix-core kernel for batched decode: Q4_K, 1 <= m_rows <= 16, on Q8_K activations already
 // in the workspace.
 bool mfma_decode_supported(int type, int m_rows);

@@ -240,6 +240,8 @@ int launch_mfma_decode(int type, const uint8_t* w, long long row_bytes, const Ac
 
 int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                   long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+  if (m_rows <= kFusedQuantMaxRows)
+    return launch_gemv_lpb(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
   if (act.q != nullptr && mfma_decode_supported(type, 1)) {
     // passes of up to 16 activation rows on the matrix cores
     for (int m0 = 0; m0 < m_rows; m0 += 16) {

@@ -64,22 +64,27 @@ def test_supports_and_sizes(lib) -> None:
 
 def test_argument_errors_return_status_without_launching(lib) -> None:
     vp = ctypes.c_void_p
+    a = vp(0x10000)  # a well-aligned stand-in address: nothing is dereferenced on these paths
     # unsupported type / shape -> -1
-    assert lib.mxa_gemm(10, vp(1), vp(1), vp(1), 1, 4, 4096, vp(1), 1 << 20, None) == -1
-    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 1, 4, 4000, vp(1), 1 << 20, None) == -1
-    assert lib.mxa_gemm(12, None, vp(1), vp(1), 1, 4, 4096, vp(1), 1 << 20, None) == -1
-    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 0, 4, 4096, vp(1), 1 << 20, None) == -1
+    assert lib.mxa_gemm(10, a, a, a, 1, 4, 4096, a, 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, a, a, a, 1, 4, 4000, a, 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, None, a, a, 1, 4, 4096, a, 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, a, a, a, 0, 4, 4096, a, 1 << 20, None) == -1
+    # misaligned weights (dwords), activations or workspace (16-byte vectors) -> -1
+    assert lib.mxa_gemm(12, vp(0x10002), a, a, 1, 4, 4096, a, 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, a, vp(0x10008), a, 1, 4, 4096, a, 1 << 20, None) == -1
+    assert lib.mxa_gemm(12, a, a, a, 16, 4, 4096, vp(0x10004), 1 << 20, None) == -1
+    assert lib.mxa_quantize_q8_k(vp(0x10004), 2, 512, a, 1 << 20, None) == -1
     # workspace too small -> -2
-    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 16, 4, 4096, vp(1), 1000, None) == -2
-    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 16, 4, 4096, None, 1 << 20, None) == -2
-    assert lib.mxa_gemm(12, vp(1), vp(1), vp(1), 5, 4, 4096, vp(1), 1000, None) == -2
-    assert lib.mxa_quantize_q8_k(vp(1), 2, 512, vp(1), 10, None) == -2
-    assert lib.mxa_dequantize(11, vp(1), 4, vp(1), None) == -1
-    assert lib.mxa_dequant_rows(12, vp(1), 10, vp(1), 2, 300, vp(1), None) == -1
+    assert lib.mxa_gemm(12, a, a, a, 16, 4, 4096, a, 1000, None) == -2
+    assert lib.mxa_gemm(12, a, a, a, 16, 4, 4096, None, 1 << 20, None) == -2
+    assert lib.mxa_gemm(12, a, a, a, 5, 4, 4096, a, 1000, None) == -2
+    assert lib.mxa_quantize_q8_k(a, 2, 512, a, 10, None) == -2
+    assert lib.mxa_dequantize(11, a, 4, a, None) == -1
+    assert lib.mxa_dequant_rows(12, a, 10, a, 2, 300, a, None) == -1
     n = 5
     types = (ctypes.c_int * n)(*([12] * n))
-    assert lib.mxa_gemm_multi(n, types, vp(1), vp(1), vp(1), vp(1), 1, 4096, vp(1), 1 << 20,
-                              None) == -1
+    assert lib.mxa_gemm_multi(n, types, a, a, a, a, 1, 4096, a, 1 << 20, None) == -1
     assert lib.mxa_last_error() == b""
 
 

@@ -192,3 +192,35 @@ def test_unsupported_shapes_fail_loudly(gpu) -> None:
         gpu.matmul(D.Q4_K, w, x, 5, 512)  # wrong row count
     with pytest.raises(ValueError):
         gpu.matmul(D.Q4_K, w.cpu(), x, 4, 512)  # host tensor
+
+
+# Shapes for the decode kernel's row/lane geometry (n_tokens <= 4): one wave holds
+# R = 64 // blocks-per-row rows, so small K gives many rows per wave and more (row, token) pairs
+# than lanes; K > 64 * 256 takes several passes over a row; N not a multiple of the rows per
+# workgroup leaves partial tiles and idle waves.
+DECODE_SHAPES = [(1, 256, 2), (130, 256, 4), (65, 512, 3), (3, 16640, 1), (5, 16640, 4),
+                 (9, 18432, 2), (70, 4096, 4), (29, 2304, 3), (301, 1024, 1)]
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("n,k,m", DECODE_SHAPES)
+def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None:
+    w = S.packed_weight(ggml_type, n, k, seed=n * 7 + k + m)
+    x = S.activations(m, k, seed=m * 5 + n)
+    check_gemm(gpu, oracle, ggml_type, w, x, n, k)
+
+
+@pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
+@pytest.mark.parametrize("n,k,m", [(130, 256, 4), (5, 16640, 3), (70, 4096, 1)])
+def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> None:
+    """The same kernel reading Q8_K activations from the workspace instead of quantizing them."""
+    from matricxon_amd.gemm import q8k_bytes
+
+    w = S.packed_weight(ggml_type, n, k, seed=n + m)
+    x = dev(S.activations(m, k, seed=k + m))
+    ws = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device="cuda")
+    gpu.quantize_into(x, ws)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    got = host(gpu.matmul_q8k(ggml_type, dev(w), ws, None, out, m, n, k))
+    want = oracle.gemm(ggml_type, w, host(x), n, k)
+    assert np.array_equal(bits(got), bits(want))
