@@ -45,10 +45,9 @@ def log(msg: str) -> None:
 
 
 def algorithmic_bytes(m: int) -> int:
-    """Bytes one launch must move at minimum: the packed weight once, the Q8_K activations
-    (int8 values, one fp32 scale and 16 int16 sums per 256 values) and the fp32 outputs."""
-    nb = K // 256
-    return N * (K // 256) * 144 + m * (K + nb * 4 + nb * 32) + m * N * 4
+    """Bytes one launch must move at minimum: the packed weight once, the fp32 activations and the
+    fp32 outputs (weight + M*K*4 + M*N*4)."""
+    return N * (K // 256) * 144 + m * K * 4 + m * N * 4
 
 
 def weight_bytes() -> int:
