@@ -98,6 +98,88 @@ def cpu_baseline(w_np, x_np, seconds: float):
     }
 
 
+def _graph_us(fn, steps: int, warmup: int) -> float:
+    """Microseconds per step of a HIP-graph replay of `steps` calls of fn(i)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(steps):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
+    """BASELINE configs 1-5 on seeded synthetic data; weights rotated over
+    copies totalling > 1 GiB where one copy fits in the 256 MB MALL."""
+    import torch
+
+    from matricxon_amd import synthetic as S
+    from matricxon_amd.quant_types import row_bytes
+
+    def weights(t, n, k, seed):
+        w = torch.from_numpy(S.packed_weight(t, n, k, seed=seed)).to(dev)
+        c = max(1, math.ceil((1 << 30) / w.numel()) + 1) if w.numel() < (512 << 20) else 1
+        return [w] + [w.clone() for _ in range(c - 1)]
+
+    def report(name, us, wbytes, flops=None):
+        d = {"config": name, "us": round(us, 2), "weight_gbs": round(wbytes / us / 1e3, 1),
+             "pct_hbm": round(100 * wbytes / us / 1e3 / HBM_PEAK_GBS, 1)}
+        if flops:
+            d["tflops"] = round(flops / us / 1e6, 1)
+        print(json.dumps(d), file=sys.stderr, flush=True)
+
+    def gemv(name, t, n, k, ms, seed):
+        ws = weights(t, n, k, seed)
+        for m in ms:
+            x = torch.from_numpy(S.activations(m, k, seed=seed + m)).to(dev)
+            y = torch.empty((m, n), dtype=torch.float32, device=dev)
+            us = _graph_us(lambda i: gemm.matmul(t, ws[i % len(ws)], x, n, k, out=y), steps, warmup)
+            report(f"{name} M={m}", us, n * row_bytes(t, k), 2.0 * m * n * k)
+        del ws
+
+    gemv("cfg1 Q8_0 4096x4096", 8, 4096, 4096, [1], 11)
+    gemv("cfg2 Q4_K 14336x4096", 12, 14336, 4096, [1, 4, 8, 16], 12)
+    gemv("cfg3 Q6_K 128256x4096", 14, 128256, 4096, [1, 16], 13)
+    # q, k (Q4_K), v (Q6_K), o, gate, up (Q4_K), down (Q6_K)
+    layer = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096), (12, 4096, 4096),
+             (12, 14336, 4096), (12, 14336, 4096), (14, 4096, 14336)]
+    lw = [weights(t, n, k, 40 + i)[:2] for i, (t, n, k) in enumerate(layer)]
+    for m in (1, 16):
+        xs = {k: torch.from_numpy(S.activations(m, k, seed=50 + k)).to(dev) for k in (4096, 14336)}
+        ys = [torch.empty((m, n), dtype=torch.float32, device=dev) for _, n, _ in layer]
+
+        def layer_step(i):
+            for j, (t, n, k) in enumerate(layer):
+                gemm.matmul(t, lw[j][i % 2], xs[k], n, k, out=ys[j])
+        wb = sum(n * row_bytes(t, k) for t, n, k in layer)
+        report(f"cfg4 llama3-8b layer (7 projections) M={m}", _graph_us(layer_step, steps, warmup),
+               wb, 2.0 * m * sum(n * k for _, n, k in layer))
+    del lw
+    for t, name, n in ((12, "cfg5 Q4_K 14336x4096", 14336), (23, "cfg5 IQ4_XS 4096x4096", 4096)):
+        w = torch.from_numpy(S.packed_weight(t, n, 4096, seed=60 + t)).to(dev)
+        for m in (512, 2048):
+            x = torch.from_numpy(S.activations(m, 4096, seed=70 + m)).to(dev)
+            y = torch.empty((m, n), dtype=torch.float32, device=dev)
+            us = _graph_us(lambda i: gemm.matmul(t, w, x, n, 4096, out=y), max(3, steps // 10), 2)
+            report(f"{name} prefill M={m}", us, n * row_bytes(t, 4096), 2.0 * m * n * 4096)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +192,8 @@ def main() -> int:
                     help="only the per-launch kernel timing loop (for rocprofv3 --pmc runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (scale for HBM counters)")
+    ap.add_argument("--configs", action="store_true",
+                    help="also time BASELINE configs 1-5 (one JSON line each on stderr)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -220,6 +304,9 @@ def main() -> int:
         log(f"M={m}: {ms_step * 1e3:.2f} us/step, {results[m]['weight_gbs']:.0f} weight GB/s; "
             f"matmul kernel {kern_us:.2f} us/launch (HIP events over the replay), "
             f"{results[m]['kernel_alg_gbs']:.0f} GB/s algorithmic")
+
+    if args.configs:
+        bench_configs(gemm, dev, max(20, args.steps // 4), args.warmup)
 
     if args.calibrate_copy:
         nbytes = args.calibrate_copy << 20

@@ -64,6 +64,12 @@ bool mfma_decode_supported(int type, int m_rows);
 int launch_mfma_decode(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                        long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Matrix-core kernel for m_rows > 4 (batched decode and prefill) on Q8_K activations already in
+// the workspace: Q4_K, Q6_K, Q8_0.
+bool mtile_supported(int type);
+int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 // The matmul for any m_rows: picks the kernel (matrix-core decode, or the dot4 GEMV in passes of
 // up to 16 rows).
 int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,

@@ -242,6 +242,21 @@ int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& ac
                   long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (m_rows <= kFusedQuantMaxRows)
     return launch_gemv_lpb(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+  if (act.q != nullptr && mtile_supported(type))
+    return launch_mtile(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+  if (type == T_IQ4_XS) {
+    // float activations: the decode kernel in passes of kFusedQuantMaxRows rows (the one IQ4_XS
+    // summation order of every kernel here, so a row's result does not depend on the batch)
+    for (int m0 = 0; m0 < m_rows; m0 += kFusedQuantMaxRows) {
+      Act a = act;
+      a.q = nullptr;
+      a.x = act.x + (size_t)m0 * act.k;
+      const int st = launch_gemv_lpb(type, w, row_bytes, a, y + (size_t)m0 * ldy, ldy,
+                                     min(kFusedQuantMaxRows, m_rows - m0), n_rows, stream);
+      if (st != 0) return st;
+    }
+    return 0;
+  }
   if (act.q != nullptr && mfma_decode_supported(type, 1)) {
     // passes of up to 16 activation rows on the matrix cores
     for (int m0 = 0; m0 < m_rows; m0 += 16) {
