@@ -45,12 +45,27 @@ __device__ __forceinline__ void lds_words(const uint8_t* base, int off, uint32_t
   for (int i = 0; i < NW; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
 }
 
-// Activations of one 256-value block of row m in LDS: q8 values, 16 bsums, scale (or 256 floats).
+// Activations of one 256-value block of row m in LDS: q8 values, 16 bsums (or 256 floats).
 struct ActBlock {
   const int8_t* q;
   const int16_t* bsums;
   float d;
   const float* x;
+  __device__ i32x4a4 q16(int off) const { return *(const i32x4a4*)(q + off); }  // q8[off .. off + 15]
+  __device__ u32x4a4 bs8(int h) const { return *(const u32x4a4*)(bsums + 8 * h); }  // bsums 8h .. 8h + 7
+  __device__ uint32_t bs2(int j) const { return *(const uint32_t*)(bsums + 2 * j); }  // bsums 2j, 2j + 1
+  __device__ float4 x4(int off) const { return *(const float4*)(x + off); }
+};
+
+// The same block held in registers (one activation row): the arrays are only ever indexed with
+// constants once the compute loops are unrolled.
+struct ActRegs {
+  i32x4a4 q[16];
+  u32x4a4 bs[2];
+  __device__ i32x4a4 q16(int off) const { return q[off >> 4]; }
+  __device__ u32x4a4 bs8(int h) const { return bs[h]; }
+  __device__ uint32_t bs2(int j) const { return bs[j >> 2][j & 3]; }
+  __device__ float4 x4(int) const { return float4{0.0f, 0.0f, 0.0f, 0.0f}; }
 };
 
 template <>
@@ -58,8 +73,8 @@ struct Lpb<T_Q4_K> {
   static constexpr int kBytes = 144;
   static constexpr bool kHasD = false;
   // value: fmaf(d, sumi, -(dmin * summ))   (mx_dot_k_ssse3.c:150-154)
-  template <int MAXM>
-  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
     const uint8_t* blk = wb + off;  // 4-byte aligned
     const u32x4a4 h = *(const u32x4a4*)blk;
     uint32_t q[32];
@@ -74,7 +89,7 @@ struct Lpb<T_Q4_K> {
     for (int m = 0; m < MAXM; ++m) {
       if (m < M) {
         // X[sb]: sum of the 32 activations of sub-block sb (its two 16-value bsums)
-        const u32x4a4 b0 = *(const u32x4a4*)a[m].bsums, b1 = *(const u32x4a4*)(a[m].bsums + 8);
+        const u32x4a4 b0 = a[m].bs8(0), b1 = a[m].bs8(1);
         const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
         int X[8];
 #pragma unroll
@@ -87,8 +102,8 @@ struct Lpb<T_Q4_K> {
           int lo = 0, hs = 0;
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
-            const i32x4a4 xl = *(const i32x4a4*)(a[m].q + 64 * c + 16 * i);
-            const i32x4a4 xh = *(const i32x4a4*)(a[m].q + 64 * c + 32 + 16 * i);
+            const i32x4a4 xl = a[m].q16(64 * c + 16 * i);
+            const i32x4a4 xh = a[m].q16(64 * c + 32 + 16 * i);
             const int xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -117,8 +132,8 @@ struct Lpb<T_Q6_K> {
   static constexpr int kBytes = 210;
   static constexpr bool kHasD = true;
   // value: sumi = sum_s sc_s * sum((u - 32) * q8); fold (y.d * d) * sumi   (mx_dot_k_ssse3.c:167-209)
-  template <int MAXM>
-  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
     uint32_t w[53];  // bytes 0..211: ql 0..127, qh 128..191, scales 192..207, d 208..209
     lds_words<53>(wb, off, w);
     int sumi[MAXM];
@@ -138,10 +153,10 @@ struct Lpb<T_Q6_K> {
 #pragma unroll
         for (int m = 0; m < MAXM; ++m) {
           if (m < M) {
-            const uint32_t bwd = *(const uint32_t*)(a[m].bsums + 8 * h + 2 * g);
+            const uint32_t bwd = a[m].bs2(4 * h + g);
 #pragma unroll
             for (int half16 = 0; half16 < 2; ++half16) {  // sub-block 8h + 2g + half16
-              const i32x4a4 x = *(const i32x4a4*)(a[m].q + 128 * h + 32 * g + 16 * half16);
+              const i32x4a4 x = a[m].q16(128 * h + 32 * g + 16 * half16);
               int sdot = 0;
               sdot = sdot4(U[4 * half16 + 0], (uint32_t)x.x, sdot);
               sdot = sdot4(U[4 * half16 + 1], (uint32_t)x.y, sdot);
@@ -167,8 +182,8 @@ struct Lpb<T_Q8_0> {
   static constexpr int kBytes = 272;  // eight 34-byte blocks
   static constexpr bool kHasD = false;
   // value: block_sum = sum_k d_k * sum(qs * q8) in k order (mx_dot_q8_0.c:8-18)
-  template <int MAXM>
-  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
     const uint8_t* blk = wb + off;  // 4-byte aligned
     float bs[MAXM];
 #pragma unroll
@@ -193,8 +208,8 @@ struct Lpb<T_Q8_0> {
 #pragma unroll
         for (int m = 0; m < MAXM; ++m) {
           if (m < M) {
-            const i32x4a4 x0 = *(const i32x4a4*)(a[m].q + 32 * k);
-            const i32x4a4 x1 = *(const i32x4a4*)(a[m].q + 32 * k + 16);
+            const i32x4a4 x0 = a[m].q16(32 * k);
+            const i32x4a4 x1 = a[m].q16(32 * k + 16);
             int p = 0;
             p = sdot4(qs[0], (uint32_t)x0.x, p);
             p = sdot4(qs[1], (uint32_t)x0.y, p);
@@ -224,8 +239,8 @@ struct Lpb<T_IQ4_XS> {
   // the order every IQ4_XS kernel here uses, so a token's result does not depend on the batch:
   // p = sequential fmaf over a sub-block's 16 low-nibble / 16 high-nibble elements four at a
   // time, quarters fmaf(dl1, p1, dl0 * p0), block (q0 + q1) + (q2 + q3), rows sum blocks in order
-  template <int MAXM>
-  __device__ static void compute(const uint8_t* wb, int off, const ActBlock* a, int M, float* V, float& D) {
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
     const uint8_t* blk = wb + off;  // 4-byte aligned
     uint32_t w[34];
 #pragma unroll
@@ -256,8 +271,8 @@ struct Lpb<T_IQ4_XS> {
             for (int i = 0; i < 4; ++i) {
               const uint32_t qw = w[2 + 4 * ib + i];
               const uint32_t gl = iq4_lookup4(qw & 0x0F0F0F0Fu), gh = iq4_lookup4((qw >> 4) & 0x0F0F0F0Fu);
-              const float4 xl = *(const float4*)(a[m].x + 32 * ib + 4 * i);
-              const float4 xh = *(const float4*)(a[m].x + 32 * ib + 16 + 4 * i);
+              const float4 xl = a[m].x4(32 * ib + 4 * i);
+              const float4 xh = a[m].x4(32 * ib + 16 + 4 * i);
               p[t] = fmaf(xl.x, sbyte_f<0>(gl), p[t]);
               p[t] = fmaf(xl.y, sbyte_f<1>(gl), p[t]);
               p[t] = fmaf(xl.z, sbyte_f<2>(gl), p[t]);
@@ -427,7 +442,7 @@ __global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict
         ablk[m].x = (const float*)(act_q + (mc * ab + b) * kActBlk);
       }
       float V[MAXM], D;
-      L::template compute<MAXM>(wreg, boff, ablk, M, V, D);
+      L::template compute<MAXM, ActBlock>(wreg, boff, ablk, M, V, D);
       if (lane < nrows * cb) {
 #pragma unroll
         for (int m = 0; m < MAXM; ++m)
@@ -648,10 +663,14 @@ __device__ __forceinline__ void stage_activations(const Act& act, int M, int aw,
   __syncthreads();  // second barrier: the activations are in LDS
 }
 
-template <int TYPE, int MAXM, bool FUSEQ>
-__global__ __launch_bounds__(1024) void gemv_pipe_kernel(const uint8_t* w, long long row_bytes,
+// ACTREG (one activation row, 64 % nb == 0): lane l's block of the row is l % nb in every stage,
+// so the lane keeps that block's Q8_K values in registers instead of reading LDS per stage.
+template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG>
+__global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long long row_bytes,
                                                          Act act, float* __restrict__ y,
                                                          long long ldy, int M, int N, PipeGeo geo) {
+  static_assert(!ACTREG || (MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0)),
+                "register activations: one Q8_K row, types whose compute leaves room for them");
   using L = Lpb<TYPE>;
   constexpr bool kFloatAct = TYPE == T_IQ4_XS;
   constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
@@ -710,6 +729,13 @@ __global__ __launch_bounds__(1024) void gemv_pipe_kernel(const uint8_t* w, long 
   const int step = 64 % nb;
   int b = lane % nb;
   const int lane_off = mis + (int)__umul24(lane, L::kBytes);
+  ActRegs areg;
+  if constexpr (ACTREG) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) areg.q[i] = *(const i32x4a4*)(act_q + b * kActBlk + 16 * i);
+    areg.bs[0] = *(const u32x4a4*)(act_bs + 16 * b);
+    areg.bs[1] = *(const u32x4a4*)(act_bs + 16 * b + 8);
+  }
   for (int s = 0; s < stages; ++s) {
     // copies issued after stage s: stages s + 1 .. min(s + P - 1, stages - 1)
     int after = 0;
@@ -733,7 +759,10 @@ __global__ __launch_bounds__(1024) void gemv_pipe_kernel(const uint8_t* w, long 
       ablk[m].x = (const float*)(act_q + row * kActBlk + aoff);
     }
     float V[MAXM], D;
-    L::template compute<MAXM>(wreg + (s % (P + 1)) * buf_bytes, boff, ablk, M, V, D);
+    if constexpr (ACTREG)  // lanes past the range end compute with their own block: never stored
+      L::template compute<1, ActRegs>(wreg + (s % (P + 1)) * buf_bytes, boff, &areg, 1, V, D);
+    else
+      L::template compute<MAXM, ActBlock>(wreg + (s % (P + 1)) * buf_bytes, boff, ablk, M, V, D);
     b += step;
     b = b >= nb ? b - nb : b;
     const int j = 64 * s + jl;
@@ -802,7 +831,7 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
     const bool persistent = mode < 2;
     P = mode % 2 == 0 ? 1 : 2;
     const int budget = (persistent ? kLdsMax : kLdsMax / 2) - act_lds;
-    for (nw = min(16 - na, 8); nw >= 2 && !ok; --nw) {
+    for (nw = 8; nw >= 2 && !ok; --nw) {  // nw + na <= 12 waves: the kernel's launch bound
       R = persistent ? (int)((N + (long long)ncu * nw - 1) / ((long long)ncu * nw)) : max(1, 512 / nb);
       ok = nw * wave_bytes(P, R) <= budget;
       if (ok) break;
@@ -815,10 +844,15 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   const int lds = act_lds + nw * wave_bytes(P, R);
   if (lds > kLdsMax) return -1;
   const int grid = (int)((N + (long long)nw * R - 1) / ((long long)nw * R));
-  auto kern = gemv_pipe_kernel<TYPE, MAXM, FUSEQ>;
-  static bool lds_set = false;
+  constexpr bool kRegOk = MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0);
+  const bool actreg = kRegOk && 64 % nb == 0;
+  auto kern = actreg ? gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk> : gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>;
+  static bool lds_set = false;  // both variants may be launched: allow the full LDS for each
   if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    (void)hipFuncSetAttribute((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    (void)hipFuncSetAttribute((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
     lds_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (nw + na)), lds, stream, w, row_bytes, act, y,
