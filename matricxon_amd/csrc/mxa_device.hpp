@@ -129,6 +129,7 @@ struct Act {
   const float* x;
   int k;
   int nb;
+  void* xsplit;  // IQ4_XS prefill: workspace for the bf16 split of x (nullptr when not provided)
 };
 
 // Grid-order tile index for workgroup `wg` of `n_wg` such that consecutive tiles land on the same

@@ -813,7 +813,7 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   if (nb > kWaveLanes) return -1;
   const int total = M * nb;
   const int act_lds = total * (kActBlk + 32 + 4) + 16;
-  if (act_lds > 48 * 1024) return -1;
+  if (act_lds > 80 * 1024) return -1;  // the rest of LDS must still hold 2+ waves' buffers
   const int na = min(4, (total + 15) / 16);
   const int ncu = cu_count();
   PipeGeo geo;

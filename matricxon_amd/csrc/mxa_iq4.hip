@@ -1,0 +1,166 @@
+// IQ4_XS prefill (M > 16) on the matrix cores.
+//
+// The reference multiplies fp32 activations by dl * K[q] (app/native/src/mx_dot_f32.c:32-58, K the
+// IQ4_NL grid, dl = d * (ls - 32) per 32-value sub-block). Here x is first split into two bf16
+// parts, x = hi + lo (hi = x rounded to bf16, lo = the rest rounded to bf16; relative error of the
+// pair about 2^-17), written to the workspace by split_bf16_kernel. The grid values are small
+// integers, exact in bf16, so v_mfma_f32_16x16x32_bf16 on (hi, K) then (lo, K) gives sum(K * x) of
+// one sub-block per MFMA pair: with A = x (16 activation rows x 32 k) and B = K (32 k x 16 weight
+// rows), lane l supplies row (l % 16) and k-group g = l / 16, i.e. elements 32 t + 8 g + (0..7) of
+// sub-block t. The sub-block scale dl is applied in fp32 after the MFMA. The result meets the
+// float tolerance against the reference (rel-L2 <= 1e-4); its summation order differs from the
+// decode kernels', which is why batches of up to 16 rows stay on those.
+#include "mxa_kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mxa {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte aligned
+
+constexpr int kRowsPerWg = 64;             // weight rows per workgroup (16 per wave)
+constexpr int kXStride = QK * 2 + 16;      // LDS bytes per activation row (bf16), padded
+
+// bf16 bits of x rounded to nearest even (NaN stays NaN, overflow gives +-Inf).
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict__ x,
+                                                         uint16_t* __restrict__ hi,
+                                                         uint16_t* __restrict__ lo, long long n4) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  const float4 v = ((const float4*)x)[i];
+  const float e[4] = {v.x, v.y, v.z, v.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    h[k] = bf16_rne(e[k]);
+    const float rest = e[k] - __builtin_bit_cast(float, h[k] << 16);  // exact in fp32
+    l[k] = bf16_rne(rest);
+  }
+  ((uint2*)hi)[i] = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  ((uint2*)lo)[i] = uint2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+}
+
+// Eight bf16 grid values (as four dwords) for the eight 4-bit indices in the low nibbles of the
+// bytes of (a, b).
+__device__ __forceinline__ u32x4a4 grid_bf16x8(uint32_t a, uint32_t b) {
+  const uint32_t ka = iq4_lookup4(a), kb = iq4_lookup4(b);
+  uint32_t f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = __builtin_bit_cast(uint32_t, (float)(int8_t)(uint8_t)(ka >> (8 * i)));
+    f[4 + i] = __builtin_bit_cast(uint32_t, (float)(int8_t)(uint8_t)(kb >> (8 * i)));
+  }
+  // bf16 = the top half of an fp32 holding a small integer (exact); two per dword
+  return u32x4a4{__builtin_amdgcn_perm(f[1], f[0], 0x07060302u), __builtin_amdgcn_perm(f[3], f[2], 0x07060302u),
+                 __builtin_amdgcn_perm(f[5], f[4], 0x07060302u), __builtin_amdgcn_perm(f[7], f[6], 0x07060302u)};
+}
+
+struct IQ4W {
+  uint32_t hdr[2];   // d | scales_h, scales_l
+  uint32_t qs[16];   // for sub-block t: qs[16 t + 8 (g & 1) ..] as two dwords
+};
+
+__device__ __forceinline__ IQ4W load_iq4(const uint8_t* row, int b, int g) {
+  const uint8_t* blk = row + (size_t)b * 136;  // 8-byte aligned blocks (4-byte aligned rows)
+  IQ4W L;
+  const u32x2a4 h = ld8(blk);
+  L.hdr[0] = h.x, L.hdr[1] = h.y;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const u32x2a4 v = ld8(blk + 8 + 16 * t + 8 * (g & 1));
+    L.qs[2 * t] = v.x, L.qs[2 * t + 1] = v.y;
+  }
+  return L;
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void iq4_mtile_kernel(const uint8_t* w, long long row_bytes,
+                                                        const uint16_t* __restrict__ xh,
+                                                        const uint16_t* __restrict__ xl, int K,
+                                                        float* __restrict__ y, long long ldy, int M,
+                                                        int N) {
+  constexpr int kRows = 16 * MT;
+  __shared__ __align__(16) uint8_t Xh[kRows * kXStride];
+  __shared__ __align__(16) uint8_t Xl[kRows * kXStride];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int ln = lane & 15, g = lane >> 4;
+  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * kRowsPerWg + 16 * wave;
+  const int m0 = blockIdx.y * kRows;
+  const uint8_t* row = w + (size_t)min(n0 + ln, N - 1) * row_bytes;
+  const int nb = K / QK;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  IQ4W cur = load_iq4(row, 0, g), nxt;
+  for (int b = 0; b < nb; ++b) {
+    // 1. the block's activations (bf16 hi / lo) into LDS; rows >= M repeat row M - 1
+    for (int p = tid; p < kRows * 64; p += 256) {  // 16-byte pieces: 32 per row of hi, 32 of lo
+      const int r = p >> 6, pc = p & 63, part = pc >> 5, q = pc & 31;
+      const size_t src = (size_t)min(m0 + r, M - 1) * K + (size_t)b * QK;
+      const uint16_t* sp = (part ? xl : xh) + src;
+      *(u32x4a4*)((part ? Xl : Xh) + r * kXStride + 16 * q) = ld16((const uint8_t*)sp + 16 * q);
+    }
+    if (b + 1 < nb) nxt = load_iq4(row, b + 1, g);
+    __syncthreads();
+    // 2. the block: per sub-block t, B = grid values of elements 32 t + 8 g .. of row n
+    const float d = half_to_float(cur.hdr[0]);
+    const uint32_t sh = cur.hdr[0] >> 16, sl = cur.hdr[1];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int ls = (int)(((sl >> (4 * t)) & 15u) | (((sh >> (2 * t)) & 3u) << 4));
+      const float dl = d * (float)(ls - 32);
+      const uint32_t q0 = cur.qs[2 * t], q1 = cur.qs[2 * t + 1];
+      const uint32_t i0 = (g >= 2 ? q0 >> 4 : q0) & 0x0F0F0F0Fu, i1 = (g >= 2 ? q1 >> 4 : q1) & 0x0F0F0F0Fu;
+      const bf16x8 bk = __builtin_bit_cast(bf16x8, grid_bf16x8(i0, i1));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int off = (16 * mt + ln) * kXStride + 2 * (32 * t + 8 * g);
+        const bf16x8 ah = __builtin_bit_cast(bf16x8, *(const u32x4*)(Xh + off));
+        const bf16x8 al = __builtin_bit_cast(bf16x8, *(const u32x4*)(Xl + off));
+        f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bk, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bk, D, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(dl, D[i], acc[mt][i]);
+      }
+    }
+    __syncthreads();
+    cur = nxt;
+  }
+  const int n = n0 + ln;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + 16 * mt + 4 * g + i;
+      if (m < M && n < N) y[(size_t)m * ldy + n] = acc[mt][i];
+    }
+}
+
+}  // namespace
+
+size_t iq4_prefill_workspace(int m_rows, int k) { return (size_t)m_rows * k * 2 * 2; }
+
+int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, void* workspace,
+                       float* y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream) {
+  uint16_t* hi = (uint16_t*)workspace;
+  uint16_t* lo = hi + (size_t)m_rows * k;
+  const long long n4 = (long long)m_rows * k / 4;
+  hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, x, hi,
+                     lo, n4);
+  constexpr int MT = 4;
+  const dim3 grid((n_rows + kRowsPerWg - 1) / kRowsPerWg, (m_rows + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL(iq4_mtile_kernel<MT>, grid, dim3(256), 0, stream, w, row_bytes, hi, lo, k, y,
+                     ldy, m_rows, n_rows);
+  return 0;
+}
+
+}  // namespace mxa

@@ -70,6 +70,13 @@ bool mtile_supported(int type);
 int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// IQ4_XS prefill on the matrix cores (m_rows >= kIq4MfmaMinRows): x split into bf16 hi / lo in
+// `workspace` (iq4_prefill_workspace bytes), then bf16 MFMAs per 32-value sub-block.
+constexpr int kIq4MfmaMinRows = 17;
+size_t iq4_prefill_workspace(int m_rows, int k);
+int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, void* workspace,
+                       float* y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream);
+
 // The matmul for any m_rows: picks the kernel (matrix-core decode, or the dot4 GEMV in passes of
 // up to 16 rows).
 int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,

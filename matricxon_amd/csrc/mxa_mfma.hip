@@ -244,9 +244,11 @@ int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& ac
     return launch_gemv_lpb(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
   if (act.q != nullptr && mtile_supported(type))
     return launch_mtile(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+  if (type == T_IQ4_XS && m_rows >= kIq4MfmaMinRows && act.xsplit != nullptr)
+    return launch_iq4_prefill(w, row_bytes, act.x, act.xsplit, y, ldy, m_rows, act.k, n_rows, stream);
   if (type == T_IQ4_XS) {
-    // float activations: the decode kernel in passes of kFusedQuantMaxRows rows (the one IQ4_XS
-    // summation order of every kernel here, so a row's result does not depend on the batch)
+    // float activations: the decode kernel in passes of kFusedQuantMaxRows rows (the summation
+    // order of the decode kernels, so a row's result does not depend on a batch of up to 16)
     for (int m0 = 0; m0 < m_rows; m0 += kFusedQuantMaxRows) {
       Act a = act;
       a.q = nullptr;

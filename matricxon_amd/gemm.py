@@ -190,7 +190,12 @@ class HipGemm:
         n_tokens = x32.shape[0]
         outs = [int(o) for _, _, o in items]
         y = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
-        ws_bytes = max(self.workspace_bytes(int(t), n_tokens, in_features) for t, _, _ in items)
+        # the Q8_K part and the IQ4_XS split part are separate regions of one workspace
+        need = {False: 0, True: 0}
+        for t, _, _ in items:
+            is_iq4 = int(t) == 23
+            need[is_iq4] = max(need[is_iq4], self.workspace_bytes(int(t), n_tokens, in_features))
+        ws_bytes = need[False] + need[True]
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
         n = len(items)
         types = (ctypes.c_int * n)(*[int(t) for t, _, _ in items])

@@ -60,6 +60,7 @@ def test_supports_and_sizes(lib) -> None:
     assert lib.mxa_workspace_bytes(12, 5, 256) == 1280 + 256 + 256
     assert lib.mxa_workspace_bytes(12, 4, 4096) == 0  # quantized inside the matmul kernel
     assert lib.mxa_workspace_bytes(23, 16, 4096) == 0  # IQ4_XS reads float activations
+    assert lib.mxa_workspace_bytes(23, 17, 4096) == 17 * 4096 * 4  # prefill: bf16 hi/lo of x
 
 
 def test_argument_errors_return_status_without_launching(lib) -> None:

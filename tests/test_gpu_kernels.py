@@ -224,3 +224,18 @@ def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> 
     got = host(gpu.matmul_q8k(ggml_type, dev(w), ws, None, out, m, n, k))
     want = oracle.gemm(ggml_type, w, host(x), n, k)
     assert np.array_equal(bits(got), bits(want))
+
+
+def test_gemm_multi_mixed_types_prefill(gpu, oracle) -> None:
+    """Q8_K-based and IQ4_XS weights sharing one prefill-sized input: the workspace holds both
+    the Q8_K activations and the bf16 split of x, and every output equals its separate call."""
+    k, m = 1024, 20
+    items = [(D.Q4_K, 48), (D.IQ4_XS, 32), (D.Q6_K, 16)]
+    ws = [dev(S.packed_weight(t, o, k, seed=40 + i)) for i, (t, o) in enumerate(items)]
+    x_np = S.activations(m, k, seed=12)
+    x = dev(x_np)
+    multi = gpu.matmul_multi([(t, w, o) for (t, o), w in zip(items, ws)], x)
+    for (t, o), w, y in zip(items, ws, multi):
+        assert torch.equal(y, gpu.matmul(t, w, x, o, k))
+        want = oracle.gemm(t, host(w), x_np, o, k)
+        assert_within_tolerance(host(y), want)
