@@ -67,8 +67,9 @@ size_t split_part(bool any_iq4, int n_tokens, int k) {
 extern "C" {
 
 const char* mxa_build_info(void) {
-  return "matricxon_amd gfx950: bit-exact dequant (Q8_0/Q4_K/Q6_K/IQ4_XS); dot4 GEMV with "
-         "in-kernel Q8_K quantization (M<=4); Q4_K int8-MFMA batched decode (M<=16)";
+  return "matricxon_amd gfx950: bit-exact dequant (Q8_0/Q4_K/Q6_K/IQ4_XS); decode (M<=4): "
+         "pipelined LDS-DMA GEMV with in-kernel Q8_K quantization; M>4: int8 MFMA tiles "
+         "(Q4_K/Q6_K/Q8_0), bf16 split MFMA prefill (IQ4_XS)";
 }
 
 int mxa_supports(int ggml_type, int in_features) {
@@ -127,8 +128,9 @@ int mxa_gemm_q8k(int ggml_type, const void* w, const float* x, float* y, int n_t
   }
   const mxa::Act act = make_act(x, abuf, in_features);
   const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
-  mxa::launch_matmul(ggml_type, (const uint8_t*)w, rb, act, y, out_features, n_tokens,
-                     out_features, (hipStream_t)stream);
+  if (mxa::launch_matmul(ggml_type, (const uint8_t*)w, rb, act, y, out_features, n_tokens,
+                         out_features, (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
   return check_launch();
 }
 
@@ -168,8 +170,9 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
   long long col = 0;
   for (int i = 0; i < n; ++i) {
     const long long rb = (long long)mxa_row_bytes(types[i], in_features);
-    mxa::launch_matmul(types[i], (const uint8_t*)ws[i], rb, act, y + col, total, n_tokens,
-                       outs[i], s);
+    if (mxa::launch_matmul(types[i], (const uint8_t*)ws[i], rb, act, y + col, total, n_tokens,
+                           outs[i], s) != 0)
+      return MXA_ERR_UNSUPPORTED;
     const int st = check_launch();
     if (st != MXA_OK) return st;
     col += outs[i];

@@ -47,22 +47,11 @@ int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long
 // Activation rows up to which the matmul kernels quantize x themselves (no workspace).
 constexpr int kFusedQuantMaxRows = 4;
 
-// y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of one packed weight. A K-quant or
-// Q8_0 weight with act.q == nullptr (only for m_rows <= kFusedQuantMaxRows) quantizes act.x in
-// the kernel.
-int launch_gemv(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
-                long long ldy, int m_rows, int n_rows, hipStream_t stream);
-
-// Decode GEMV for 1 <= m_rows <= 4 with lane-per-block compute on weight rows staged into LDS
-// by coalesced copies. Same contract as launch_gemv.
+// Decode GEMV for 1 <= m_rows <= 4: y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of
+// one packed weight, lane-per-block compute on weight rows staged into LDS by coalesced copies. A
+// K-quant or Q8_0 weight with act.q == nullptr quantizes act.x to Q8_K in the kernel.
 int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream);
-
-// Matrix-core kernel for batched decode: Q4_K, 1 <= m_rows <= 16, on Q8_K activations already
-// in the workspace.
-bool mfma_decode_supported(int type, int m_rows);
-int launch_mfma_decode(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
-                       long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Matrix-core kernel for m_rows > 4 (batched decode and prefill) on Q8_K activations already in
 // the workspace: Q4_K, Q6_K, Q8_0.
@@ -77,8 +66,7 @@ size_t iq4_prefill_workspace(int m_rows, int k);
 int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, void* workspace,
                        float* y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream);
 
-// The matmul for any m_rows: picks the kernel (matrix-core decode, or the dot4 GEMV in passes of
-// up to 16 rows).
+// The matmul for any m_rows: picks the kernel (mxa_dispatch.hip); -1 when no kernel applies.
 int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                   long long ldy, int m_rows, int n_rows, hipStream_t stream);
 

@@ -62,14 +62,26 @@ struct ActTile {
   int qs, bst;            // row strides (bytes, halves)
 };
 
-// ---------------------------------------------------------------------------------------- Q4_K
-struct Q4W {
-  u32x4a4 hdr, qa, qb;
-};
+// Every type provides: W (a lane's bytes of one weight tile's block) and load(); P = prep(W, g),
+// the B operands of that tile and block; F = frag(A, bb, mt, ln, g), the A operands of activation
+// tile mt (shared by all weight tiles of the wave); value(P, F, g, sink), which calls
+// sink(e, v, d) with the block value of m = 4 g + e of the tile, n = lane % 16; and fold(acc, xd,
+// v, d), the oracle's fold step.
 
-template <int MT>
+// ---------------------------------------------------------------------------------------- Q4_K
 struct TileQ4 {
-  using W = Q4W;
+  struct W {
+    u32x4a4 hdr, qa, qb;
+  };
+  struct P {
+    i32x4 bh[4], bl[4];  // planes of MFMA t: (sc >> 3) * u and (sc & 7) * u
+    f16x4 bmin;
+    float d, dmin;
+  };
+  struct F {
+    i32x4 a[4];
+    f16x4 bs;
+  };
   __device__ static W load(const uint8_t* row, int b, int g) {
     const uint8_t* blk = row + (size_t)b * 144;
     W L;
@@ -78,17 +90,15 @@ struct TileQ4 {
     L.qb = ld16_stream(blk + 32 + 32 * g);
     return L;
   }
-  // The block value of (m, n) and its fold step (mx_dot_k_ssse3.c:150-154).
   __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
-  // sink(mt, i, v, d) receives the block value of m = 16 mt + 4 g + i, n = lane % 16.
-  template <class S>
-  __device__ static void block(const W& L, const ActTile& A, int bb, int ln, int g, S&& sink) {
-    const float d = half_to_float(L.hdr.x), dmin = half_to_float(L.hdr.x >> 16);
+  __device__ static P prep(const W& L, int g) {
+    P p;
+    p.d = half_to_float(L.hdr.x);
+    p.dmin = half_to_float(L.hdr.x >> 16);
     const K4Scales s = k4_scales(L.hdr.y, L.hdr.z, L.hdr.w);
     const uint32_t sc0 = k4_pick(s.sc_lo, s.sc_hi, 2 * g), sc1 = k4_pick(s.sc_lo, s.sc_hi, 2 * g + 1);
     const uint32_t mn0 = k4_pick(s.mn_lo, s.mn_hi, 2 * g), mn1 = k4_pick(s.mn_lo, s.mn_hi, 2 * g + 1);
     const uint32_t q[8] = {L.qa.x, L.qa.y, L.qa.z, L.qa.w, L.qb.x, L.qb.y, L.qb.z, L.qb.w};
-    i32x4 bh[4], bl[4];  // planes of MFMA t: (sc >> 3) * u and (sc & 7) * u
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t sh = (t < 2 ? sc0 : sc1) >> 3, sl = (t < 2 ? sc0 : sc1) & 7;
@@ -97,40 +107,52 @@ struct TileQ4 {
       for (int i = 0; i < 4; ++i)
         u[i] = t == 0 ? q[i] & 0x0F0F0F0Fu : t == 1 ? q[4 + i] & 0x0F0F0F0Fu
              : t == 2 ? (q[i] >> 4) & 0x0F0F0F0Fu : (q[4 + i] >> 4) & 0x0F0F0F0Fu;
-      bh[t] = as_i32x4(mul_bytes(u[0], sh), mul_bytes(u[1], sh), mul_bytes(u[2], sh), mul_bytes(u[3], sh));
-      bl[t] = as_i32x4(mul_bytes(u[0], sl), mul_bytes(u[1], sl), mul_bytes(u[2], sl), mul_bytes(u[3], sl));
+      p.bh[t] = as_i32x4(mul_bytes(u[0], sh), mul_bytes(u[1], sh), mul_bytes(u[2], sh), mul_bytes(u[3], sh));
+      p.bl[t] = as_i32x4(mul_bytes(u[0], sl), mul_bytes(u[1], sl), mul_bytes(u[2], sl), mul_bytes(u[3], sl));
     }
     const _Float16 m0 = (_Float16)(float)mn0, m1 = (_Float16)(float)mn1;
-    const f16x4 bmin = {m0, m0, m1, m1};
+    p.bmin = f16x4{m0, m0, m1, m1};
+    return p;
+  }
+  __device__ static F frag(const ActTile& A, int bb, int mt, int ln, int g) {
+    F f;
+    const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 64 * g;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 64 * g;
-      i32x4 a[4];
+    for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
+    f.bs = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
+    return f;
+  }
+  template <class S>
+  __device__ static void value(const P& p, const F& f, int, S&& sink) {
+    i32x4 sum = {0, 0, 0, 0};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
-      i32x4 sum = {0, 0, 0, 0};
+    for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bh[t], sum, 0, 0, 0);
+    sum = sum * 8;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bh[t], sum, 0, 0, 0);
-      sum = sum * 8;
+    for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bl[t], sum, 0, 0, 0);
+    // summ = sum over the 16 bsums of min_{s/2} * bsum: A = bsums (k = 4g..4g+3), B = mins
+    const f32x4 summ = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bmin, f32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bl[t], sum, 0, 0, 0);
-      const f16x4 amin = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
-      const f32x4 summ = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, bmin, f32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sink(mt, i, fmaf(d, (float)sum[i], -(dmin * summ[i])), 0.0f);
-    }
+    for (int i = 0; i < 4; ++i) sink(i, fmaf(p.d, (float)sum[i], -(p.dmin * summ[i])), 0.0f);
   }
 };
 
 // ---------------------------------------------------------------------------------------- Q6_K
-struct Q6W {
-  u32x4a4 qla, qlb, qh, sc;  // ql[64h + 16q ..], ql[64h + 32 + 16q ..], qh[32h + 16q ..], scales
-  uint32_t d;
-};
-
-template <int MT>
 struct TileQ6 {
-  using W = Q6W;
+  struct W {
+    u32x4a4 qla, qlb, qh, sc;  // ql[64h + 16q ..], ql[64h + 32 + 16q ..], qh[32h + 16q ..], scales
+    uint32_t d;
+  };
+  struct P {
+    u32x4a4 bu[4];  // codes u of MFMA t (elements 128 h + 32 t + 16 q + j)
+    int scv[4][4];  // scale of the sub-block of (MFMA t, lane group g2), row n
+    f16x4 bsc;      // scales 4 g .. 4 g + 3 of row n (the bsums term)
+    float d;
+  };
+  struct F {
+    i32x4 a[4];
+    f16x4 bs;
+  };
   // 16 bytes at p, 2-byte aligned at worst (210-byte blocks): dword loads + v_alignbyte. The fifth
   // dword is read only when p is not 4-byte aligned, so no byte past p + 15 is touched.
   __device__ static u32x4a4 ld16_a2(const uint8_t* p) {
@@ -155,70 +177,73 @@ struct TileQ6 {
   }
   // block value sumi (as float) with the block's d; fold (xd * d) * sumi (mx_dot_k_ssse3.c:200-206)
   __device__ static float fold(float acc, float xd, float v, float d) { return fmaf(xd * d, v, acc); }
-  template <class S>
-  __device__ static void block(const W& L, const ActTile& A, int bb, int ln, int g, S&& sink) {
-    const float d = half_to_float(L.d);
+  __device__ static P prep(const W& L, int g) {
+    P p;
+    p.d = half_to_float(L.d);
     const uint32_t la[4] = {L.qla.x, L.qla.y, L.qla.z, L.qla.w};
     const uint32_t lb[4] = {L.qlb.x, L.qlb.y, L.qlb.z, L.qlb.w};
     const uint32_t hh[4] = {L.qh.x, L.qh.y, L.qh.z, L.qh.w};
     const uint32_t scw[4] = {L.sc.x, L.sc.y, L.sc.z, L.sc.w};
-    // B of MFMA t (codes of elements 128 h + 32 t + 16 q + j), then one copy per lane group g2
-    // that is zero outside lane group g2
-    u32x4a4 bu[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      bu[0][i] = q6_codes<0>(la[i], hh[i]);
-      bu[1][i] = q6_codes<1>(lb[i], hh[i]);
-      bu[2][i] = q6_codes<2>(la[i], hh[i]);
-      bu[3][i] = q6_codes<3>(lb[i], hh[i]);
+      p.bu[0][i] = q6_codes<0>(la[i], hh[i]);
+      p.bu[1][i] = q6_codes<1>(lb[i], hh[i]);
+      p.bu[2][i] = q6_codes<2>(la[i], hh[i]);
+      p.bu[3][i] = q6_codes<3>(lb[i], hh[i]);
     }
-    // scales of row n = lane % 16 for sub-block 8 h + 2 t + q, by (t, g2)
-    int scv[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int g2 = 0; g2 < 4; ++g2) {
         const int sub = 8 * (g2 >> 1) + 2 * t + (g2 & 1);
-        scv[t][g2] = (int)(int8_t)(uint8_t)(scw[sub >> 2] >> (8 * (sub & 3)));
+        p.scv[t][g2] = (int)(int8_t)(uint8_t)(scw[sub >> 2] >> (8 * (sub & 3)));
       }
-    // C = sum over the 16 sub-blocks of bsums(m) * sc(n): A = bsums 4 g.. of row m, B = scales
-    // 4 g.. of row n (sub-block s = 4 g + e)
     const uint32_t sw = scw[g];
-    const f16x4 bsc = {(_Float16)(float)(int8_t)(sw & 0xFF), (_Float16)(float)(int8_t)((sw >> 8) & 0xFF),
-                       (_Float16)(float)(int8_t)((sw >> 16) & 0xFF), (_Float16)(float)(int8_t)(sw >> 24)};
+    p.bsc = f16x4{(_Float16)(float)(int8_t)(sw & 0xFF), (_Float16)(float)(int8_t)((sw >> 8) & 0xFF),
+                  (_Float16)(float)(int8_t)((sw >> 16) & 0xFF), (_Float16)(float)(int8_t)(sw >> 24)};
+    return p;
+  }
+  __device__ static F frag(const ActTile& A, int bb, int mt, int ln, int g) {
+    F f;
+    const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 128 * (g >> 1) + 16 * (g & 1);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 128 * (g >> 1) + 16 * (g & 1);
-      int sumi[4] = {0, 0, 0, 0};
+    for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 32 * t));
+    f.bs = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
+    return f;
+  }
+  template <class S>
+  __device__ static void value(const P& p, const F& f, int g, S&& sink) {
+    int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const i32x4 a = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 32 * t));
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int g2 = 0; g2 < 4; ++g2) {
-          const bool on = g == g2;
-          const i32x4 b = as_i32x4(on ? bu[t].x : 0u, on ? bu[t].y : 0u, on ? bu[t].z : 0u, on ? bu[t].w : 0u);
-          const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
-          // |D| <= 16 * 63 * 127 < 2^17, |sc| <= 128: 24-bit products
+      for (int g2 = 0; g2 < 4; ++g2) {
+        const bool on = g == g2;  // B restricted to lane group g2: one sub-block's dot
+        const i32x4 b = as_i32x4(on ? p.bu[t].x : 0u, on ? p.bu[t].y : 0u, on ? p.bu[t].z : 0u, on ? p.bu[t].w : 0u);
+        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+        // |D| <= 16 * 63 * 127 < 2^17, |sc| <= 128: 24-bit products
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scv[t][g2], D[i]);
-        }
+        for (int i = 0; i < 4; ++i) sumi[i] += __mul24(p.scv[t][g2], D[i]);
       }
-      const f16x4 abs_ = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
-      const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x16f16(abs_, bsc, f32x4{0, 0, 0, 0}, 0, 0, 0);
+    // C = sum over the 16 sub-blocks of bsums(m) * sc(n), exact (|C| < 2^22)
+    const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bsc, f32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sink(mt, i, (float)(sumi[i] - 32 * (int)C[i]), d);  // C exact (< 2^22)
-    }
+    for (int i = 0; i < 4; ++i) sink(i, (float)(sumi[i] - 32 * (int)C[i]), p.d);
   }
 };
 
 // ---------------------------------------------------------------------------------------- Q8_0
-struct Q8W {
-  uint32_t w[17];  // bytes 68 g .. 68 g + 67 of the 272-byte group: blocks 2 g and 2 g + 1
-};
-
-template <int MT>
 struct TileQ8 {
-  using W = Q8W;
+  struct W {
+    uint32_t w[17];  // bytes 68 g .. 68 g + 67 of the 272-byte group: blocks 2 g and 2 g + 1
+  };
+  struct P {
+    u32x4a4 qb[4];  // quants of MFMA t: block 2 g + t / 2, elements 16 (t % 2) ..
+    float dk[8];    // d of the 8 blocks of row n
+  };
+  struct F {
+    i32x4 a[4];
+  };
   __device__ static W load(const uint8_t* row, int b, int g) {
     const uint8_t* p = row + (size_t)b * 272 + 68 * g;  // 4-byte aligned
     W L;
@@ -232,140 +257,214 @@ struct TileQ8 {
   }
   // block value sum_k d_k * p_k in k order; fold xd * value (mx_dot_q8_0.c:8-18)
   __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
-  template <class S>
-  __device__ static void block(const W& L, const ActTile& A, int bb, int ln, int g, S&& sink) {
-    // quants of MFMA t: block 2 g + t / 2, elements 16 (t % 2) ..
-    u32x4a4 qb[4];
+  __device__ static P prep(const W& L, int g) {
+    P p;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      qb[0][i] = __builtin_amdgcn_alignbyte(L.w[i + 1], L.w[i], 2);
-      qb[1][i] = __builtin_amdgcn_alignbyte(L.w[i + 5], L.w[i + 4], 2);
-      qb[2][i] = L.w[9 + i];
-      qb[3][i] = L.w[13 + i];
+      p.qb[0][i] = __builtin_amdgcn_alignbyte(L.w[i + 1], L.w[i], 2);
+      p.qb[1][i] = __builtin_amdgcn_alignbyte(L.w[i + 5], L.w[i + 4], 2);
+      p.qb[2][i] = L.w[9 + i];
+      p.qb[3][i] = L.w[13 + i];
     }
-    // d of the 8 blocks of row n: this lane holds blocks 2 g and 2 g + 1; lane n + 16 g2 holds 2 g2..
+    // this lane holds the d of blocks 2 g and 2 g + 1; lane n + 16 g2 holds those of 2 g2..
+    const int ln = (int)(__lane_id() & 15);
     const uint32_t mine = (L.w[0] & 0xFFFFu) | (L.w[8] & 0xFFFF0000u);
-    float dk[8];
 #pragma unroll
     for (int g2 = 0; g2 < 4; ++g2) {
       const uint32_t v = (uint32_t)__shfl((int)mine, ln + 16 * g2, 64);
-      dk[2 * g2] = half_to_float(v);
-      dk[2 * g2 + 1] = half_to_float(v >> 16);
+      p.dk[2 * g2] = half_to_float(v);
+      p.dk[2 * g2 + 1] = half_to_float(v >> 16);
     }
+    (void)g;
+    return p;
+  }
+  __device__ static F frag(const ActTile& A, int bb, int mt, int ln, int g) {
+    F f;
+    const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 64 * g;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 64 * g;
-      i32x4 a[4];
+    for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
+    return f;
+  }
+  template <class S>
+  __device__ static void value(const P& p, const F& f, int g, S&& sink) {
+    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
-      float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < 8; ++k) {  // block k = 2 g2 + h: MFMAs t = 2 h, 2 h + 1 of lane group g2
+      const int g2 = k >> 1, h = k & 1;
+      const bool on = g == g2;
+      i32x4 D = {0, 0, 0, 0};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {  // block k = 2 g2 + h: MFMAs t = 2 h, 2 h + 1 of lane group g2
-        const int g2 = k >> 1, h = k & 1;
-        const bool on = g == g2;
-        i32x4 D = {0, 0, 0, 0};
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int t = 2 * h + tt;
-          const i32x4 b = as_i32x4(on ? qb[t].x : 0u, on ? qb[t].y : 0u, on ? qb[t].z : 0u, on ? qb[t].w : 0u);
-          D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b, D, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) bs[i] = fmaf(dk[k], (float)D[i], bs[i]);
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 2 * h + tt;
+        const i32x4 b = as_i32x4(on ? p.qb[t].x : 0u, on ? p.qb[t].y : 0u, on ? p.qb[t].z : 0u, on ? p.qb[t].w : 0u);
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], b, D, 0, 0, 0);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sink(mt, i, bs[i], 0.0f);
+      for (int i = 0; i < 4; ++i) bs[i] = fmaf(p.dk[k], (float)D[i], bs[i]);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sink(i, bs[i], 0.0f);
   }
 };
 
-template <int TYPE, int MT>
+template <int TYPE>
 struct TileOf;
-template <int MT> struct TileOf<T_Q4_K, MT> { using T = TileQ4<MT>; };
-template <int MT> struct TileOf<T_Q6_K, MT> { using T = TileQ6<MT>; };
-template <int MT> struct TileOf<T_Q8_0, MT> { using T = TileQ8<MT>; };
+template <> struct TileOf<T_Q4_K> { using T = TileQ4; };
+template <> struct TileOf<T_Q6_K> { using T = TileQ6; };
+template <> struct TileOf<T_Q8_0> { using T = TileQ8; };
 
-template <int TYPE, int MT>
+// Row-tiled kernel: MT activation tiles x NT weight tiles of 16 rows per wave, 4 waves.
+template <int TYPE, int MT, int NT>
 __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long row_bytes, Act act,
                                                     float* __restrict__ y, long long ldy, int M, int N) {
-  using Tile = typename TileOf<TYPE, MT>::T;
+  using Tile = typename TileOf<TYPE>::T;
   using W = typename Tile::W;
   constexpr int kRows = 16 * MT;
   __shared__ __align__(16) int8_t Aq[kRows * kQStride];
   __shared__ __align__(16) _Float16 Ab[kRows * kBStride];
   __shared__ __align__(16) float Ad[kCB * kRows];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = blockDim.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ln = lane & 15, g = lane >> 4;
-  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * (nthr >> 2) + 16 * wave;  // 16 rows per wave
+  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * 4 * 16 * NT + 16 * NT * wave;
   const int m0 = blockIdx.y * kRows;
-  const uint8_t* row = w + (size_t)min(n0 + ln, N - 1) * row_bytes;
+  const uint8_t* row[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) row[nt] = w + (size_t)min(n0 + 16 * nt + ln, N - 1) * row_bytes;
   const int nb = act.nb;
-  float acc[MT][4];
+  float acc[MT][NT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
-
-  W cur[kCB], nxt[kCB];
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-  for (int i = 0; i < kCB; ++i) cur[i] = Tile::load(row, min(i, nb - 1), g);
+      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
 
+  W cur[NT], nxt[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) cur[nt] = Tile::load(row[nt], 0, g);
+
+  // Activation staging, software-pipelined: chunk c + 1 is loaded into registers while chunk c
+  // is computed, and written to LDS between the two barriers. Thread tid owns the same pieces of
+  // every chunk (rows >= M repeat row M - 1, blocks >= cn repeat the chunk's last block: those
+  // results are never stored).
+  constexpr int kQPieces = kRows * kCB * 16;                   // 16-byte pieces of q8
+  constexpr int kQPer = (kQPieces + 255) / 256;
+  constexpr int kBPieces = kRows * kCB * 2;                    // halves of a block's 16 bsums
+  constexpr int kBPer = (kBPieces + 255) / 256;
+  constexpr int kDPer = (kRows * kCB + 255) / 256;
+  struct Stage {
+    u32x4a4 q[kQPer];
+    u32x4a4 b[kBPer];
+    float d[kDPer];
+  };
+  auto load_stage = [&](int c0) {
+    Stage st;
+    const int cn = min(kCB, nb - c0);
+#pragma unroll
+    for (int j = 0; j < kQPer; ++j) {
+      const int p = min(tid + 256 * j, kQPieces - 1);
+      const int r = p / (kCB * 16), o = p - r * (kCB * 16), bb = min(o >> 4, cn - 1), pc = o & 15;
+      st.q[j] = ld16((const uint8_t*)(act.q + (size_t)min(m0 + r, M - 1) * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
+    }
+#pragma unroll
+    for (int j = 0; j < kBPer; ++j) {
+      const int p = min(tid + 256 * j, kBPieces - 1);
+      const int r = p / (kCB * 2), o = p - r * (kCB * 2), bb = min(o >> 1, cn - 1), hf = o & 1;
+      st.b[j] = ld16((const uint8_t*)(act.bsums + ((size_t)min(m0 + r, M - 1) * nb + c0 + bb) * 16) + 16 * hf);
+    }
+#pragma unroll
+    for (int j = 0; j < kDPer; ++j) {
+      const int p = min(tid + 256 * j, kRows * kCB - 1), bb = p / kRows, r = p - bb * kRows;
+      st.d[j] = act.d[(size_t)min(m0 + r, M - 1) * nb + c0 + min(bb, cn - 1)];
+    }
+    return st;
+  };
+  auto store_stage = [&](const Stage& st) {
+#pragma unroll
+    for (int j = 0; j < kQPer; ++j) {
+      const int p = tid + 256 * j;
+      if (p < kQPieces) {
+        const int r = p / (kCB * 16), o = p - r * (kCB * 16);
+        *(u32x4a4*)(Aq + r * kQStride + (o >> 4) * QK + 16 * (o & 15)) = st.q[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBPer; ++j) {
+      const int p = tid + 256 * j;
+      if (p < kBPieces) {  // bsums as fp16 (exact: |.| <= 2032)
+        const int r = p / (kCB * 2), o = p - r * (kCB * 2);
+        const uint32_t wv[4] = {st.b[j].x, st.b[j].y, st.b[j].z, st.b[j].w};
+        f16x8 hv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hv[2 * i] = (_Float16)(float)(int16_t)(wv[i] & 0xFFFFu);
+          hv[2 * i + 1] = (_Float16)(float)(int16_t)(wv[i] >> 16);
+        }
+        *(f16x8*)(Ab + r * kBStride + (o >> 1) * 16 + 8 * (o & 1)) = hv;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kDPer; ++j) {
+      const int p = tid + 256 * j;
+      if (p < kRows * kCB) Ad[p] = st.d[j];
+    }
+  };
+
+  static_assert(4 * 64 == 256, "four waves");
+  {
+    const Stage st0 = load_stage(0);
+    store_stage(st0);
+  }
+  __syncthreads();
   for (int c0 = 0; c0 < nb; c0 += kCB) {
     const int cn = min(kCB, nb - c0);
-    // 1. the chunk's activations into LDS (rows >= M repeat row M - 1, blocks >= cn repeat the
-    //    last block: those results are never stored)
-    constexpr int kPieces = kRows * kCB * 16;  // 16-byte pieces of q8
-    for (int p = tid; p < kPieces; p += nthr) {
-      const int r = p / (kCB * 16), o = p - r * (kCB * 16), bb = min(o >> 4, cn - 1), pc = o & 15;
-      const int mr = min(m0 + r, M - 1);
-      *(u32x4a4*)(Aq + r * kQStride + (o >> 4) * QK + 16 * pc) =
-          ld16((const uint8_t*)(act.q + (size_t)mr * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
-    }
-    for (int p = tid; p < kRows * kCB * 2; p += nthr) {  // bsums as fp16 (exact: |.| <= 2032)
-      const int r = p / (kCB * 2), o = p - r * (kCB * 2), bb = min(o >> 1, cn - 1), hf = o & 1;
-      const int mr = min(m0 + r, M - 1);
-      const u32x4a4 v = ld16((const uint8_t*)(act.bsums + ((size_t)mr * nb + c0 + bb) * 16) + 16 * hf);
-      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-      f16x8 hv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        hv[2 * i] = (_Float16)(float)(int16_t)(wv[i] & 0xFFFFu);
-        hv[2 * i + 1] = (_Float16)(float)(int16_t)(wv[i] >> 16);
-      }
-      *(f16x8*)(Ab + r * kBStride + (o >> 1) * 16 + 8 * hf) = hv;
-    }
-    for (int p = tid; p < kRows * kCB; p += nthr) {
-      const int bb = p / kRows, r = p - bb * kRows;
-      Ad[p] = act.d[(size_t)min(m0 + r, M - 1) * nb + c0 + min(bb, cn - 1)];
-    }
-    // 2. weights of the next chunk
-    const int c1 = c0 + kCB;
-    if (c1 < nb) {
-#pragma unroll
-      for (int i = 0; i < kCB; ++i) nxt[i] = Tile::load(row, min(c1 + i, nb - 1), g);
-    }
-    __syncthreads();
-    // 3. the chunk's blocks, folded in order
+    const bool more = c0 + kCB < nb;
+    Stage st;
+    if (more) st = load_stage(c0 + kCB);
+    // the chunk's blocks in order; the next block's weights load meanwhile
     const ActTile A{Aq, Ab, kQStride, kBStride};
 #pragma unroll
-    for (int i = 0; i < kCB; ++i)
-      if (i < cn)
-        Tile::block(cur[i], A, i, ln, g, [&](int mt, int e, float v, float dd) {
-          acc[mt][e] = Tile::fold(acc[mt][e], Ad[i * kRows + 16 * mt + 4 * g + e], v, dd);
-        });
-    __syncthreads();
+    for (int i = 0; i < kCB; ++i) {
+      if (i < cn) {
+        const int b = c0 + i;
+        if (b + 1 < nb) {
 #pragma unroll
-    for (int i = 0; i < kCB; ++i) cur[i] = nxt[i];
-  }
-  const int n = n0 + ln;
+          for (int nt = 0; nt < NT; ++nt) nxt[nt] = Tile::load(row[nt], b + 1, g);
+        }
+        typename Tile::P pp[NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+        for (int nt = 0; nt < NT; ++nt) pp[nt] = Tile::prep(cur[nt], g);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + 16 * mt + 4 * g + i;
-      if (m < M && n < N) y[(size_t)m * ldy + n] = acc[mt][i];
+        for (int mt = 0; mt < MT; ++mt) {
+          const typename Tile::F f = Tile::frag(A, i, mt, ln, g);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            Tile::value(pp[nt], f, g, [&](int e, float v, float dd) {
+              acc[mt][nt][e] = Tile::fold(acc[mt][nt][e], Ad[i * kRows + 16 * mt + 4 * g + e], v, dd);
+            });
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) cur[nt] = nxt[nt];
+      }
     }
+    __syncthreads();  // every wave is done with this chunk's LDS
+    if (more) {
+      store_stage(st);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = n0 + 16 * nt + ln;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mt + 4 * g + i;
+        if (m < M && n < N) y[(size_t)m * ldy + n] = acc[mt][nt][i];
+      }
+  }
 }
 
 // Batched decode (M <= 16): 32 weight rows per workgroup and the blocks of each chunk split over
@@ -380,7 +479,7 @@ constexpr int kDecBStride = kDecCh * 16 + 8;
 template <int TYPE>
 __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long row_bytes, Act act,
                                                    float* __restrict__ y, long long ldy, int M, int N) {
-  using Tile = typename TileOf<TYPE, 1>::T;
+  using Tile = typename TileOf<TYPE>::T;
   using W = typename Tile::W;
   __shared__ __align__(16) int8_t Aq[16 * kDecQStride];
   __shared__ __align__(16) _Float16 Ab[16 * kDecBStride];
@@ -446,12 +545,15 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
     for (int i = 0; i < 2; ++i) {
       const int bb = wave + 4 * i;
       if (bb < cn) {
+        const typename Tile::F f = Tile::frag(A, bb, 0, ln, g);
 #pragma unroll
-        for (int t = 0; t < kDecRT; ++t)
-          Tile::block(cur[i][t], A, bb, ln, g, [&](int, int e, float v, float dd) {
+        for (int t = 0; t < kDecRT; ++t) {
+          const typename Tile::P pp = Tile::prep(cur[i][t], g);
+          Tile::value(pp, f, g, [&](int e, float v, float dd) {
             Tp[t][bb][4 * g + e][ln] = v;
             if (g == 0 && e == 0) Dp[t][bb][ln] = dd;
           });
+        }
       }
     }
     __syncthreads();
@@ -476,14 +578,13 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
   }
 }
 
-template <int TYPE, int MT>
+template <int TYPE, int MT, int NT>
 int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
               int N, hipStream_t stream) {
-  const int gy = (M + 16 * MT - 1) / (16 * MT);
-  constexpr int waves = 4;
-  const dim3 grid((N + 16 * waves - 1) / (16 * waves), gy);
-  hipLaunchKernelGGL((mtile_kernel<TYPE, MT>), grid, dim3(64 * waves), 0, stream, w, row_bytes, act,
-                     y, ldy, M, N);
+  const int rows = 4 * 16 * NT;
+  const dim3 grid((N + rows - 1) / rows, (M + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL((mtile_kernel<TYPE, MT, NT>), grid, dim3(256), 0, stream, w, row_bytes, act, y,
+                     ldy, M, N);
   return 0;
 }
 
@@ -496,9 +597,11 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
     hipLaunchKernelGGL(mdec_kernel<TYPE>, dim3(tiles), dim3(256), 0, stream, w, row_bytes, act, y, ldy, M, N);
     return 0;
   }
-  // up to 64 rows: 16-row activation tiles; prefill: 64-row tiles
-  if (M <= 64) return launch_mt<TYPE, 1>(w, row_bytes, act, y, ldy, M, N, stream);
-  return launch_mt<TYPE, 4>(w, row_bytes, act, y, ldy, M, N, stream);
+  // up to 64 rows: 16-row activation tiles; prefill: 64 activation rows x (Q4_K) 128 weight rows
+  // per workgroup; Q6_K / Q8_0 keep 64 weight rows (their B operands need twice the registers)
+  if (M <= 64) return launch_mt<TYPE, 1, 1>(w, row_bytes, act, y, ldy, M, N, stream);
+  constexpr int NT = 1;
+  return launch_mt<TYPE, 4, NT>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
 }  // namespace
