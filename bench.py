@@ -170,6 +170,13 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
         wb = sum(n * row_bytes(t, k) for t, n, k in layer)
         report(f"cfg4 llama3-8b layer (7 projections) M={m}", _graph_us(layer_step, steps, warmup),
                wb, 2.0 * m * sum(n * k for _, n, k in layer))
+        names = ["q", "k", "v", "o", "gate", "up", "down"]
+        for j, (t, n, k) in enumerate(layer):
+            if names[j] in ("k", "up"):  # same shapes as v (size) / gate
+                continue
+            us = _graph_us(lambda i: gemm.matmul(t, lw[j][i % 2], xs[k], n, k, out=ys[j]), steps, warmup)
+            report(f"cfg4   {names[j]} {'Q4_K' if t == 12 else 'Q6_K'} {n}x{k} M={m}", us,
+                   n * row_bytes(t, k), 2.0 * m * n * k)
     del lw
     for t, name, n in ((12, "cfg5 Q4_K 14336x4096", 14336), (23, "cfg5 IQ4_XS 4096x4096", 4096)):
         w = torch.from_numpy(S.packed_weight(t, n, 4096, seed=60 + t)).to(dev)

@@ -49,6 +49,19 @@ __device__ __forceinline__ float quad_sum(float v) {
   v += __builtin_bit_cast(float, quad_xor1(__builtin_bit_cast(int, v)));
   return v + __builtin_bit_cast(float, quad_xor2(__builtin_bit_cast(int, v)));
 }
+// Maximum over the 16 lanes of a DPP row (lanes 16r..16r+15): quad butterflies, then the
+// half-row and row mirrors. fmaxf ignores a NaN operand.
+__device__ __forceinline__ float max16(float v) {
+#define MXA_DPP_MAX(ctrl) \
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)))
+  MXA_DPP_MAX(0xB1);
+  MXA_DPP_MAX(0x4E);
+  MXA_DPP_MAX(0x141);
+  MXA_DPP_MAX(0x140);
+#undef MXA_DPP_MAX
+  return v;
+}
+
 // Value of lane (quad base + i) broadcast to the whole quad.
 template <int I>
 __device__ __forceinline__ int quad_bcast(int v) {

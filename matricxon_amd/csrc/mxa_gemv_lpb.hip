@@ -293,18 +293,6 @@ struct Lpb<T_IQ4_XS> {
   __device__ static float fold(float acc, float, float v, float) { return acc + v; }
 };
 
-// 16-lane maximum (lanes 16g..16g+15): quad butterflies, then the half-row and row mirrors.
-__device__ __forceinline__ float max16(float v) {
-#define MXA_DPP_MAX(ctrl) \
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)))
-  MXA_DPP_MAX(0xB1);
-  MXA_DPP_MAX(0x4E);
-  MXA_DPP_MAX(0x141);
-  MXA_DPP_MAX(0x140);
-#undef MXA_DPP_MAX
-  return v;
-}
-
 // LDS layout of a workgroup (dynamic shared memory):
 //   [act]  per activation row m and staged block bb: 256 q8 + kActPad | ... then bsums (32 B each)
 //          and scales (4 B each); IQ4_XS: 1024 B of floats + kActPad per block

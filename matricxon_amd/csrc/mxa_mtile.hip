@@ -471,12 +471,13 @@ __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long 
 // the 4 waves (wave w takes blocks w and w + 4 of an 8-block chunk, for both 16-row tiles), so that
 // N = 4096..14336 still gives the GPU 128..448 workgroups. The block values go through LDS and are
 // folded in block order by the thread that owns the output.
-constexpr int kDecRT = 2;                     // 16-row weight tiles per workgroup
 constexpr int kDecCh = 8;                     // blocks per chunk
 constexpr int kDecQStride = kDecCh * QK + 16;
 constexpr int kDecBStride = kDecCh * 16 + 8;
 
-template <int TYPE>
+// kDecRT 16-row weight tiles per workgroup: 2, or 1 for Q6_K (its per-lane block bytes need twice
+// the registers; one tile keeps two waves per SIMD).
+template <int TYPE, int kDecRT>
 __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long row_bytes, Act act,
                                                    float* __restrict__ y, long long ldy, int M, int N) {
   using Tile = typename TileOf<TYPE>::T;
@@ -494,7 +495,10 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
 #pragma unroll
   for (int t = 0; t < kDecRT; ++t) rows[t] = w + (size_t)min(n0 + 16 * t + ln, N - 1) * row_bytes;
   const int nb = act.nb;
-  float acc[2] = {0.0f, 0.0f};
+  constexpr int kOut = kDecRT * 256 / 256;  // outputs per thread: kDecRT tiles x 16 x 16 / 256
+  float acc[kOut];
+#pragma unroll
+  for (int k = 0; k < kOut; ++k) acc[k] = 0.0f;
 
   W cur[2][kDecRT], nxt[2][kDecRT];
   {
@@ -559,7 +563,7 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
     __syncthreads();
     // 4. fold the chunk's blocks in order: thread -> outputs (tile, m, n)
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < kOut; ++k) {
       const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15, n = idx & 15;
       for (int bb = 0; bb < cn; ++bb) acc[k] = Tile::fold(acc[k], Ad[bb * 16 + m], Tp[t][bb][m][n], Dp[t][bb][n]);
     }
@@ -572,7 +576,7 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
     }
   }
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < kOut; ++k) {
     const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15, n = n0 + 16 * t + (idx & 15);
     if (m < M && n < N) y[(size_t)m * ldy + n] = acc[k];
   }
@@ -593,8 +597,9 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
                    int M, int N, hipStream_t stream) {
   // M <= 16: the block-split kernel unless the 64-row tiles alone give >= 512 workgroups
   if (M <= 16 && N < 512 * 64) {
-    const int tiles = (N + 16 * kDecRT - 1) / (16 * kDecRT);
-    hipLaunchKernelGGL(mdec_kernel<TYPE>, dim3(tiles), dim3(256), 0, stream, w, row_bytes, act, y, ldy, M, N);
+    constexpr int RT = TYPE == T_Q6_K ? 1 : 2;
+    const int tiles = (N + 16 * RT - 1) / (16 * RT);
+    hipLaunchKernelGGL((mdec_kernel<TYPE, RT>), dim3(tiles), dim3(256), 0, stream, w, row_bytes, act, y, ldy, M, N);
     return 0;
   }
   // up to 64 rows: 16-row activation tiles; prefill: 64 activation rows x (Q4_K) 128 weight rows

@@ -8,48 +8,59 @@
 
 namespace mxa {
 
-// One wave per (row m, 256-value block b); lane l owns elements 4l..4l+3. Restates
-// mx_quantize_row_q8_k (app/native/src/mx_common.c:42-69): amax over the block; an all-zero block
-// gives q = 0, bsums = 0, d = 0; otherwise iscale = 127/amax and d = amax/127 are correctly
-// rounded divisions, q = clamp(round-half-even(x * iscale), +-127) (lrintf in the default
-// rounding mode is v_rndne_f32), bsums are the sums of q over 16 values.
+// 16 lanes per (row m, 256-value block b), four blocks per wave; lane part p owns elements
+// 16p..16p+15. Restates mx_quantize_row_q8_k (app/native/src/mx_common.c:42-69): amax over the
+// block; an all-zero block gives q = 0, bsums = 0, d = 0; otherwise iscale = 127/amax and
+// d = amax/127 are correctly rounded divisions, q = clamp(round-half-even(x * iscale), +-127)
+// (lrintf in the default rounding mode is v_rndne_f32), bsums are the sums of q over 16 values.
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
                                                            int8_t* __restrict__ q,
                                                            float* __restrict__ d,
                                                            int16_t* __restrict__ bsums, int m_rows,
                                                            int k, int nb) {
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wave >= m_rows * nb) return;
-  const int m = wave / nb, b = wave - m * nb;
-  const size_t base = (size_t)m * k + (size_t)b * QK + 4 * lane;
-  const float4 v = *(const float4*)(x + base);
+  const int blk = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int p = threadIdx.x & 15;
+  if (blk >= m_rows * nb) return;  // whole 16-lane rows leave together (the DPP max stays in a row)
+  const int m = blk / nb, b = blk - m * nb;
+  const size_t base = (size_t)m * k + (size_t)b * QK + 16 * p;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 f = *(const float4*)(x + base + 4 * i);
+    v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+  }
   // fmaxf ignores a NaN operand and the running maximum starts at 0, as the reference's
   // `ax > amax ? ax : amax` from 0: a NaN input never becomes amax.
-  float amax = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
+  float amax = 0.0f;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = max16(amax);
+  int qv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) qv[i] = 0;
   if (amax != 0.0f) {
     const float iscale = 127.0f / amax;
-    q0 = (int)fminf(fmaxf(rintf(v.x * iscale), -127.0f), 127.0f);
-    q1 = (int)fminf(fmaxf(rintf(v.y * iscale), -127.0f), 127.0f);
-    q2 = (int)fminf(fmaxf(rintf(v.z * iscale), -127.0f), 127.0f);
-    q3 = (int)fminf(fmaxf(rintf(v.w * iscale), -127.0f), 127.0f);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = (int)fminf(fmaxf(rintf(v[i] * iscale), -127.0f), 127.0f);
   }
-  const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
-                          ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
-  *(uint32_t*)(q + base) = packed;
-  const int s = quad_sum(q0 + q1 + q2 + q3);
-  if ((lane & 3) == 0) bsums[((size_t)m * nb + b) * 16 + (lane >> 2)] = (int16_t)s;
-  if (lane == 0) d[(size_t)m * nb + b] = amax / 127.0f;
+  uint32_t packed[4];
+  int bsum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    packed[i] = (uint32_t)(qv[4 * i] & 0xFF) | ((uint32_t)(qv[4 * i + 1] & 0xFF) << 8) |
+                ((uint32_t)(qv[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * i + 3] & 0xFF) << 24);
+    bsum += qv[4 * i] + qv[4 * i + 1] + qv[4 * i + 2] + qv[4 * i + 3];
+  }
+  *(uint4*)(q + base) = uint4{packed[0], packed[1], packed[2], packed[3]};
+  bsums[((size_t)m * nb + b) * 16 + p] = (int16_t)bsum;
+  if (p == 0) d[(size_t)m * nb + b] = amax / 127.0f;
 }
 
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream) {
   const int nb = k / QK;
-  const int waves = m_rows * nb;
-  const int grid = (waves + 3) / 4;
+  const int blocks = m_rows * nb;
+  const int grid = (blocks + 15) / 16;
   hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, stream, x, a.q, a.d, a.bsums,
                      m_rows, k, nb);
 }
