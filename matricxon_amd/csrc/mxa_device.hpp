@@ -145,6 +145,43 @@ struct Act {
   void* xsplit;  // IQ4_XS prefill: workspace for the bf16 split of x (nullptr when not provided)
 };
 
+// ------------------------------------------------------------------ LDS copies and their waits
+// A weight wave streams packed bytes into LDS with global_load_lds_dwordx4 and waits for them
+// with its own s_waitcnt: copies complete in issue order, so "the copies of stage s have landed"
+// is "at most n copies are outstanding", n being the copies issued after stage s.
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_u8*)p;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63]; lgkmcnt and expcnt are not waited for.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define MXA_VM(k) \
+  case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0x0F70); break;
+#define MXA_VM8(k) MXA_VM(k) MXA_VM(k + 1) MXA_VM(k + 2) MXA_VM(k + 3) MXA_VM(k + 4) \
+  MXA_VM(k + 5) MXA_VM(k + 6) MXA_VM(k + 7)
+  switch (n) {
+    MXA_VM8(0) MXA_VM8(8) MXA_VM8(16) MXA_VM8(24) MXA_VM8(32) MXA_VM8(40) MXA_VM8(48) MXA_VM8(56)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+#undef MXA_VM8
+#undef MXA_VM
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+}
+
+constexpr int kMaxCopies = 63;  // the largest vmcnt: copies a weight wave may have outstanding
+
+// global_load_lds_dwordx4: 16 bytes per lane from `g` to LDS byte address m0 + 16 * lane. Issued
+// as inline assembly so that the compiler's own wait insertion does not see it (it would add
+// vmcnt(0) before unrelated instructions); the kernel waits for these copies itself.
+__device__ __forceinline__ void copy16_to_lds(const void* g, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr) : "memory");
+}
+
 // Grid-order tile index for workgroup `wg` of `n_wg` such that consecutive tiles land on the same
 // XCD: workgroups are dealt to the 8 XCDs round-robin, so XCD x gets a contiguous tile range.
 __device__ __forceinline__ int xcd_tile(int wg, int n_wg) {

@@ -8,6 +8,19 @@
 
 namespace mxa {
 
+int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
 int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                   long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (m_rows <= kFusedQuantMaxRows)

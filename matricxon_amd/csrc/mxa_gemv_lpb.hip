@@ -26,7 +26,6 @@ constexpr int kWaveLanes = 64;
 constexpr int kActPad = 16;  // LDS bytes of padding after each staged 256-value activation block
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 template <int TYPE>
 struct Lpb;
@@ -516,31 +515,6 @@ int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, float* y, 
 // in the issue queue instead of computing. After its last stage one lane per (row, activation
 // row) folds the row's nb block values in order.
 
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63]; lgkmcnt and expcnt are not waited for.
-__device__ __forceinline__ void wait_vmcnt(int n) {
-#define MXA_VM(k) \
-  case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0x0F70); break;
-#define MXA_VM8(k) MXA_VM(k) MXA_VM(k + 1) MXA_VM(k + 2) MXA_VM(k + 3) MXA_VM(k + 4) \
-  MXA_VM(k + 5) MXA_VM(k + 6) MXA_VM(k + 7)
-  switch (n) {
-    MXA_VM8(0) MXA_VM8(8) MXA_VM8(16) MXA_VM8(24) MXA_VM8(32) MXA_VM8(40) MXA_VM8(48) MXA_VM8(56)
-    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-  }
-#undef MXA_VM8
-#undef MXA_VM
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("" ::: "memory");
-}
-
-constexpr int kMaxCopies = 63;  // the largest vmcnt: copies a weight wave may have outstanding
-
-// global_load_lds_dwordx4: 16 bytes per lane from `g` to LDS byte address m0 + 16 * lane. Issued
-// as inline assembly so that the compiler's own wait insertion does not see it (it would add
-// vmcnt(0) before unrelated instructions); the kernel waits for these copies itself.
-__device__ __forceinline__ void copy16_to_lds(const void* g, uint32_t lds_addr) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr) : "memory");
-}
-
 struct PipeGeo {
   int rows_per_wave;  // R
   int weight_waves;
@@ -680,9 +654,10 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long l
   const int R = geo.rows_per_wave, P = geo.ahead, ww = wave - na;
   const int vslots = R * nb;
   const int buf_bytes = geo.buf_kb * 1024;
-  const int wave_bytes = (P + 1) * buf_bytes + vslots * 4 * (MAXM + 1);
+  const int nbuf = min(P + 1, (vslots + 63) >> 6);  // P >= the stage count: no buffer is reused
+  const int wave_bytes = nbuf * buf_bytes + vslots * 4 * (MAXM + 1);
   uint8_t* wreg = region + ww * wave_bytes;
-  float* Vbuf = (float*)(wreg + (P + 1) * buf_bytes);  // [MAXM][vslots]
+  float* Vbuf = (float*)(wreg + nbuf * buf_bytes);  // [MAXM][vslots]
   float* Dbuf = Vbuf + MAXM * vslots;                   // [vslots]
 
   const int n0 = (xcd_tile(blockIdx.x, gridDim.x) * geo.weight_waves + ww) * R;
@@ -694,10 +669,10 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long l
   // whole aligned 16-byte chunks: the first and last may extend past the matrix, but a 16-byte
   // aligned chunk holding one of its bytes never leaves that byte's page
   const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
-  const uint32_t lds_w = (uint32_t)(uintptr_t)(lds_u8*)wreg;
+  const uint32_t lds_w = lds_addr(wreg);
   auto issue = [&](int s) {
     const uintptr_t g = s_al + (uintptr_t)s * 64 * L::kBytes + (uintptr_t)lane * 16;
-    const uint32_t dst = lds_w + (uint32_t)((s % (P + 1)) * buf_bytes);
+    const uint32_t dst = lds_w + (uint32_t)((s % nbuf) * buf_bytes);
     const int n = stage_copies<L::kBytes>(s, nblk, mis);
     if (s + 1 < stages) {  // the bytes of a later stage follow: no copy passes the matrix end
       for (int t = 0; t < n; ++t) copy16_to_lds((const void*)(g + (uintptr_t)t * 1024), dst + t * 1024);
@@ -748,9 +723,9 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long l
     }
     float V[MAXM], D;
     if constexpr (ACTREG)  // lanes past the range end compute with their own block: never stored
-      L::template compute<1, ActRegs>(wreg + (s % (P + 1)) * buf_bytes, boff, &areg, 1, V, D);
+      L::template compute<1, ActRegs>(wreg + (s % nbuf) * buf_bytes, boff, &areg, 1, V, D);
     else
-      L::template compute<MAXM, ActBlock>(wreg + (s % (P + 1)) * buf_bytes, boff, ablk, M, V, D);
+      L::template compute<MAXM, ActBlock>(wreg + (s % nbuf) * buf_bytes, boff, ablk, M, V, D);
     b += step;
     b = b >= nb ? b - nb : b;
     const int j = 64 * s + jl;
@@ -769,23 +744,24 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long l
     const float* dd = Dbuf + fr * nb;
     const float* xd = act_d + fm * nb;
     float acc = 0.0f;
-    for (int bb = 0; bb < nb; ++bb)
+    int bb = 0;
+    // 16 blocks' operands are read from LDS before they are folded: the chain of dependent
+    // fmas then waits for one LDS round trip, not one per block
+    for (; bb + 16 <= nb; bb += 16) {
+      float vv[16], xx[16], ww[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        vv[i] = v[bb + i];
+        xx[i] = kFloatAct ? 0.0f : xd[bb + i];
+        ww[i] = L::kHasD ? dd[bb + i] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc = L::fold(acc, xx[i], vv[i], ww[i]);
+    }
+    for (; bb < nb; ++bb)
       acc = L::fold(acc, kFloatAct ? 0.0f : xd[bb], v[bb], L::kHasD ? dd[bb] : 0.0f);
     y[(size_t)fm * ldy + n0 + fr] = acc;
   }
-}
-
-int cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      n = v;
-    else
-      n = 256;
-  }
-  return n;
 }
 
 // Returns -1 when the shape does not suit the pipelined form (the caller uses gemv_lpb_kernel).
@@ -807,7 +783,9 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   PipeGeo geo;
   geo.act_waves = na;
   geo.buf_kb = kBufKb;
-  auto wave_bytes = [&](int P, int R) { return (P + 1) * kBufKb * 1024 + R * nb * 4 * (MAXM + 1); };
+  auto wave_bytes = [&](int P, int R) {
+    return min(P + 1, (R * nb + 63) / 64) * kBufKb * 1024 + R * nb * 4 * (MAXM + 1);
+  };
   // First choice: one workgroup per CU whose waves stream all their rows (every row requested in
   // one round). When the rows' block values do not fit beside the buffers: two workgroups per CU
   // of about 8 stages per wave, so that one fills its pipeline while the other drains. One stage

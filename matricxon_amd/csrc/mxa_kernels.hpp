@@ -44,6 +44,9 @@ int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long
                    long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
                    hipStream_t stream);
 
+// Compute units of the current device (cached after the first call).
+int cu_count();
+
 // Activation rows up to which the matmul kernels quantize x themselves (no workspace).
 constexpr int kFusedQuantMaxRows = 4;
 
@@ -58,6 +61,12 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
 bool mtile_supported(int type);
 int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
+// Batched decode (m_rows <= 16) on the matrix cores with the weight rows streamed into LDS by
+// coalesced copies, one persistent workgroup per CU: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
+// workspace. -1 when the shape does not suit it (the caller uses launch_mtile).
+int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                   long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // IQ4_XS prefill on the matrix cores (m_rows >= kIq4MfmaMinRows): x split into bf16 hi / lo in
 // `workspace` (iq4_prefill_workspace bytes), then bf16 MFMAs per 32-value sub-block.

@@ -1,317 +1,26 @@
 // Matrix-core matmul for M > 4 activation rows (batched decode and prefill), Q4_K / Q6_K / Q8_0.
 //
-// Tiling. A workgroup of 1, 2 or 4 waves owns 16 consecutive weight rows per wave and 16 * MT
-// activation rows (the host picks the wave count that gives the GPU enough workgroups); grid.y walks the activation rows, so a weight block is read once per 16 * MT
-// activation rows. The Q8_K activations (always pre-quantized in the workspace here) are staged in
-// LDS per chunk of kCB blocks; each wave keeps its rows' blocks of the next chunk in registers
-// while it computes the current one.
+// Tiling. A workgroup of 4 waves owns 16 consecutive weight rows per wave and 16 * MT activation
+// rows; grid.y walks the activation rows, so a weight block is read once per 16 * MT activation
+// rows. The Q8_K activations (always pre-quantized in the workspace here) are staged in LDS per
+// chunk of kCB blocks; each wave keeps its rows' blocks of the next chunk in registers while it
+// computes the current one.
 //
-// Operands of v_mfma_i32_16x16x64_i8: A (16 activation rows m x 64 k) from LDS, B (64 k x 16 weight
-// rows n) built in registers from the packed bytes. Lane l supplies row (l % 16) and k-group
-// g = l / 16 of both; its output holds n = l % 16 and m = 4 g + i (i < 4). The k-group / MFMA t
-// assignment of the 256 values of a block differs per type and is chosen so that every lane-group
-// slice of an MFMA lies inside one scale sub-block:
-//   Q4_K  (8 sub-blocks of 32): lane group g, MFMA t: elements 64 g + 16 t + (0..15). The scale is
-//         folded into B exactly as two int8 planes, (sc >> 3) * u and (sc & 7) * u (both <= 105),
-//         8 * plane_hi + plane_lo; the min term sum(min * bsums) is one fp16 MFMA (exact).
-//   Q6_K  (16 sub-blocks of 16): lane group g (half h = g / 2, quarter q = g % 2), MFMA t: elements
-//         128 h + 32 t + 16 q + (0..15) = sub-block 8 h + 2 t + q. A lane group then reads 16
-//         bytes of qh and 2 x 16 of ql that no other lane group reads. B is the unsigned code u =
-//         q + 32 (<= 63); masking B to one lane group per MFMA gives each sub-block's integer dot,
-//         scaled by its signed 8-bit scale in integer arithmetic; the -32 * sum(sc * bsums) term is
-//         one fp16 MFMA of bsums (|.| <= 2032) against the scales, exact.
-//   Q8_0  (8 blocks of 32): lane group g, MFMA t: elements 64 g + 16 t + (0..15), i.e. Q8_0 block
-//         2 g + t / 2; B is the int8 quants as stored, masked to one lane group per MFMA pair.
-//
-// Numerics: integer block dots are exact; the fp32 steps and their order are the CPU oracle's
-// (app/native/src/mx_dot_k_ssse3.c:150-154, 200-206; mx_dot_q8_0.c:8-18) and the blocks are folded
-// in order 0..nb-1, so the outputs equal the oracle and the decode kernels bit for bit.
+// Operands: the tile builders of mxa_tiles.hpp, with A (16 activation rows x 64 k) read from LDS.
+// The blocks are folded in order 0..nb-1, so the outputs equal the oracle and the decode kernels
+// bit for bit.
 #include "mxa_kernels.hpp"
+#include "mxa_tiles.hpp"
 
 #pragma clang fp contract(off)
 
 namespace mxa {
 namespace {
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte aligned (LDS reads)
-
 constexpr int kCB = 2;                    // blocks per activation chunk
 constexpr int kQStride = kCB * QK + 16;   // LDS bytes per activation row (padding: distinct banks)
 constexpr int kBStride = kCB * 16 + 8;    // LDS halves per activation row of bsums
 
-__device__ __forceinline__ i32x4 as_i32x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  return i32x4{(int)a, (int)b, (int)c, (int)d};
-}
-
-// Each byte of u times s (s * byte <= 255, so no carry crosses a byte): v_pk_mul_lo_u16.
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t u, uint32_t s) {
-  const u16x2 a = __builtin_bit_cast(u16x2, u);
-  const u16x2 b = {(uint16_t)s, (uint16_t)s};
-  return __builtin_bit_cast(uint32_t, a * b);
-}
-
-// Activation chunk in LDS: q8 rows, bsums (as fp16) and scales of 16 * MT rows x kCB blocks.
-struct ActTile {
-  const int8_t* q;        // row r at q + r * qs, block bb at + bb * QK
-  const _Float16* bs;     // row r at bs + r * bst, block bb at + bb * 16
-  int qs, bst;            // row strides (bytes, halves)
-};
-
-// Every type provides: W (a lane's bytes of one weight tile's block) and load(); P = prep(W, g),
-// the B operands of that tile and block; F = frag(A, bb, mt, ln, g), the A operands of activation
-// tile mt (shared by all weight tiles of the wave); value(P, F, g, sink), which calls
-// sink(e, v, d) with the block value of m = 4 g + e of the tile, n = lane % 16; and fold(acc, xd,
-// v, d), the oracle's fold step.
-
-// ---------------------------------------------------------------------------------------- Q4_K
-struct TileQ4 {
-  struct W {
-    u32x4a4 hdr, qa, qb;
-  };
-  struct P {
-    i32x4 bh[4], bl[4];  // planes of MFMA t: (sc >> 3) * u and (sc & 7) * u
-    f16x4 bmin;
-    float d, dmin;
-  };
-  struct F {
-    i32x4 a[4];
-    f16x4 bs;
-  };
-  __device__ static W load(const uint8_t* row, int b, int g) {
-    const uint8_t* blk = row + (size_t)b * 144;
-    W L;
-    L.hdr = ld16_stream(blk);
-    L.qa = ld16_stream(blk + 16 + 32 * g);
-    L.qb = ld16_stream(blk + 32 + 32 * g);
-    return L;
-  }
-  __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
-  __device__ static P prep(const W& L, int g) {
-    P p;
-    p.d = half_to_float(L.hdr.x);
-    p.dmin = half_to_float(L.hdr.x >> 16);
-    const K4Scales s = k4_scales(L.hdr.y, L.hdr.z, L.hdr.w);
-    const uint32_t sc0 = k4_pick(s.sc_lo, s.sc_hi, 2 * g), sc1 = k4_pick(s.sc_lo, s.sc_hi, 2 * g + 1);
-    const uint32_t mn0 = k4_pick(s.mn_lo, s.mn_hi, 2 * g), mn1 = k4_pick(s.mn_lo, s.mn_hi, 2 * g + 1);
-    const uint32_t q[8] = {L.qa.x, L.qa.y, L.qa.z, L.qa.w, L.qb.x, L.qb.y, L.qb.z, L.qb.w};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t sh = (t < 2 ? sc0 : sc1) >> 3, sl = (t < 2 ? sc0 : sc1) & 7;
-      uint32_t u[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        u[i] = t == 0 ? q[i] & 0x0F0F0F0Fu : t == 1 ? q[4 + i] & 0x0F0F0F0Fu
-             : t == 2 ? (q[i] >> 4) & 0x0F0F0F0Fu : (q[4 + i] >> 4) & 0x0F0F0F0Fu;
-      p.bh[t] = as_i32x4(mul_bytes(u[0], sh), mul_bytes(u[1], sh), mul_bytes(u[2], sh), mul_bytes(u[3], sh));
-      p.bl[t] = as_i32x4(mul_bytes(u[0], sl), mul_bytes(u[1], sl), mul_bytes(u[2], sl), mul_bytes(u[3], sl));
-    }
-    const _Float16 m0 = (_Float16)(float)mn0, m1 = (_Float16)(float)mn1;
-    p.bmin = f16x4{m0, m0, m1, m1};
-    return p;
-  }
-  __device__ static F frag(const ActTile& A, int bb, int mt, int ln, int g) {
-    F f;
-    const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 64 * g;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
-    f.bs = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
-    return f;
-  }
-  template <class S>
-  __device__ static void value(const P& p, const F& f, int, S&& sink) {
-    i32x4 sum = {0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bh[t], sum, 0, 0, 0);
-    sum = sum * 8;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bl[t], sum, 0, 0, 0);
-    // summ = sum over the 16 bsums of min_{s/2} * bsum: A = bsums (k = 4g..4g+3), B = mins
-    const f32x4 summ = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bmin, f32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sink(i, fmaf(p.d, (float)sum[i], -(p.dmin * summ[i])), 0.0f);
-  }
-};
-
-// ---------------------------------------------------------------------------------------- Q6_K
-struct TileQ6 {
-  struct W {
-    u32x4a4 qla, qlb, qh, sc;  // ql[64h + 16q ..], ql[64h + 32 + 16q ..], qh[32h + 16q ..], scales
-    uint32_t d;
-  };
-  struct P {
-    u32x4a4 bu[4];  // codes u of MFMA t (elements 128 h + 32 t + 16 q + j)
-    int scv[4][4];  // scale of the sub-block of (MFMA t, lane group g2), row n
-    f16x4 bsc;      // scales 4 g .. 4 g + 3 of row n (the bsums term)
-    float d;
-  };
-  struct F {
-    i32x4 a[4];
-    f16x4 bs;
-  };
-  // 16 bytes at p, 2-byte aligned at worst (210-byte blocks): dword loads + v_alignbyte. The fifth
-  // dword is read only when p is not 4-byte aligned, so no byte past p + 15 is touched.
-  __device__ static u32x4a4 ld16_a2(const uint8_t* p) {
-    const uintptr_t a = (uintptr_t)p;
-    const uint8_t* base = (const uint8_t*)(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);
-    const u32x4a4 v = ld16_stream(base);
-    const uint32_t e = sh ? __builtin_nontemporal_load((const uint32_t*)(base + 16)) : 0u;
-    return u32x4a4{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
-                   __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh)};
-  }
-  __device__ static W load(const uint8_t* row, int b, int g) {
-    const uint8_t* blk = row + (size_t)b * 210;
-    const int h = g >> 1, q = g & 1;
-    W L;
-    L.qla = ld16_a2(blk + 64 * h + 16 * q);
-    L.qlb = ld16_a2(blk + 64 * h + 32 + 16 * q);
-    L.qh = ld16_a2(blk + 128 + 32 * h + 16 * q);
-    L.sc = ld16_a2(blk + 192);
-    L.d = (uint32_t)*(const uint16_t*)(blk + 208);
-    return L;
-  }
-  // block value sumi (as float) with the block's d; fold (xd * d) * sumi (mx_dot_k_ssse3.c:200-206)
-  __device__ static float fold(float acc, float xd, float v, float d) { return fmaf(xd * d, v, acc); }
-  __device__ static P prep(const W& L, int g) {
-    P p;
-    p.d = half_to_float(L.d);
-    const uint32_t la[4] = {L.qla.x, L.qla.y, L.qla.z, L.qla.w};
-    const uint32_t lb[4] = {L.qlb.x, L.qlb.y, L.qlb.z, L.qlb.w};
-    const uint32_t hh[4] = {L.qh.x, L.qh.y, L.qh.z, L.qh.w};
-    const uint32_t scw[4] = {L.sc.x, L.sc.y, L.sc.z, L.sc.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p.bu[0][i] = q6_codes<0>(la[i], hh[i]);
-      p.bu[1][i] = q6_codes<1>(lb[i], hh[i]);
-      p.bu[2][i] = q6_codes<2>(la[i], hh[i]);
-      p.bu[3][i] = q6_codes<3>(lb[i], hh[i]);
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int g2 = 0; g2 < 4; ++g2) {
-        const int sub = 8 * (g2 >> 1) + 2 * t + (g2 & 1);
-        p.scv[t][g2] = (int)(int8_t)(uint8_t)(scw[sub >> 2] >> (8 * (sub & 3)));
-      }
-    const uint32_t sw = scw[g];
-    p.bsc = f16x4{(_Float16)(float)(int8_t)(sw & 0xFF), (_Float16)(float)(int8_t)((sw >> 8) & 0xFF),
-                  (_Float16)(float)(int8_t)((sw >> 16) & 0xFF), (_Float16)(float)(int8_t)(sw >> 24)};
-    return p;
-  }
-  __device__ static F frag(const ActTile& A, int bb, int mt, int ln, int g) {
-    F f;
-    const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 128 * (g >> 1) + 16 * (g & 1);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 32 * t));
-    f.bs = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
-    return f;
-  }
-  template <class S>
-  __device__ static void value(const P& p, const F& f, int g, S&& sink) {
-    int sumi[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int g2 = 0; g2 < 4; ++g2) {
-        const bool on = g == g2;  // B restricted to lane group g2: one sub-block's dot
-        const i32x4 b = as_i32x4(on ? p.bu[t].x : 0u, on ? p.bu[t].y : 0u, on ? p.bu[t].z : 0u, on ? p.bu[t].w : 0u);
-        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], b, i32x4{0, 0, 0, 0}, 0, 0, 0);
-        // |D| <= 16 * 63 * 127 < 2^17, |sc| <= 128: 24-bit products
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sumi[i] += __mul24(p.scv[t][g2], D[i]);
-      }
-    // C = sum over the 16 sub-blocks of bsums(m) * sc(n), exact (|C| < 2^22)
-    const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bsc, f32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sink(i, (float)(sumi[i] - 32 * (int)C[i]), p.d);
-  }
-};
-
-// ---------------------------------------------------------------------------------------- Q8_0
-struct TileQ8 {
-  struct W {
-    uint32_t w[17];  // bytes 68 g .. 68 g + 67 of the 272-byte group: blocks 2 g and 2 g + 1
-  };
-  struct P {
-    u32x4a4 qb[4];  // quants of MFMA t: block 2 g + t / 2, elements 16 (t % 2) ..
-    float dk[8];    // d of the 8 blocks of row n
-  };
-  struct F {
-    i32x4 a[4];
-  };
-  __device__ static W load(const uint8_t* row, int b, int g) {
-    const uint8_t* p = row + (size_t)b * 272 + 68 * g;  // 4-byte aligned
-    W L;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4a4 v = ld16_stream(p + 16 * i);
-      L.w[4 * i] = v.x, L.w[4 * i + 1] = v.y, L.w[4 * i + 2] = v.z, L.w[4 * i + 3] = v.w;
-    }
-    L.w[16] = __builtin_nontemporal_load((const uint32_t*)(p + 64));
-    return L;
-  }
-  // block value sum_k d_k * p_k in k order; fold xd * value (mx_dot_q8_0.c:8-18)
-  __device__ static float fold(float acc, float xd, float v, float) { return fmaf(xd, v, acc); }
-  __device__ static P prep(const W& L, int g) {
-    P p;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p.qb[0][i] = __builtin_amdgcn_alignbyte(L.w[i + 1], L.w[i], 2);
-      p.qb[1][i] = __builtin_amdgcn_alignbyte(L.w[i + 5], L.w[i + 4], 2);
-      p.qb[2][i] = L.w[9 + i];
-      p.qb[3][i] = L.w[13 + i];
-    }
-    // this lane holds the d of blocks 2 g and 2 g + 1; lane n + 16 g2 holds those of 2 g2..
-    const int ln = (int)(__lane_id() & 15);
-    const uint32_t mine = (L.w[0] & 0xFFFFu) | (L.w[8] & 0xFFFF0000u);
-#pragma unroll
-    for (int g2 = 0; g2 < 4; ++g2) {
-      const uint32_t v = (uint32_t)__shfl((int)mine, ln + 16 * g2, 64);
-      p.dk[2 * g2] = half_to_float(v);
-      p.dk[2 * g2 + 1] = half_to_float(v >> 16);
-    }
-    (void)g;
-    return p;
-  }
-  __device__ static F frag(const ActTile& A, int bb, int mt, int ln, int g) {
-    F f;
-    const int8_t* arow = A.q + (16 * mt + ln) * A.qs + bb * QK + 64 * g;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
-    return f;
-  }
-  template <class S>
-  __device__ static void value(const P& p, const F& f, int g, S&& sink) {
-    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {  // block k = 2 g2 + h: MFMAs t = 2 h, 2 h + 1 of lane group g2
-      const int g2 = k >> 1, h = k & 1;
-      const bool on = g == g2;
-      i32x4 D = {0, 0, 0, 0};
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int t = 2 * h + tt;
-        const i32x4 b = as_i32x4(on ? p.qb[t].x : 0u, on ? p.qb[t].y : 0u, on ? p.qb[t].z : 0u, on ? p.qb[t].w : 0u);
-        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], b, D, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) bs[i] = fmaf(p.dk[k], (float)D[i], bs[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sink(i, bs[i], 0.0f);
-  }
-};
-
-template <int TYPE>
-struct TileOf;
-template <> struct TileOf<T_Q4_K> { using T = TileQ4; };
-template <> struct TileOf<T_Q6_K> { using T = TileQ6; };
-template <> struct TileOf<T_Q8_0> { using T = TileQ8; };
 
 // Row-tiled kernel: MT activation tiles x NT weight tiles of 16 rows per wave, 4 waves.
 template <int TYPE, int MT, int NT>
@@ -595,7 +304,9 @@ int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
 template <int TYPE>
 int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                    int M, int N, hipStream_t stream) {
-  // M <= 16: the block-split kernel unless the 64-row tiles alone give >= 512 workgroups
+  // M <= 16: the streaming kernel, else the block-split kernel unless the 64-row tiles alone give
+  // >= 512 workgroups
+  if (M <= 16 && launch_bstream(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && N < 512 * 64) {
     constexpr int RT = TYPE == T_Q6_K ? 1 : 2;
     const int tiles = (N + 16 * RT - 1) / (16 * RT);

@@ -210,6 +210,22 @@ def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None
     check_gemm(gpu, oracle, ggml_type, w, x, n, k)
 
 
+# Shapes for the batched-decode streaming kernel (5..16 tokens): rows per workgroup = max(16,
+# N / CUs), so N = 4100 leaves a one-row tile and a three-row last workgroup, N = 5000 a four-row
+# tile; K = 2304 gives an odd block count (the last wave owns one block), K = 768 three waves,
+# K = 5120 and 8192 four blocks per wave; Q6_K rows of 210 x odd bytes start on 2-byte boundaries.
+BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
+                (5000, 1024, 16), (23, 768, 7), (260, 5120, 9)]
+
+
+@pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
+@pytest.mark.parametrize("n,k,m", BATCH_SHAPES)
+def test_batched_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None:
+    w = S.packed_weight(ggml_type, n, k, seed=n * 3 + k + m)
+    x = S.activations(m, k, seed=m * 11 + n)
+    check_gemm(gpu, oracle, ggml_type, w, x, n, k)
+
+
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
 @pytest.mark.parametrize("n,k,m", [(130, 256, 4), (5, 16640, 3), (70, 4096, 1)])
 def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> None:
