@@ -170,6 +170,21 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
         wb = sum(n * row_bytes(t, k) for t, n, k in layer)
         report(f"cfg4 llama3-8b layer (7 projections) M={m}", _graph_us(layer_step, steps, warmup),
                wb, 2.0 * m * sum(n * k for _, n, k in layer))
+        # the layer as the model issues it: q|k|v and gate|up share their input (one activation
+        # quantization each; one launch per group for up to 4 tokens)
+        qkv_out = torch.empty((m, 6144), dtype=torch.float32, device=dev)
+        gu_out = torch.empty((m, 28672), dtype=torch.float32, device=dev)
+
+        def layer_shared_step(i):
+            gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (0, 1, 2)],
+                              xs[4096], out=qkv_out)
+            gemm.matmul(layer[3][0], lw[3][i % 2], xs[4096], 4096, 4096, out=ys[3])
+            gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (4, 5)],
+                              xs[4096], out=gu_out)
+            gemm.matmul(layer[6][0], lw[6][i % 2], xs[14336], 4096, 14336, out=ys[6])
+        report(f"cfg4 llama3-8b layer (q|k|v, o, gate|up, down) M={m}",
+               _graph_us(layer_shared_step, steps, warmup), wb,
+               2.0 * m * sum(n * k for _, n, k in layer))
         names = ["q", "k", "v", "o", "gate", "up", "down"]
         for j, (t, n, k) in enumerate(layer):
             if names[j] in ("k", "up"):  # same shapes as v (size) / gate

@@ -167,6 +167,16 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
   }
   mxa::Act act = make_act(x, abuf, in_features);
   if (split_bytes > 0) act.xsplit = (uint8_t*)workspace + q8k_bytes;
+  if (n > 1 && !any_iq4 && n_tokens <= mxa::kFusedQuantMaxRows) {  // one launch for all weights
+    mxa::DecodeSeg seg[4];
+    long long c0 = 0;
+    for (int i = 0; i < n; ++i) {
+      seg[i] = mxa::DecodeSeg{types[i], (const uint8_t*)ws[i],
+                              (long long)mxa_row_bytes(types[i], in_features), y + c0, outs[i]};
+      c0 += outs[i];
+    }
+    if (mxa::launch_decode_multi(seg, n, act, total, n_tokens, s) == 0) return check_launch();
+  }
   long long col = 0;
   for (int i = 0; i < n; ++i) {
     const long long rb = (long long)mxa_row_bytes(types[i], in_features);

@@ -627,16 +627,17 @@ __device__ __forceinline__ void stage_activations(const Act& act, int M, int aw,
 
 // ACTREG (one activation row, 64 % nb == 0): lane l's block of the row is l % nb in every stage,
 // so the lane keeps that block's Q8_K values in registers instead of reading LDS per stage.
+// One workgroup's share of a pipelined decode: rows of workgroup tile `tile` (R rows per weight
+// wave) of one packed weight.
 template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG>
-__global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long long row_bytes,
-                                                         Act act, float* __restrict__ y,
-                                                         long long ldy, int M, int N, PipeGeo geo) {
+__device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
+                                          const Act& act, float* __restrict__ y, long long ldy,
+                                          int M, int N, const PipeGeo& geo, int tile) {
   static_assert(!ACTREG || (MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0)),
                 "register activations: one Q8_K row, types whose compute leaves room for them");
   using L = Lpb<TYPE>;
   constexpr bool kFloatAct = TYPE == T_IQ4_XS;
   constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
-  extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar control flow
@@ -660,7 +661,7 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long l
   float* Vbuf = (float*)(wreg + nbuf * buf_bytes);  // [MAXM][vslots]
   float* Dbuf = Vbuf + MAXM * vslots;                   // [vslots]
 
-  const int n0 = (xcd_tile(blockIdx.x, gridDim.x) * geo.weight_waves + ww) * R;
+  const int n0 = (tile * geo.weight_waves + ww) * R;
   const int nrows = max(0, min(R, N - n0));
   const int nblk = nrows * nb, stages = (nblk + 63) >> 6;
   const uint8_t* src0 = w + (size_t)min(n0, N - 1) * row_bytes;
@@ -765,6 +766,52 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long l
 }
 
 // Returns -1 when the shape does not suit the pipelined form (the caller uses gemv_lpb_kernel).
+template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG>
+__global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, long long row_bytes,
+                                                         Act act, float* __restrict__ y,
+                                                         long long ldy, int M, int N, PipeGeo geo) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  pipe_rows<TYPE, MAXM, FUSEQ, ACTREG>(smem, w, row_bytes, act, y, ldy, M, N, geo,
+                                       xcd_tile(blockIdx.x, gridDim.x));
+}
+
+// Several packed weights that share the activations (e.g. q, k and v) in one launch: workgroups
+// wg0 .. of segment s take its rows, R_s rows per weight wave; outputs go to columns of y.
+constexpr int kMaxSegs = 4;
+struct PipeSeg {
+  const uint8_t* w;
+  long long row_bytes;
+  float* y;  // the segment's first output column
+  int n, type, wg0, rows_per_wave;
+};
+struct PipeSegs {
+  PipeSeg s[kMaxSegs];
+  int count;
+};
+
+template <int MAXM, bool FUSEQ, bool ACTREG>
+__global__ __launch_bounds__(768) void gemv_pipe_multi_kernel(PipeSegs segs, Act act, long long ldy,
+                                                               int M, PipeGeo geo) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int wg = blockIdx.x;
+  int i = 0;
+  while (i + 1 < segs.count && wg >= segs.s[i + 1].wg0) ++i;
+  const PipeSeg sg = segs.s[i];
+  PipeGeo g = geo;
+  g.rows_per_wave = sg.rows_per_wave;
+  switch (sg.type) {
+    case T_Q4_K:
+      pipe_rows<T_Q4_K, MAXM, FUSEQ, ACTREG>(smem, sg.w, sg.row_bytes, act, sg.y, ldy, M, sg.n, g, wg - sg.wg0);
+      break;
+    case T_Q8_0:
+      pipe_rows<T_Q8_0, MAXM, FUSEQ, ACTREG>(smem, sg.w, sg.row_bytes, act, sg.y, ldy, M, sg.n, g, wg - sg.wg0);
+      break;
+    default:
+      pipe_rows<T_Q6_K, MAXM, FUSEQ, false>(smem, sg.w, sg.row_bytes, act, sg.y, ldy, M, sg.n, g, wg - sg.wg0);
+      break;
+  }
+}
+
 template <int TYPE, int MAXM, bool FUSEQ>
 int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                 int M, int N, hipStream_t stream) {
@@ -826,6 +873,76 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   return 0;
 }
 
+template <int TYPE>
+constexpr int kStageKb = (15 + 64 * Lpb<TYPE>::kBytes + 1023) / 1024;  // copies of a full stage
+
+// One launch over several weights of the K-quant / Q8_0 types that share the activations. Each
+// weight gets workgroups in proportion to its bytes (at least one) and its own rows per wave; the
+// stage buffers are sized for the largest block type. -1 when the shapes do not fit.
+template <int MAXM, bool FUSEQ>
+int launch_pipe_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int M,
+                      hipStream_t stream) {
+  constexpr int kLdsMax = 160 * 1024;
+  constexpr int kActBlk = QK + kActPad;
+  const int nb = act.nb;
+  if (count < 1 || count > kMaxSegs || nb > kWaveLanes) return -1;
+  int buf_kb = 0;
+  double total = 0.0;
+  for (int i = 0; i < count; ++i) {
+    const int t = seg[i].type;
+    if (t != T_Q4_K && t != T_Q6_K && t != T_Q8_0) return -1;
+    buf_kb = max(buf_kb, t == T_Q4_K ? kStageKb<T_Q4_K> : t == T_Q6_K ? kStageKb<T_Q6_K> : kStageKb<T_Q8_0>);
+    total += (double)seg[i].n * (double)seg[i].row_bytes;
+  }
+  const int act_lds = M * nb * (kActBlk + 32 + 4) + 16;
+  if (act_lds > 80 * 1024) return -1;
+  const int na = min(4, (M * nb + 15) / 16);
+  const int ncu = cu_count();
+  PipeGeo geo;
+  geo.act_waves = na;
+  geo.buf_kb = buf_kb;
+  PipeSegs segs;
+  segs.count = count;
+  int lds = 0, grid = 0;
+  bool ok = false;
+  for (int P = 1; P <= 2 && !ok; ++P) {
+    for (int nw = 8; nw >= 2 && !ok; --nw) {
+      int wg0 = 0, wave_max = 0;
+      for (int i = 0; i < count; ++i) {
+        const int share = max(1, (int)((double)ncu * seg[i].n * seg[i].row_bytes / total + 0.5));
+        const int R = (seg[i].n + share * nw - 1) / (share * nw);
+        const int wgs = (seg[i].n + nw * R - 1) / (nw * R);
+        segs.s[i] = PipeSeg{seg[i].w, seg[i].row_bytes, seg[i].y, seg[i].n, seg[i].type, wg0, R};
+        wg0 += wgs;
+        const int nbuf = min(P + 1, (R * nb + 63) / 64);
+        wave_max = max(wave_max, nbuf * buf_kb * 1024 + R * nb * 4 * (MAXM + 1));
+      }
+      if (act_lds + nw * wave_max <= kLdsMax && buf_kb * P <= kMaxCopies) {
+        ok = true;
+        geo.ahead = P;
+        geo.weight_waves = nw;
+        geo.rows_per_wave = 0;  // per segment
+        lds = act_lds + nw * wave_max;
+        grid = wg0;
+      }
+    }
+  }
+  if (!ok) return -1;
+  const bool actreg = MAXM == 1 && 64 % nb == 0;
+  auto kern = actreg ? gemv_pipe_multi_kernel<MAXM, FUSEQ, MAXM == 1> : gemv_pipe_multi_kernel<MAXM, FUSEQ, false>;
+  static bool lds_set = false;
+  if (!lds_set) {
+    (void)hipFuncSetAttribute((const void*)gemv_pipe_multi_kernel<MAXM, FUSEQ, MAXM == 1>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    (void)hipFuncSetAttribute((const void*)gemv_pipe_multi_kernel<MAXM, FUSEQ, false>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    lds_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (geo.weight_waves + na)), lds, stream, segs, act,
+                     ldy, M, geo);
+  return 0;
+}
+
 template <int TYPE, int MAXM, bool FUSEQ>
 int launch_decode(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                   int M, int N, hipStream_t stream) {
@@ -847,6 +964,18 @@ int launch_lpb_type(const uint8_t* w, long long row_bytes, const Act& act, float
 }
 
 }  // namespace
+
+int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy,
+                        int m_rows, hipStream_t stream) {
+  if (m_rows < 1 || m_rows > kFusedQuantMaxRows) return -1;
+  const bool fuse = act.q == nullptr;
+  if (m_rows == 1) return fuse ? launch_pipe_multi<1, true>(seg, count, act, ldy, m_rows, stream)
+                               : launch_pipe_multi<1, false>(seg, count, act, ldy, m_rows, stream);
+  if (m_rows == 2) return fuse ? launch_pipe_multi<2, true>(seg, count, act, ldy, m_rows, stream)
+                               : launch_pipe_multi<2, false>(seg, count, act, ldy, m_rows, stream);
+  return fuse ? launch_pipe_multi<4, true>(seg, count, act, ldy, m_rows, stream)
+              : launch_pipe_multi<4, false>(seg, count, act, ldy, m_rows, stream);
+}
 
 int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream) {

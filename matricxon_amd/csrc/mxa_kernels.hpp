@@ -56,6 +56,21 @@ constexpr int kFusedQuantMaxRows = 4;
 int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// One of several packed weights that share the activations of a multi-weight launch.
+struct DecodeSeg {
+  int type;
+  const uint8_t* w;
+  long long row_bytes;
+  float* y;  // the weight's first output column (row stride ldy)
+  int n;     // output rows of the weight
+};
+
+// Decode for 1 <= m_rows <= 4 over up to 4 K-quant / Q8_0 weights in one launch (shared-input
+// projections such as q/k/v or gate/up); quantizes act.x itself when act.q == nullptr. -1 when
+// the weights do not suit it (the caller launches them one by one).
+int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
+                        hipStream_t stream);
+
 // Matrix-core kernel for m_rows > 4 (batched decode and prefill) on Q8_K activations already in
 // the workspace: Q4_K, Q6_K, Q8_0.
 bool mtile_supported(int type);

@@ -169,11 +169,13 @@ class HipGemm:
                                              workspace.numel(), _stream(x.device))
         self._check(status, "mxa_quantize_q8_k", 15)
 
-    def matmul_multi(self, items: list[tuple[int, torch.Tensor, int]],
-                     x: torch.Tensor) -> list[torch.Tensor]:
+    def matmul_multi(self, items: list[tuple[int, torch.Tensor, int]], x: torch.Tensor,
+                     out: torch.Tensor | None = None) -> list[torch.Tensor]:
         """`items`: (ggml_type, packed, out_features) per weight sharing input `x`
         (n_tokens, in_features): one activation quantization, one float32 output per weight,
-        as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them."""
+        as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them. For up to 4 tokens
+        and K-quant / Q8_0 weights this is a single kernel launch. `out`, if given, is the
+        float32 (n_tokens, sum of out_features) result buffer the outputs are views of."""
         import ctypes
 
         if not 1 <= len(items) <= 4:
@@ -189,7 +191,14 @@ class HipGemm:
         x32 = x.detach().reshape(-1, in_features).to(device=device, dtype=torch.float32).contiguous()
         n_tokens = x32.shape[0]
         outs = [int(o) for _, _, o in items]
-        y = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
+        if out is None:
+            y = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
+        else:
+            if (out.dtype != torch.float32 or out.device != device or not out.is_contiguous()
+                    or tuple(out.shape) != (n_tokens, sum(outs))):
+                raise ValueError("out must be a contiguous float32 (n_tokens, sum of out_features) "
+                                 "tensor on the weights' device")
+            y = out
         # the Q8_K part and the IQ4_XS split part are separate regions of one workspace
         need = {False: 0, True: 0}
         for t, _, _ in items:

@@ -183,6 +183,42 @@ def test_gemm_multi_equals_separate_calls(gpu) -> None:
         assert torch.equal(y, gpu.matmul(t, w, x, o, k))
 
 
+# Shared-input weights in one launch (decode, <= 4 tokens): the q/k/v and gate/up shapes of the
+# layer config at reduced N, mixed block types, row counts that leave partial workgroups.
+MULTI_CASES = [
+    ([(D.Q4_K, 512), (D.Q4_K, 128), (D.Q6_K, 128)], 4096, 1),
+    ([(D.Q4_K, 700), (D.Q4_K, 700)], 4096, 2),
+    ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65), (D.Q4_K, 1)], 2048, 4),
+    ([(D.Q6_K, 300), (D.Q8_0, 40)], 768, 3),
+]
+
+
+@pytest.mark.parametrize("items,k,m", MULTI_CASES)
+def test_gemm_multi_single_launch_matches_oracle(gpu, oracle, items, k, m) -> None:
+    ws = [S.packed_weight(t, o, k, seed=90 + i) for i, (t, o) in enumerate(items)]
+    x_np = S.activations(m, k, seed=91 + m)
+    x = dev(x_np)
+    multi = gpu.matmul_multi([(t, dev(w), o) for (t, o), w in zip(items, ws)], x)
+    for (t, o), w, y in zip(items, ws, multi):
+        got = host(y)
+        want = oracle.gemm(t, w, x_np, o, k)
+        assert np.array_equal(bits(got), bits(want)), f"type {t} ({o} x {k}), {m} tokens"
+        assert torch.equal(y, gpu.matmul(t, dev(w), x, o, k))
+
+
+def test_gemm_multi_into_out_buffer(gpu) -> None:
+    k, m = 1024, 1
+    items = [(D.Q4_K, 32), (D.Q6_K, 48)]
+    ws = [dev(S.packed_weight(t, o, k, seed=i)) for i, (t, o) in enumerate(items)]
+    x = dev(S.activations(m, k, seed=3))
+    out = torch.empty((m, 80), dtype=torch.float32, device="cuda")
+    ys = gpu.matmul_multi([(t, w, o) for (t, o), w in zip(items, ws)], x, out=out)
+    assert ys[0].data_ptr() == out.data_ptr()
+    assert torch.equal(out[:, 32:], gpu.matmul(D.Q6_K, ws[1], x, 48, k))
+    with pytest.raises(ValueError):
+        gpu.matmul_multi([(t, w, o) for (t, o), w in zip(items, ws)], x, out=out[:, :40])
+
+
 def test_unsupported_shapes_fail_loudly(gpu) -> None:
     w = dev(S.packed_weight(D.Q4_K, 4, 512, seed=1))
     x = dev(S.activations(1, 512, seed=1))
