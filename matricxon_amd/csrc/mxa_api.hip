@@ -167,7 +167,7 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
   }
   mxa::Act act = make_act(x, abuf, in_features);
   if (split_bytes > 0) act.xsplit = (uint8_t*)workspace + q8k_bytes;
-  if (n > 1 && !any_iq4 && n_tokens <= mxa::kFusedQuantMaxRows) {  // one launch for all weights
+  if (n > 1 && !any_iq4 && n_tokens <= 16) {  // decode: one launch for all weights
     mxa::DecodeSeg seg[4];
     long long c0 = 0;
     for (int i = 0; i < n; ++i) {
@@ -175,7 +175,10 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
                               (long long)mxa_row_bytes(types[i], in_features), y + c0, outs[i]};
       c0 += outs[i];
     }
-    if (mxa::launch_decode_multi(seg, n, act, total, n_tokens, s) == 0) return check_launch();
+    const int st = n_tokens <= mxa::kFusedQuantMaxRows
+                       ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
+                       : mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
+    if (st == 0) return check_launch();
   }
   long long col = 0;
   for (int i = 0; i < n; ++i) {

@@ -73,20 +73,20 @@ __device__ __forceinline__ void wait_at_least(const int* p, int target) {
   while (lds_load(p) < target) __builtin_amdgcn_s_sleep(1);
 }
 
+// Workgroup `wg` of one packed weight: rows wg * R .. of it.
 template <int TYPE, int C>
-__global__ __launch_bounds__(768) void bstream_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                      float* __restrict__ y, long long ldy, int M,
-                                                      int N, BsGeo geo) {
+__device__ __forceinline__ void bstream_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
+                                             const Act& act, float* __restrict__ y, long long ldy,
+                                             int M, int N, const BsGeo& geo, int wg) {
   using Tile = typename TileOf<TYPE>::T;
   constexpr int TB = kBlockBytes<TYPE>;
   constexpr int kLaneCopies = (kTileCopies<TYPE> + kCopyWaves - 1) / kCopyWaves;
-  extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ncw = geo.ncw, nct = 64 * ncw;  // compute waves and their threads
   const int nb = act.nb;
-  const int r0 = blockIdx.x * geo.rows_per_wg;
+  const int r0 = wg * geo.rows_per_wg;
   const int rows = min(geo.rows_per_wg, N - r0);  // >= 1: the grid is ceil(N / R)
   const int T = (rows + 15) >> 4;
   const int rs = geo.rs, nbuf = geo.nbuf, buf_bytes = geo.buf_bytes, ntp = geo.ntp;
@@ -294,6 +294,47 @@ __global__ __launch_bounds__(768) void bstream_kernel(const uint8_t* w, long lon
 }
 
 template <int TYPE, int C>
+__global__ __launch_bounds__(768) void bstream_kernel(const uint8_t* w, long long row_bytes, Act act,
+                                                      float* __restrict__ y, long long ldy, int M,
+                                                      int N, BsGeo geo) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  bstream_rows<TYPE, C>(smem, w, row_bytes, act, y, ldy, M, N, geo, blockIdx.x);
+}
+
+// Several weights sharing the activations in one launch: workgroups wg0 .. of segment s take its
+// rows; each segment has its own rows per workgroup and stage geometry.
+constexpr int kMaxSegs = 4;
+struct BsSeg {
+  const uint8_t* w;
+  long long row_bytes;
+  float* y;  // the segment's first output column
+  int n, type, wg0, rows_per_wg, rs, buf_bytes;
+};
+struct BsSegs {
+  BsSeg s[kMaxSegs];
+  int count;
+};
+
+template <int C>
+__global__ __launch_bounds__(768) void bstream_multi_kernel(BsSegs segs, Act act, long long ldy, int M,
+                                                            BsGeo geo) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int wg = blockIdx.x;
+  int i = 0;
+  while (i + 1 < segs.count && wg >= segs.s[i + 1].wg0) ++i;
+  const BsSeg sg = segs.s[i];
+  BsGeo g = geo;
+  g.rows_per_wg = sg.rows_per_wg;
+  g.rs = sg.rs;
+  g.buf_bytes = sg.buf_bytes;
+  switch (sg.type) {
+    case T_Q4_K: bstream_rows<T_Q4_K, C>(smem, sg.w, sg.row_bytes, act, sg.y, ldy, M, sg.n, g, wg - sg.wg0); break;
+    case T_Q6_K: bstream_rows<T_Q6_K, C>(smem, sg.w, sg.row_bytes, act, sg.y, ldy, M, sg.n, g, wg - sg.wg0); break;
+    default: bstream_rows<T_Q8_0, C>(smem, sg.w, sg.row_bytes, act, sg.y, ldy, M, sg.n, g, wg - sg.wg0); break;
+  }
+}
+
+template <int TYPE, int C>
 int launch_bs(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
               int N, hipStream_t stream) {
   constexpr int kLdsMax = 160 * 1024;
@@ -339,6 +380,67 @@ int launch_bs_type(const uint8_t* w, long long row_bytes, const Act& act, float*
   return -1;
 }
 
+template <int TYPE>
+int stage_bytes_ok(long long row_bytes) {  // bytes of a tile's stage buffer, or -1
+  const int bytes = (16 * row_chunks(row_bytes) * 16 + 1023) / 1024 * 1024;
+  return bytes / 1024 > kTileCopies<TYPE> ? -1 : bytes;
+}
+
+template <int C>
+int launch_bs_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int M,
+                    hipStream_t stream) {
+  constexpr int kLdsMax = 160 * 1024;
+  const int nb = act.nb;
+  const int ncu = cu_count();
+  BsGeo geo;
+  geo.ncw = (nb + C - 1) / C;
+  if (count < 1 || count > kMaxSegs || geo.ncw + kCopyWaves > 12) return -1;
+  BsSegs segs;
+  segs.count = count;
+  int buf_max = 0;
+  double total = 0.0;
+  for (int i = 0; i < count; ++i) {
+    const int t = seg[i].type;
+    const int bytes = t == T_Q4_K ? stage_bytes_ok<T_Q4_K>(seg[i].row_bytes)
+                    : t == T_Q6_K ? stage_bytes_ok<T_Q6_K>(seg[i].row_bytes)
+                    : t == T_Q8_0 ? stage_bytes_ok<T_Q8_0>(seg[i].row_bytes) : -1;
+    if (bytes < 0) return -1;
+    buf_max = max(buf_max, bytes);
+    total += (double)seg[i].n * (double)seg[i].row_bytes;
+  }
+  auto lds_bytes = [&](int nbuf, int ntp) {
+    return nbuf * buf_max + ntp * nb * (256 + 16) * 4 + nb * 16 * 4 + kOutTiles * 256 * 4 +
+           kCtrlInts * 4;
+  };
+  geo.nbuf = 0;
+  const int pref[4][2] = {{3, 2}, {3, 1}, {2, 2}, {2, 1}};
+  for (int i = 0; i < 4 && geo.nbuf == 0; ++i)
+    if (lds_bytes(pref[i][0], pref[i][1]) <= kLdsMax) geo.nbuf = pref[i][0], geo.ntp = pref[i][1];
+  if (geo.nbuf == 0 || geo.nbuf * ((buf_max / 1024 + kCopyWaves - 1) / kCopyWaves) > kMaxCopies) return -1;
+  int wg0 = 0;
+  for (int i = 0; i < count; ++i) {
+    const int share = max(1, (int)((double)ncu * seg[i].n * seg[i].row_bytes / total + 0.5));
+    const int R = max(16, (seg[i].n + share - 1) / share);
+    const int t = seg[i].type;
+    segs.s[i] = BsSeg{seg[i].w, seg[i].row_bytes, seg[i].y, seg[i].n, t, wg0, R,
+                      row_chunks(seg[i].row_bytes),
+                      t == T_Q4_K ? stage_bytes_ok<T_Q4_K>(seg[i].row_bytes)
+                      : t == T_Q6_K ? stage_bytes_ok<T_Q6_K>(seg[i].row_bytes)
+                                    : stage_bytes_ok<T_Q8_0>(seg[i].row_bytes)};
+    wg0 += (seg[i].n + R - 1) / R;
+  }
+  const int lds = lds_bytes(geo.nbuf, geo.ntp);
+  static bool lds_set = false;
+  if (!lds_set) {
+    (void)hipFuncSetAttribute((const void*)bstream_multi_kernel<C>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((bstream_multi_kernel<C>), dim3(wg0), dim3(64 * (geo.ncw + kCopyWaves)), lds,
+                     stream, segs, act, ldy, M, geo);
+  return 0;
+}
+
 }  // namespace
 
 int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
@@ -350,6 +452,14 @@ int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& a
     case T_Q8_0: return launch_bs_type<T_Q8_0>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }
+}
+
+int launch_bstream_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy,
+                         int m_rows, hipStream_t stream) {
+  if (act.q == nullptr || m_rows < 1 || m_rows > 16) return -1;
+  if (act.nb <= 8) return launch_bs_multi<1>(seg, count, act, ldy, m_rows, stream);
+  if (act.nb <= 16) return launch_bs_multi<2>(seg, count, act, ldy, m_rows, stream);
+  return -1;
 }
 
 }  // namespace mxa

@@ -83,6 +83,11 @@ int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act
 int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// The streaming batched decode over up to 4 K-quant / Q8_0 weights that share the activations,
+// in one launch. -1 when the weights do not suit it.
+int launch_bstream_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
+                         hipStream_t stream);
+
 // IQ4_XS prefill on the matrix cores (m_rows >= kIq4MfmaMinRows): x split into bf16 hi / lo in
 // `workspace` (iq4_prefill_workspace bytes), then bf16 MFMAs per 32-value sub-block.
 constexpr int kIq4MfmaMinRows = 17;

@@ -183,13 +183,17 @@ def test_gemm_multi_equals_separate_calls(gpu) -> None:
         assert torch.equal(y, gpu.matmul(t, w, x, o, k))
 
 
-# Shared-input weights in one launch (decode, <= 4 tokens): the q/k/v and gate/up shapes of the
-# layer config at reduced N, mixed block types, row counts that leave partial workgroups.
+# Shared-input weights in one launch (decode, up to 16 tokens): the q/k/v and gate/up shapes of
+# the layer config at reduced N, mixed block types, row counts that leave partial workgroups.
 MULTI_CASES = [
     ([(D.Q4_K, 512), (D.Q4_K, 128), (D.Q6_K, 128)], 4096, 1),
     ([(D.Q4_K, 700), (D.Q4_K, 700)], 4096, 2),
     ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65), (D.Q4_K, 1)], 2048, 4),
     ([(D.Q6_K, 300), (D.Q8_0, 40)], 768, 3),
+    ([(D.Q4_K, 512), (D.Q4_K, 128), (D.Q6_K, 128)], 4096, 16),
+    ([(D.Q4_K, 700), (D.Q4_K, 700)], 4096, 8),
+    ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65), (D.Q4_K, 1)], 2048, 5),
+    ([(D.Q6_K, 300), (D.Q8_0, 40)], 768, 11),
 ]
 
 
