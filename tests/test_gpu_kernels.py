@@ -252,10 +252,12 @@ def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None
 
 # Shapes for the batched-decode streaming kernel (5..16 tokens): rows per workgroup = max(16,
 # N / CUs), so N = 4100 leaves a one-row tile and a three-row last workgroup, N = 5000 a four-row
-# tile; K = 2304 gives an odd block count (the last wave owns one block), K = 768 three waves,
-# K = 5120 and 8192 four blocks per wave; Q6_K rows of 210 x odd bytes start on 2-byte boundaries.
+# tile; K = 2304 gives an odd block count (the last wave owns one block), K = 768 three waves;
+# rows of more than 16 blocks stream in parts of 8 (K = 5120: a short last part; 14336: the down
+# projection's 56 blocks; 4352: Q6_K parts that start on 2-byte boundaries); Q6_K rows of 210 x
+# odd bytes start on 2-byte boundaries.
 BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
-                (5000, 1024, 16), (23, 768, 7), (260, 5120, 9)]
+                (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
