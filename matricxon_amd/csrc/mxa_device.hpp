@@ -143,6 +143,7 @@ struct Act {
   int k;
   int nb;
   void* xsplit;  // IQ4_XS prefill: workspace for the bf16 split of x (nullptr when not provided)
+  const uint8_t* ablk;  // prefill: the regrouped Q8_K activations (nullptr when not provided)
 };
 
 // ------------------------------------------------------------------ LDS copies and their waits
@@ -180,6 +181,10 @@ constexpr int kMaxCopies = 63;  // the largest vmcnt: copies a weight wave may h
 // vmcnt(0) before unrelated instructions); the kernel waits for these copies itself.
 __device__ __forceinline__ void copy16_to_lds(const void* g, uint32_t lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr) : "memory");
+}
+// The same from a wave-uniform base plus a 32-bit per-lane byte offset (no 64-bit address math).
+__device__ __forceinline__ void copy16_to_lds_s(const void* base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
 // Grid-order tile index for workgroup `wg` of `n_wg` such that consecutive tiles land on the same

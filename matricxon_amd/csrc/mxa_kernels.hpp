@@ -40,6 +40,16 @@ inline ActBuffers act_layout(void* ws, int m_rows, int k) {
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream);
 
+// Prefill (m_rows >= kPrefillMinRows): the Q8_K activations regrouped per tile of kPrefillRows
+// rows and per block into one contiguous stage [q rows, padded to kPrefillQStride][bsums fp16]
+// [d], so that the streaming prefill kernel copies a stage with whole 1 KB copies.
+constexpr int kPrefillMinRows = 1024;
+constexpr int kPrefillRows = 64;
+constexpr int kPrefillQStride = QK + 16;  // padded row: the 16 rows of an MFMA read hit distinct banks
+constexpr int kPrefillStageBytes = kPrefillRows * (kPrefillQStride + 32 + 4);
+size_t act_blocked_bytes(int m_rows, int k);
+void launch_act_blocked(const ActBuffers& a, void* out, int m_rows, int k, hipStream_t stream);
+
 int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long n_src_rows,
                    long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
                    hipStream_t stream);
@@ -83,10 +93,21 @@ int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act
 int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Batched decode (m_rows <= 16, rows of up to 16 blocks) with each workgroup's share of the weight
+// rows resident in LDS (requested at launch, one hand-over per 16-row tile): Q4_K, Q6_K, Q8_0 on
+// Q8_K activations in the workspace. -1 when the share does not fit.
+int launch_bres(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 // The streaming batched decode over up to 4 K-quant / Q8_0 weights that share the activations,
 // in one launch. -1 when the weights do not suit it.
 int launch_bstream_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
                          hipStream_t stream);
+
+// Streaming prefill on the matrix cores (Q4_K; m_rows >= kPrefillMinRows) on the regrouped
+// activations in act.ablk. -1 when it does not apply.
+int launch_ptile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // IQ4_XS prefill on the matrix cores (m_rows >= kIq4MfmaMinRows): x split into bf16 hi / lo in
 // `workspace` (iq4_prefill_workspace bytes), then bf16 MFMAs per 32-value sub-block.

@@ -306,6 +306,7 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
                    int M, int N, hipStream_t stream) {
   // M <= 16: the streaming kernel, else the block-split kernel unless the 64-row tiles alone give
   // >= 512 workgroups
+  if (M <= 16 && launch_bres(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && launch_bstream(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && N < 512 * 64) {
     constexpr int RT = TYPE == T_Q6_K ? 1 : 2;
@@ -317,6 +318,7 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
   // per workgroup; Q6_K / Q8_0 keep 64 weight rows (their B operands need twice the registers)
   if (M <= 64) return launch_mt<TYPE, 1, 1>(w, row_bytes, act, y, ldy, M, N, stream);
   constexpr int NT = 1;
+  if (M >= kPrefillMinRows && launch_ptile(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   return launch_mt<TYPE, 4, NT>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 

@@ -52,6 +52,15 @@ __device__ __forceinline__ f16x4 bsums_f16x4(const int16_t* p) {
                (_Float16)(float)(int16_t)(v.y & 0xFFFFu), (_Float16)(float)(int16_t)(v.y >> 16)};
 }
 
+// The lane-group mask of a B operand, built where it is used. `fresh` hides the operand from
+// common-subexpression elimination, so a caller that feeds one weight tile to many activation
+// tiles rebuilds the 16 masked operands per tile instead of keeping them all live.
+template <bool kFresh>
+__device__ __forceinline__ i32x4 masked_b(u32x4a4 v, bool on) {
+  if constexpr (kFresh) asm volatile("" : "+v"(v));
+  return as_i32x4(on ? v.x : 0u, on ? v.y : 0u, on ? v.z : 0u, on ? v.w : 0u);
+}
+
 // Activation chunk in LDS: q8 rows, bsums (as fp16) and scales of 16 * MT rows x kCB blocks.
 struct ActTile {
   const int8_t* q;        // row r at q + r * qs, block bb at + bb * QK
@@ -136,7 +145,7 @@ struct TileQ4 {
     f.bs = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
     return f;
   }
-  template <class S>
+  template <bool kFresh = false, class S>
   __device__ static void value(const P& p, const F& f, int, S&& sink) {
     i32x4 sum = {0, 0, 0, 0};
 #pragma unroll
@@ -254,7 +263,7 @@ struct TileQ6 {
     f.bs = *(const f16x4*)(A.bs + (16 * mt + ln) * A.bst + bb * 16 + 4 * g);
     return f;
   }
-  template <class S>
+  template <bool kFresh = false, class S>
   __device__ static void value(const P& p, const F& f, int g, S&& sink) {
     int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -262,7 +271,7 @@ struct TileQ6 {
 #pragma unroll
       for (int g2 = 0; g2 < 4; ++g2) {
         const bool on = g == g2;  // B restricted to lane group g2: one sub-block's dot
-        const i32x4 b = as_i32x4(on ? p.bu[t].x : 0u, on ? p.bu[t].y : 0u, on ? p.bu[t].z : 0u, on ? p.bu[t].w : 0u);
+        const i32x4 b = masked_b<kFresh>(p.bu[t], on);
         const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], b, i32x4{0, 0, 0, 0}, 0, 0, 0);
         // |D| <= 16 * 63 * 127 < 2^17, |sc| <= 128: 24-bit products
 #pragma unroll
@@ -348,7 +357,7 @@ struct TileQ8 {
     for (int t = 0; t < 4; ++t) f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(arow + 16 * t));
     return f;
   }
-  template <class S>
+  template <bool kFresh = false, class S>
   __device__ static void value(const P& p, const F& f, int g, S&& sink) {
     float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -359,7 +368,7 @@ struct TileQ8 {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int t = 2 * h + tt;
-        const i32x4 b = as_i32x4(on ? p.qb[t].x : 0u, on ? p.qb[t].y : 0u, on ? p.qb[t].z : 0u, on ? p.qb[t].w : 0u);
+        const i32x4 b = masked_b<kFresh>(p.qb[t], on);
         D = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], b, D, 0, 0, 0);
       }
 #pragma unroll

@@ -255,9 +255,13 @@ def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None
 # tile; K = 2304 gives an odd block count (the last wave owns one block), K = 768 three waves;
 # rows of more than 16 blocks stream in parts of 8 (K = 5120: a short last part; 14336: the down
 # projection's 56 blocks; 4352: Q6_K parts that start on 2-byte boundaries); Q6_K rows of 210 x
-# odd bytes start on 2-byte boundaries.
+# odd bytes start on 2-byte boundaries. Rows of up to 16 blocks whose workgroup share fits LDS run
+# resident (N = 14336: 56 rows, a half last tile; Q6_K / Q8_0 at N = 8192: two tiles; 3000 x
+# 2304: 12 rows per workgroup, odd block count; 14000 x 512: 55 rows of 2 blocks), larger ones
+# stream.
 BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
-                (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6)]
+                (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6),
+                (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
@@ -268,8 +272,25 @@ def test_batched_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m)
     check_gemm(gpu, oracle, ggml_type, w, x, n, k)
 
 
+# Prefill: 64-row activation tiles, and from 1024 rows the Q4_K streaming kernel (128 x 64 tiles):
+# N below, at and past whole 128-row tiles, M at and past whole 64-row tiles (rows past M repeat
+# row M - 1 in the regrouped activations), odd and long block counts (K = 2304: 9 blocks, 14336:
+# 56).
+PREFILL_SHAPES = [(129, 768, 128), (260, 2048, 200), (300, 4096, 130), (50, 14336, 140),
+                  (513, 2304, 257), (1000, 4096, 320), (300, 2048, 1030), (129, 1024, 1100),
+                  (50, 4352, 1024), (513, 2304, 1089)]
+
+
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
-@pytest.mark.parametrize("n,k,m", [(130, 256, 4), (5, 16640, 3), (70, 4096, 1)])
+@pytest.mark.parametrize("n,k,m", PREFILL_SHAPES)
+def test_prefill_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None:
+    w = S.packed_weight(ggml_type, n, k, seed=n * 5 + k + m)
+    x = S.activations(m, k, seed=m * 7 + n)
+    check_gemm(gpu, oracle, ggml_type, w, x, n, k)
+
+
+@pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
+@pytest.mark.parametrize("n,k,m", [(130, 256, 4), (5, 16640, 3), (70, 4096, 1), (70, 512, 130)])
 def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> None:
     """The same kernel reading Q8_K activations from the workspace instead of quantizing them."""
     from matricxon_amd.gemm import q8k_bytes
@@ -284,10 +305,12 @@ def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> 
     assert np.array_equal(bits(got), bits(want))
 
 
-def test_gemm_multi_mixed_types_prefill(gpu, oracle) -> None:
-    """Q8_K-based and IQ4_XS weights sharing one prefill-sized input: the workspace holds both
-    the Q8_K activations and the bf16 split of x, and every output equals its separate call."""
-    k, m = 1024, 20
+@pytest.mark.parametrize("m", [20, 150, 1030])
+def test_gemm_multi_mixed_types_prefill(gpu, oracle, m) -> None:
+    """Q8_K-based and IQ4_XS weights sharing one prefill-sized input: the workspace holds the
+    Q8_K activations, from 1024 rows their regrouped copy (Q4_K), and the bf16 split of x, and
+    every output equals its separate call."""
+    k = 1024
     items = [(D.Q4_K, 48), (D.IQ4_XS, 32), (D.Q6_K, 16)]
     ws = [dev(S.packed_weight(t, o, k, seed=40 + i)) for i, (t, o) in enumerate(items)]
     x_np = S.activations(m, k, seed=12)
