@@ -190,9 +190,13 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
                               (long long)mxa_row_bytes(types[i], in_features), y + c0, outs[i]};
       c0 += outs[i];
     }
-    const int st = n_tokens <= mxa::kFusedQuantMaxRows
-                       ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
-                       : mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
+    int st = -1;
+    if (n_tokens <= mxa::kFusedQuantMaxRows) {
+      st = mxa::launch_decode_multi(seg, n, act, total, n_tokens, s);
+    } else {
+      st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+      if (st != 0) st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
+    }
     if (st == 0) return check_launch();
   }
   long long col = 0;

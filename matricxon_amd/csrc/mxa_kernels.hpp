@@ -93,11 +93,14 @@ int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act
 int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
-// Batched decode (m_rows <= 16, rows of up to 16 blocks) with each workgroup's share of the weight
-// rows resident in LDS (requested at launch, one hand-over per 16-row tile): Q4_K, Q6_K, Q8_0 on
-// Q8_K activations in the workspace. -1 when the share does not fit.
+// Batched decode (m_rows <= 16, rows of up to 16 blocks) with each workgroup's weight rows
+// streamed through LDS in 16-row tiles, in order: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
+// workspace. -1 when the geometry does not fit (the caller uses launch_bstream).
 int launch_bres(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
+// The same over up to 4 weights sharing the activations, in one launch.
+int launch_bres_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
+                      hipStream_t stream);
 
 // The streaming batched decode over up to 4 K-quant / Q8_0 weights that share the activations,
 // in one launch. -1 when the weights do not suit it.

@@ -194,6 +194,10 @@ MULTI_CASES = [
     ([(D.Q4_K, 700), (D.Q4_K, 700)], 4096, 8),
     ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65), (D.Q4_K, 1)], 2048, 5),
     ([(D.Q6_K, 300), (D.Q8_0, 40)], 768, 11),
+    # gate|up shape: 112 rows per workgroup, 7 tiles through 4 LDS tile slots
+    ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 16),
+    # q|k|v shape: segments of different types and tile counts
+    ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 9),
 ]
 
 
@@ -257,11 +261,13 @@ def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None
 # projection's 56 blocks; 4352: Q6_K parts that start on 2-byte boundaries); Q6_K rows of 210 x
 # odd bytes start on 2-byte boundaries. Rows of up to 16 blocks whose workgroup share fits LDS run
 # resident (N = 14336: 56 rows, a half last tile; Q6_K / Q8_0 at N = 8192: two tiles; 3000 x
-# 2304: 12 rows per workgroup, odd block count; 14000 x 512: 55 rows of 2 blocks), larger ones
-# stream.
+# 2304: 12 rows per workgroup, odd block count; 14000 x 512: 55 rows of 2 blocks); more tiles than
+# LDS slots cycle through them (30000 x 4096: 8 tiles; 40000 x 2048: 10 tiles, Q4_K in 8 slots;
+# 50000 x 4096: 13 tiles); rows of more than 16 blocks stream.
 BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
                 (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6),
-                (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10)]
+                (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10),
+                (30000, 4096, 9), (40000, 2048, 5), (50000, 4096, 16)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
