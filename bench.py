@@ -154,7 +154,7 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
         del ws
 
     gemv("cfg1 Q8_0 4096x4096", 8, 4096, 4096, [1], 11)
-    gemv("cfg2 Q4_K 14336x4096", 12, 14336, 4096, [1, 4, 8, 16], 12)
+    gemv("cfg2 Q4_K 14336x4096", 12, 14336, 4096, [1, 2, 3, 4, 8, 16], 12)
     gemv("cfg3 Q6_K 128256x4096", 14, 128256, 4096, [1, 16], 13)
     # q, k (Q4_K), v (Q6_K), o, gate, up (Q4_K), down (Q6_K)
     layer = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096), (12, 4096, 4096),

@@ -50,7 +50,7 @@ int mxa_supports(int ggml_type, int in_features);
 size_t mxa_row_bytes(int ggml_type, int in_features);
 
 /* Workspace bytes mxa_gemm needs for n_tokens rows of in_features. Q8_0 / Q4_K / Q6_K: the Q8_K
- * activation blocks, or 0 for up to 4 rows (the matmul kernel quantizes them in on-chip memory
+ * activation blocks, or 0 for up to 3 rows (the matmul kernel quantizes them in on-chip memory
  * itself); Q4_K from 1024 rows adds a second copy of them regrouped per 64-row tile and block (the
  * streaming prefill kernel's input). IQ4_XS: 0 for up to 16 rows; from 17 rows (prefill on the
  * matrix cores) the bf16 hi / lo split of x, 4 * n_tokens * in_features bytes. mxa_gemm_multi
@@ -60,7 +60,7 @@ size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features);
 /* y (n_tokens, out_features) fp32 = x (n_tokens, in_features) fp32 @ W.T, W the packed rows
  * (out_features, row_bytes) in GGUF order. The activations are quantized to Q8_K exactly as the
  * reference C kernel does (except IQ4_XS, which uses them as floats): into `workspace` first,
- * or, for n_tokens <= 4, inside the matmul kernel (one launch, no workspace).
+ * or, for n_tokens <= 3, inside the matmul kernel (one launch, no workspace).
  * Replaces `mx_gemm` (app/native/src/mx_gemm.c:219-288) and, on the GPU, the dequantize +
  * F.linear of `DevicePackedLinear.forward` (app/architectures/device_packed.py:53-63). */
 int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_tokens,

@@ -39,7 +39,7 @@ bool needs_q8k(int t) { return t != MXA_TYPE_IQ4_XS; }
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 // Up to this many activation rows the matmul kernel quantizes x itself (no workspace).
-bool fused_quant(int n_tokens) { return n_tokens <= mxa::kFusedQuantMaxRows; }
+bool fused_quant(int n_tokens) { return n_tokens <= mxa::kDecodeMaxRows; }
 
 mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
   mxa::Act act;
@@ -191,7 +191,7 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
       c0 += outs[i];
     }
     int st = -1;
-    if (n_tokens <= mxa::kFusedQuantMaxRows) {
+    if (n_tokens <= mxa::kDecodeMaxRows) {
       st = mxa::launch_decode_multi(seg, n, act, total, n_tokens, s);
     } else {
       st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);

@@ -57,7 +57,10 @@ int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long
 // Compute units of the current device (cached after the first call).
 int cu_count();
 
-// Activation rows up to which the matmul kernels quantize x themselves (no workspace).
+// Activation rows up to which the pipelined decode kernel takes a matrix, quantizing x itself (no
+// workspace): K-quant / Q8_0 weights, and IQ4_XS (which reads x as floats; larger decode batches
+// run in passes of this many rows).
+constexpr int kDecodeMaxRows = 3;
 constexpr int kFusedQuantMaxRows = 4;
 
 // Decode GEMV for 1 <= m_rows <= 4: y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of

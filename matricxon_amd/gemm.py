@@ -173,8 +173,8 @@ class HipGemm:
                      out: torch.Tensor | None = None) -> list[torch.Tensor]:
         """`items`: (ggml_type, packed, out_features) per weight sharing input `x`
         (n_tokens, in_features): one activation quantization, one float32 output per weight,
-        as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them. For up to 4 tokens
-        and K-quant / Q8_0 weights this is a single kernel launch. `out`, if given, is the
+        as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them. For up to 16 tokens
+        and K-quant / Q8_0 weights of up to 16 blocks per row this is a single matmul launch. `out`, if given, is the
         float32 (n_tokens, sum of out_features) result buffer the outputs are views of."""
         import ctypes
 

@@ -58,7 +58,8 @@ def test_supports_and_sizes(lib) -> None:
     # Q8_K workspace: q (M*K) | d (M*nb*4) | bsums (M*nb*32), each 256-aligned
     assert lib.mxa_workspace_bytes(12, 16, 4096) == 65536 + 1024 + 8192
     assert lib.mxa_workspace_bytes(12, 5, 256) == 1280 + 256 + 256
-    assert lib.mxa_workspace_bytes(12, 4, 4096) == 0  # quantized inside the matmul kernel
+    assert lib.mxa_workspace_bytes(12, 3, 4096) == 0  # quantized inside the matmul kernel
+    assert lib.mxa_workspace_bytes(12, 4, 4096) == 16384 + 256 + 2048
     assert lib.mxa_workspace_bytes(23, 16, 4096) == 0  # IQ4_XS reads float activations
     assert lib.mxa_workspace_bytes(23, 17, 4096) == 17 * 4096 * 4  # prefill: bf16 hi/lo of x
 
