@@ -21,7 +21,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte aligned
 
-constexpr int kRowsPerWg = 64;             // weight rows per workgroup (16 per wave)
 constexpr int kXStride = QK * 2 + 16;      // LDS bytes per activation row (bf16), padded
 
 // bf16 bits of x rounded to nearest even (NaN stays NaN, overflow gives +-Inf).
@@ -81,18 +80,29 @@ __device__ __forceinline__ IQ4W load_iq4(const uint8_t* row, int b, int g) {
   return L;
 }
 
+// A workgroup takes 128 weight rows (8 waves of 16) x 16 MT activation rows. The activations of a
+// block (bf16 hi and lo, 2 x 512 B per row) go to one of two LDS buffers: the next block's are
+// loaded into registers while the current block is computed and written to the other buffer
+// afterwards, so one barrier per block suffices (a buffer is rewritten only after every wave has
+// passed the barrier that ends its last use). Per sub-block t the B operand is the grid values of
+// elements 32 t + 8 g .. of row n; one MFMA pair (hi, then lo) gives sum(K * x), scaled by dl in
+// fp32, sub-blocks and blocks in order.
+constexpr int kIq4Waves = 8;
+constexpr int kIq4WgRows = 16 * kIq4Waves;
+
 template <int MT>
-__global__ __launch_bounds__(256) void iq4_mtile_kernel(const uint8_t* w, long long row_bytes,
-                                                        const uint16_t* __restrict__ xh,
-                                                        const uint16_t* __restrict__ xl, int K,
-                                                        float* __restrict__ y, long long ldy, int M,
-                                                        int N) {
+__global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t* w, long long row_bytes,
+                                                                   const uint16_t* __restrict__ xh,
+                                                                   const uint16_t* __restrict__ xl,
+                                                                   int K, float* __restrict__ y,
+                                                                   long long ldy, int M, int N) {
   constexpr int kRows = 16 * MT;
-  __shared__ __align__(16) uint8_t Xh[kRows * kXStride];
-  __shared__ __align__(16) uint8_t Xl[kRows * kXStride];
+  constexpr int kBuf = 2 * kRows * kXStride;                  // hi rows, then lo rows
+  constexpr int kPieces = kRows * 64 / (64 * kIq4Waves);      // 16-byte pieces per thread
+  extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ln = lane & 15, g = lane >> 4;
-  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * kRowsPerWg + 16 * wave;
+  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * kIq4WgRows + 16 * wave;
   const int m0 = blockIdx.y * kRows;
   const uint8_t* row = w + (size_t)min(n0 + ln, N - 1) * row_bytes;
   const int nb = K / QK;
@@ -100,18 +110,35 @@ __global__ __launch_bounds__(256) void iq4_mtile_kernel(const uint8_t* w, long l
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  IQ4W cur = load_iq4(row, 0, g), nxt;
-  for (int b = 0; b < nb; ++b) {
-    // 1. the block's activations (bf16 hi / lo) into LDS; rows >= M repeat row M - 1
-    for (int p = tid; p < kRows * 64; p += 256) {  // 16-byte pieces: 32 per row of hi, 32 of lo
-      const int r = p >> 6, pc = p & 63, part = pc >> 5, q = pc & 31;
+  // thread tid stages pieces p = tid + 512 i: row p / 64, hi (p % 64 < 32) or lo, piece p % 32;
+  // rows >= M repeat row M - 1
+  u32x4a4 stage[kPieces];
+  auto load_x = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+      const int p = tid + 64 * kIq4Waves * i, r = p >> 6, pc = p & 63, part = pc >> 5, q = pc & 31;
       const size_t src = (size_t)min(m0 + r, M - 1) * K + (size_t)b * QK;
-      const uint16_t* sp = (part ? xl : xh) + src;
-      *(u32x4a4*)((part ? Xl : Xh) + r * kXStride + 16 * q) = ld16((const uint8_t*)sp + 16 * q);
+      stage[i] = ld16((const uint8_t*)((part ? xl : xh) + src) + 16 * q);
     }
-    if (b + 1 < nb) nxt = load_iq4(row, b + 1, g);
-    __syncthreads();
-    // 2. the block: per sub-block t, B = grid values of elements 32 t + 8 g .. of row n
+  };
+  auto store_x = [&](uint8_t* buf) {
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+      const int p = tid + 64 * kIq4Waves * i, r = p >> 6, pc = p & 63, part = pc >> 5, q = pc & 31;
+      *(u32x4a4*)(buf + part * kRows * kXStride + r * kXStride + 16 * q) = stage[i];
+    }
+  };
+  IQ4W cur = load_iq4(row, 0, g), nxt;
+  load_x(0);
+  store_x(smem);
+  __syncthreads();
+  for (int b = 0; b < nb; ++b) {
+    if (b + 1 < nb) {
+      load_x(b + 1);
+      nxt = load_iq4(row, b + 1, g);
+    }
+    const uint8_t* Xh = smem + (b & 1) * kBuf;
+    const uint8_t* Xl = Xh + kRows * kXStride;
     const float d = half_to_float(cur.hdr[0]);
     const uint32_t sh = cur.hdr[0] >> 16, sl = cur.hdr[1];
 #pragma unroll
@@ -131,9 +158,13 @@ __global__ __launch_bounds__(256) void iq4_mtile_kernel(const uint8_t* w, long l
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(dl, D[i], acc[mt][i]);
       }
+      __builtin_amdgcn_sched_barrier(0);  // one sub-block's operands live at a time
+    }
+    if (b + 1 < nb) {
+      store_x(smem + ((b + 1) & 1) * kBuf);
+      cur = nxt;
     }
     __syncthreads();
-    cur = nxt;
   }
   const int n = n0 + ln;
 #pragma unroll
@@ -157,9 +188,15 @@ int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, vo
   hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, x, hi,
                      lo, n4);
   constexpr int MT = 4;
-  const dim3 grid((n_rows + kRowsPerWg - 1) / kRowsPerWg, (m_rows + 16 * MT - 1) / (16 * MT));
-  hipLaunchKernelGGL(iq4_mtile_kernel<MT>, grid, dim3(256), 0, stream, w, row_bytes, hi, lo, k, y,
-                     ldy, m_rows, n_rows);
+  constexpr int kLds = 2 * 2 * 16 * MT * kXStride;
+  static bool lds_set = false;
+  if (!lds_set) {
+    (void)hipFuncSetAttribute((const void*)iq4_mtile_kernel<MT>, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    lds_set = true;
+  }
+  const dim3 grid((n_rows + kIq4WgRows - 1) / kIq4WgRows, (m_rows + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL(iq4_mtile_kernel<MT>, grid, dim3(64 * kIq4Waves), kLds, stream, w, row_bytes, hi,
+                     lo, k, y, ldy, m_rows, n_rows);
   return 0;
 }
 
