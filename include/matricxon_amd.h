@@ -51,10 +51,9 @@ size_t mxa_row_bytes(int ggml_type, int in_features);
 
 /* Workspace bytes mxa_gemm needs for n_tokens rows of in_features. Q8_0 / Q4_K / Q6_K: the Q8_K
  * activation blocks, or 0 for up to 3 rows (the matmul kernel quantizes them in on-chip memory
- * itself); Q4_K from 1024 rows adds a second copy of them regrouped per 64-row tile and block (the
- * streaming prefill kernel's input). IQ4_XS: 0 for up to 16 rows; from 17 rows (prefill on the
- * matrix cores) the bf16 hi / lo split of x, 4 * n_tokens * in_features bytes. mxa_gemm_multi
- * over both kinds needs the sum of the largest of each kind. Host-only. */
+ * itself). IQ4_XS: 0 for up to 16 rows; from 17 rows (prefill on the matrix cores) the bf16
+ * hi / lo split of x, 4 * n_tokens * in_features bytes. mxa_gemm_multi over both kinds needs the
+ * sum of the largest of each kind. Host-only. */
 size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features);
 
 /* y (n_tokens, out_features) fp32 = x (n_tokens, in_features) fp32 @ W.T, W the packed rows

@@ -50,19 +50,13 @@ mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
   act.k = k;
   act.nb = k / mxa::QK;
   act.xsplit = nullptr;
-  act.ablk = nullptr;
   return act;
 }
 
 // Workspace parts, each 256-byte aligned: the Q8_K activations (types other than IQ4_XS, more than
-// kFusedQuantMaxRows rows), their copy regrouped per row tile and block (Q4_K, kPrefillMinRows
-// rows or more: the streaming prefill kernel's input), the bf16 split of x (IQ4_XS,
-// kIq4MfmaMinRows rows or more).
+// kDecodeMaxRows rows), then the bf16 split of x (IQ4_XS, kIq4MfmaMinRows rows or more).
 size_t q8k_part(bool any_q8k, int n_tokens, int k) {
   return any_q8k && !fused_quant(n_tokens) ? mxa::align256(mxa::act_bytes(n_tokens, k)) : 0;
-}
-size_t blk_part(bool any_q4k, int n_tokens, int k) {
-  return any_q4k && n_tokens >= mxa::kPrefillMinRows ? mxa::align256(mxa::act_blocked_bytes(n_tokens, k)) : 0;
 }
 size_t split_part(bool any_iq4, int n_tokens, int k) {
   return any_iq4 && n_tokens >= mxa::kIq4MfmaMinRows ? mxa::iq4_prefill_workspace(n_tokens, k) : 0;
@@ -90,8 +84,7 @@ size_t mxa_row_bytes(int ggml_type, int in_features) {
 size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features) {
   if (!mxa_supports(ggml_type, in_features) || n_tokens <= 0) return 0;
   if (needs_q8k(ggml_type))
-    return q8k_part(true, n_tokens, in_features) +
-           blk_part(ggml_type == MXA_TYPE_Q4_K, n_tokens, in_features);
+    return q8k_part(true, n_tokens, in_features);
   return split_part(true, n_tokens, in_features);
 }
 
@@ -148,7 +141,7 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
     return MXA_ERR_UNSUPPORTED;
   if (x == nullptr || y == nullptr || n_tokens <= 0 || !aligned(x, 16) || !aligned(workspace, 16))
     return MXA_ERR_UNSUPPORTED;
-  bool any_q8k = false, any_iq4 = false, any_q4k = false;
+  bool any_q8k = false, any_iq4 = false;
   long long total = 0;
   for (int i = 0; i < n; ++i) {
     if (!mxa_supports(types[i], in_features) || ws[i] == nullptr || outs[i] <= 0 ||
@@ -156,14 +149,12 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
       return MXA_ERR_UNSUPPORTED;
     any_q8k |= needs_q8k(types[i]);
     any_iq4 |= !needs_q8k(types[i]);
-    any_q4k |= types[i] == MXA_TYPE_Q4_K;
     total += outs[i];
   }
   hipStream_t s = (hipStream_t)stream;
   const size_t q8k_bytes = q8k_part(any_q8k, n_tokens, in_features);
-  const size_t blk_bytes = blk_part(any_q4k, n_tokens, in_features);
   const size_t split_bytes = split_part(any_iq4, n_tokens, in_features);
-  const size_t need = q8k_bytes + blk_bytes + split_bytes;
+  const size_t need = q8k_bytes + split_bytes;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MXA_ERR_WORKSPACE;
   mxa::ActBuffers buf{};
   const mxa::ActBuffers* abuf = nullptr;
@@ -171,17 +162,11 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
     buf = mxa::act_layout(workspace, n_tokens, in_features);
     abuf = &buf;
     mxa::launch_quantize_q8k(x, buf, n_tokens, in_features, s);
-    int st = check_launch();
+    const int st = check_launch();
     if (st != MXA_OK) return st;
-    if (blk_bytes > 0) {
-      mxa::launch_act_blocked(buf, (uint8_t*)workspace + q8k_bytes, n_tokens, in_features, s);
-      st = check_launch();
-      if (st != MXA_OK) return st;
-    }
   }
   mxa::Act act = make_act(x, abuf, in_features);
-  if (blk_bytes > 0) act.ablk = (const uint8_t*)workspace + q8k_bytes;
-  if (split_bytes > 0) act.xsplit = (uint8_t*)workspace + q8k_bytes + blk_bytes;
+  if (split_bytes > 0) act.xsplit = (uint8_t*)workspace + q8k_bytes;
   if (n > 1 && !any_iq4 && n_tokens <= 16) {  // decode: one launch for all weights
     mxa::DecodeSeg seg[4];
     long long c0 = 0;

@@ -143,7 +143,6 @@ struct Act {
   int k;
   int nb;
   void* xsplit;  // IQ4_XS prefill: workspace for the bf16 split of x (nullptr when not provided)
-  const uint8_t* ablk;  // prefill: the regrouped Q8_K activations (nullptr when not provided)
 };
 
 // ------------------------------------------------------------------ LDS copies and their waits

@@ -40,15 +40,6 @@ inline ActBuffers act_layout(void* ws, int m_rows, int k) {
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream);
 
-// Prefill (m_rows >= kPrefillMinRows): the Q8_K activations regrouped per tile of kPrefillRows
-// rows and per block into one contiguous stage [q rows, padded to kPrefillQStride][bsums fp16]
-// [d], so that the streaming prefill kernel copies a stage with whole 1 KB copies.
-constexpr int kPrefillMinRows = 1024;
-constexpr int kPrefillRows = 64;
-constexpr int kPrefillQStride = QK + 16;  // padded row: the 16 rows of an MFMA read hit distinct banks
-constexpr int kPrefillStageBytes = kPrefillRows * (kPrefillQStride + 32 + 4);
-size_t act_blocked_bytes(int m_rows, int k);
-void launch_act_blocked(const ActBuffers& a, void* out, int m_rows, int k, hipStream_t stream);
 
 int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long n_src_rows,
                    long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
@@ -109,11 +100,6 @@ int launch_bres_multi(const DecodeSeg* seg, int count, const Act& act, long long
 // in one launch. -1 when the weights do not suit it.
 int launch_bstream_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
                          hipStream_t stream);
-
-// Streaming prefill on the matrix cores (Q4_K; m_rows >= kPrefillMinRows) on the regrouped
-// activations in act.ablk. -1 when it does not apply.
-int launch_ptile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
-                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // IQ4_XS prefill on the matrix cores (m_rows >= kIq4MfmaMinRows): x split into bf16 hi / lo in
 // `workspace` (iq4_prefill_workspace bytes), then bf16 MFMAs per 32-value sub-block.

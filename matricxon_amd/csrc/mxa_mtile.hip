@@ -1,10 +1,13 @@
 // Matrix-core matmul for M > 4 activation rows (batched decode and prefill), Q4_K / Q6_K / Q8_0.
 //
-// Tiling. A workgroup of 4 waves owns 16 consecutive weight rows per wave and 16 * MT activation
-// rows; grid.y walks the activation rows, so a weight block is read once per 16 * MT activation
-// rows. The Q8_K activations (always pre-quantized in the workspace here) are staged in LDS per
-// chunk of kCB blocks; each wave keeps its rows' blocks of the next chunk in registers while it
-// computes the current one.
+// Tiling. A workgroup of WAVES waves owns 16 * NT consecutive weight rows per wave and 16 * MT
+// activation rows; grid.y walks the activation rows, so a weight block is read once per 16 * MT
+// activation rows and an activation chunk once per 16 * NT * WAVES weight rows. The Q8_K
+// activations (always pre-quantized in the workspace here) are staged in LDS per chunk of kCB
+// blocks, in two buffers: the next chunk is loaded into registers while the current one is
+// computed and written to the other buffer afterwards, so one barrier per chunk suffices (a
+// buffer is rewritten only after every wave has passed the barrier that ends its last use). Each
+// wave loads its rows' next block while it computes the current one.
 //
 // Operands: the tile builders of mxa_tiles.hpp, with A (16 activation rows x 64 k) read from LDS.
 // The blocks are folded in order 0..nb-1, so the outputs equal the oracle and the decode kernels
@@ -22,20 +25,27 @@ constexpr int kQStride = kCB * QK + 16;   // LDS bytes per activation row (paddi
 constexpr int kBStride = kCB * 16 + 8;    // LDS halves per activation row of bsums
 
 
-// Row-tiled kernel: MT activation tiles x NT weight tiles of 16 rows per wave, 4 waves.
-template <int TYPE, int MT, int NT>
-__global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                    float* __restrict__ y, long long ldy, int M, int N) {
+// LDS bytes of one activation chunk buffer for 16 * MT rows: q8 | bsums (fp16) | d.
+template <int MT>
+constexpr int kMtBuf = ((16 * MT * kQStride + 16 * MT * kBStride * 2 + kCB * 16 * MT * 4) + 15) / 16 * 16;
+
+// Row-tiled kernel: MT activation tiles x NT weight tiles of 16 rows per wave, WAVES waves.
+template <int TYPE, int MT, int NT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, long long row_bytes, Act act,
+                                                           float* __restrict__ y, long long ldy, int M,
+                                                           int N) {
   using Tile = typename TileOf<TYPE>::T;
   using W = typename Tile::W;
   constexpr int kRows = 16 * MT;
-  __shared__ __align__(16) int8_t Aq[kRows * kQStride];
-  __shared__ __align__(16) _Float16 Ab[kRows * kBStride];
-  __shared__ __align__(16) float Ad[kCB * kRows];
+  constexpr int kThreads = 64 * WAVES;
+  extern __shared__ __align__(16) uint8_t smem[];  // two chunk buffers of kMtBuf<MT> bytes
+  auto aq = [&](int buf) { return (int8_t*)(smem + buf * kMtBuf<MT>); };
+  auto ab = [&](int buf) { return (_Float16*)(smem + buf * kMtBuf<MT> + kRows * kQStride); };
+  auto ad = [&](int buf) { return (float*)(smem + buf * kMtBuf<MT> + kRows * kQStride + kRows * kBStride * 2); };
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ln = lane & 15, g = lane >> 4;
-  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * 4 * 16 * NT + 16 * NT * wave;
+  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * WAVES * 16 * NT + 16 * NT * wave;
   const int m0 = blockIdx.y * kRows;
   const uint8_t* row[NT];
 #pragma unroll
@@ -58,10 +68,10 @@ __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long 
   // every chunk (rows >= M repeat row M - 1, blocks >= cn repeat the chunk's last block: those
   // results are never stored).
   constexpr int kQPieces = kRows * kCB * 16;                   // 16-byte pieces of q8
-  constexpr int kQPer = (kQPieces + 255) / 256;
+  constexpr int kQPer = (kQPieces + kThreads - 1) / kThreads;
   constexpr int kBPieces = kRows * kCB * 2;                    // halves of a block's 16 bsums
-  constexpr int kBPer = (kBPieces + 255) / 256;
-  constexpr int kDPer = (kRows * kCB + 255) / 256;
+  constexpr int kBPer = (kBPieces + kThreads - 1) / kThreads;
+  constexpr int kDPer = (kRows * kCB + kThreads - 1) / kThreads;
   struct Stage {
     u32x4a4 q[kQPer];
     u32x4a4 b[kBPer];
@@ -72,27 +82,30 @@ __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long 
     const int cn = min(kCB, nb - c0);
 #pragma unroll
     for (int j = 0; j < kQPer; ++j) {
-      const int p = min(tid + 256 * j, kQPieces - 1);
+      const int p = min(tid + kThreads * j, kQPieces - 1);
       const int r = p / (kCB * 16), o = p - r * (kCB * 16), bb = min(o >> 4, cn - 1), pc = o & 15;
       st.q[j] = ld16((const uint8_t*)(act.q + (size_t)min(m0 + r, M - 1) * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
     }
 #pragma unroll
     for (int j = 0; j < kBPer; ++j) {
-      const int p = min(tid + 256 * j, kBPieces - 1);
+      const int p = min(tid + kThreads * j, kBPieces - 1);
       const int r = p / (kCB * 2), o = p - r * (kCB * 2), bb = min(o >> 1, cn - 1), hf = o & 1;
       st.b[j] = ld16((const uint8_t*)(act.bsums + ((size_t)min(m0 + r, M - 1) * nb + c0 + bb) * 16) + 16 * hf);
     }
 #pragma unroll
     for (int j = 0; j < kDPer; ++j) {
-      const int p = min(tid + 256 * j, kRows * kCB - 1), bb = p / kRows, r = p - bb * kRows;
+      const int p = min(tid + kThreads * j, kRows * kCB - 1), bb = p / kRows, r = p - bb * kRows;
       st.d[j] = act.d[(size_t)min(m0 + r, M - 1) * nb + c0 + min(bb, cn - 1)];
     }
     return st;
   };
-  auto store_stage = [&](const Stage& st) {
+  auto store_stage = [&](const Stage& st, int buf) {
+    int8_t* Aq = aq(buf);
+    _Float16* Ab = ab(buf);
+    float* Ad = ad(buf);
 #pragma unroll
     for (int j = 0; j < kQPer; ++j) {
-      const int p = tid + 256 * j;
+      const int p = tid + kThreads * j;
       if (p < kQPieces) {
         const int r = p / (kCB * 16), o = p - r * (kCB * 16);
         *(u32x4a4*)(Aq + r * kQStride + (o >> 4) * QK + 16 * (o & 15)) = st.q[j];
@@ -100,7 +113,7 @@ __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long 
     }
 #pragma unroll
     for (int j = 0; j < kBPer; ++j) {
-      const int p = tid + 256 * j;
+      const int p = tid + kThreads * j;
       if (p < kBPieces) {  // bsums as fp16 (exact: |.| <= 2032)
         const int r = p / (kCB * 2), o = p - r * (kCB * 2);
         const uint32_t wv[4] = {st.b[j].x, st.b[j].y, st.b[j].z, st.b[j].w};
@@ -115,24 +128,24 @@ __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long 
     }
 #pragma unroll
     for (int j = 0; j < kDPer; ++j) {
-      const int p = tid + 256 * j;
+      const int p = tid + kThreads * j;
       if (p < kRows * kCB) Ad[p] = st.d[j];
     }
   };
 
-  static_assert(4 * 64 == 256, "four waves");
   {
     const Stage st0 = load_stage(0);
-    store_stage(st0);
+    store_stage(st0, 0);
   }
   __syncthreads();
   for (int c0 = 0; c0 < nb; c0 += kCB) {
-    const int cn = min(kCB, nb - c0);
+    const int cn = min(kCB, nb - c0), buf = (c0 / kCB) & 1;
     const bool more = c0 + kCB < nb;
     Stage st;
     if (more) st = load_stage(c0 + kCB);
     // the chunk's blocks in order; the next block's weights load meanwhile
-    const ActTile A{Aq, Ab, kQStride, kBStride};
+    const ActTile A{aq(buf), ab(buf), kQStride, kBStride};
+    const float* Ad = ad(buf);
 #pragma unroll
     for (int i = 0; i < kCB; ++i) {
       if (i < cn) {
@@ -157,11 +170,8 @@ __global__ __launch_bounds__(256) void mtile_kernel(const uint8_t* w, long long 
         for (int nt = 0; nt < NT; ++nt) cur[nt] = nxt[nt];
       }
     }
-    __syncthreads();  // every wave is done with this chunk's LDS
-    if (more) {
-      store_stage(st);
-      __syncthreads();
-    }
+    if (more) store_stage(st, buf ^ 1);
+    __syncthreads();  // the next chunk is in LDS; every wave is done with this one
   }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -291,13 +301,20 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
   }
 }
 
-template <int TYPE, int MT, int NT>
+template <int TYPE, int MT, int NT, int WAVES>
 int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
               int N, hipStream_t stream) {
-  const int rows = 4 * 16 * NT;
+  constexpr int kLds = 2 * kMtBuf<MT>;
+  static bool lds_set = false;
+  if (!lds_set) {
+    (void)hipFuncSetAttribute((const void*)mtile_kernel<TYPE, MT, NT, WAVES>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    lds_set = true;
+  }
+  const int rows = WAVES * 16 * NT;
   const dim3 grid((N + rows - 1) / rows, (M + 16 * MT - 1) / (16 * MT));
-  hipLaunchKernelGGL((mtile_kernel<TYPE, MT, NT>), grid, dim3(256), 0, stream, w, row_bytes, act, y,
-                     ldy, M, N);
+  hipLaunchKernelGGL((mtile_kernel<TYPE, MT, NT, WAVES>), grid, dim3(64 * WAVES), kLds, stream, w,
+                     row_bytes, act, y, ldy, M, N);
   return 0;
 }
 
@@ -314,12 +331,11 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
     hipLaunchKernelGGL((mdec_kernel<TYPE, RT>), dim3(tiles), dim3(256), 0, stream, w, row_bytes, act, y, ldy, M, N);
     return 0;
   }
-  // up to 64 rows: 16-row activation tiles; prefill: 64 activation rows x (Q4_K) 128 weight rows
-  // per workgroup; Q6_K / Q8_0 keep 64 weight rows (their B operands need twice the registers)
-  if (M <= 64) return launch_mt<TYPE, 1, 1>(w, row_bytes, act, y, ldy, M, N, stream);
+  // up to 64 rows: 16-row activation tiles and 64 weight rows per workgroup; prefill: 64
+  // activation rows x 128 weight rows (8 waves)
+  if (M <= 64) return launch_mt<TYPE, 1, 1, 4>(w, row_bytes, act, y, ldy, M, N, stream);
   constexpr int NT = 1;
-  if (M >= kPrefillMinRows && launch_ptile(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
-  return launch_mt<TYPE, 4, NT>(w, row_bytes, act, y, ldy, M, N, stream);
+  return launch_mt<TYPE, 4, NT, 8>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
 }  // namespace

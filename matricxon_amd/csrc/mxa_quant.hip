@@ -56,56 +56,6 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
   if (p == 0) d[(size_t)m * nb + b] = amax / 127.0f;
 }
 
-// Q8_K activations regrouped for the streaming prefill kernel: for each tile of kPrefillRows rows
-// and each block, one contiguous range [q: rows x kPrefillQStride][bsums as fp16: rows x 32 B]
-// [d: rows x 4 B] (bsums |.| <= 2032 are exact in fp16). Rows past M repeat row M - 1. Thread per
-// 16-byte piece: 16 of q, 2 of bsums, and one for d.
-__global__ __launch_bounds__(256) void act_blocked_kernel(const int8_t* __restrict__ q,
-                                                          const float* __restrict__ d,
-                                                          const int16_t* __restrict__ bsums,
-                                                          uint8_t* __restrict__ out, int m_rows,
-                                                          int k, int nb, long long pieces) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= pieces) return;
-  const int p = (int)(i % 19);
-  const long long rb = i / 19;  // (tile, block, row)
-  const int r = (int)(rb % kPrefillRows);
-  const long long tb = rb / kPrefillRows;
-  const int b = (int)(tb % nb), mt = (int)(tb / nb);
-  const int m = min(mt * kPrefillRows + r, m_rows - 1);
-  uint8_t* stage = out + (size_t)tb * kPrefillStageBytes;
-  if (p < 16) {
-    *(u32x4a4*)(stage + r * kPrefillQStride + 16 * p) =
-        ld16((const uint8_t*)(q + (size_t)m * k + (size_t)b * QK) + 16 * p);
-  } else if (p < 18) {
-    const int h = p - 16;
-    const u32x4a4 v = ld16((const uint8_t*)(bsums + ((size_t)m * nb + b) * 16) + 16 * h);
-    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const _Float16 lo = (_Float16)(float)(int16_t)(wv[j] & 0xFFFFu);
-      const _Float16 hi = (_Float16)(float)(int16_t)(wv[j] >> 16);
-      o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-    }
-    *(u32x4a4*)(stage + kPrefillRows * kPrefillQStride + r * 32 + 16 * h) = u32x4a4{o[0], o[1], o[2], o[3]};
-  } else {
-    *(float*)(stage + kPrefillRows * (kPrefillQStride + 32) + r * 4) = d[(size_t)m * nb + b];
-  }
-}
-
-size_t act_blocked_bytes(int m_rows, int k) {
-  const size_t tiles = (size_t)(m_rows + kPrefillRows - 1) / kPrefillRows;
-  return tiles * (size_t)(k / QK) * kPrefillStageBytes;
-}
-
-void launch_act_blocked(const ActBuffers& a, void* out, int m_rows, int k, hipStream_t stream) {
-  const int nb = k / QK;
-  const long long pieces = (long long)((m_rows + kPrefillRows - 1) / kPrefillRows) * nb * kPrefillRows * 19;
-  hipLaunchKernelGGL(act_blocked_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream,
-                     a.q, a.d, a.bsums, (uint8_t*)out, m_rows, k, nb, pieces);
-}
-
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream) {
   const int nb = k / QK;

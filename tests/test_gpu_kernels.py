@@ -278,10 +278,9 @@ def test_batched_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m)
     check_gemm(gpu, oracle, ggml_type, w, x, n, k)
 
 
-# Prefill: 64-row activation tiles, and from 1024 rows the Q4_K streaming kernel (128 x 64 tiles):
-# N below, at and past whole 128-row tiles, M at and past whole 64-row tiles (rows past M repeat
-# row M - 1 in the regrouped activations), odd and long block counts (K = 2304: 9 blocks, 14336:
-# 56).
+# Prefill: 64-row activation tiles of 128 weight rows: N below, at and past whole 128-row tiles, M
+# at and past whole 64-row tiles (rows past M repeat row M - 1), odd and long block counts
+# (K = 2304: 9 blocks, 14336: 56).
 PREFILL_SHAPES = [(129, 768, 128), (260, 2048, 200), (300, 4096, 130), (50, 14336, 140),
                   (513, 2304, 257), (1000, 4096, 320), (300, 2048, 1030), (129, 1024, 1100),
                   (50, 4352, 1024), (513, 2304, 1089)]
@@ -313,9 +312,8 @@ def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> 
 
 @pytest.mark.parametrize("m", [20, 150, 1030])
 def test_gemm_multi_mixed_types_prefill(gpu, oracle, m) -> None:
-    """Q8_K-based and IQ4_XS weights sharing one prefill-sized input: the workspace holds the
-    Q8_K activations, from 1024 rows their regrouped copy (Q4_K), and the bf16 split of x, and
-    every output equals its separate call."""
+    """Q8_K-based and IQ4_XS weights sharing one prefill-sized input: the workspace holds both
+    the Q8_K activations and the bf16 split of x, and every output equals its separate call."""
     k = 1024
     items = [(D.Q4_K, 48), (D.IQ4_XS, 32), (D.Q6_K, 16)]
     ws = [dev(S.packed_weight(t, o, k, seed=40 + i)) for i, (t, o) in enumerate(items)]
