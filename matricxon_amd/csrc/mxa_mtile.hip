@@ -165,6 +165,7 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
             Tile::value(pp[nt], f, g, [&](int e, float v, float dd) {
               acc[mt][nt][e] = Tile::fold(acc[mt][nt][e], Ad[i * kRows + 16 * mt + 4 * g + e], v, dd);
             });
+          if constexpr (MT > 4) __builtin_amdgcn_sched_barrier(0);  // one tile's A operands at a time
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) cur[nt] = nxt[nt];
@@ -335,6 +336,8 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
   // activation rows x 128 weight rows (8 waves)
   if (M <= 64) return launch_mt<TYPE, 1, 1, 4>(w, row_bytes, act, y, ldy, M, N, stream);
   constexpr int NT = 1;
+  if constexpr (TYPE == T_Q4_K)
+    if (M > 256) return launch_mt<TYPE, 8, NT, 8>(w, row_bytes, act, y, ldy, M, N, stream);
   return launch_mt<TYPE, 4, NT, 8>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
