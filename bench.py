@@ -125,7 +125,7 @@ def _graph_us(fn, steps: int, warmup: int) -> float:
 
 
 def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
-    """BASELINE configs 1-5 on seeded synthetic data; weights rotated over
+    """The reference's benchmark configs 1-5 on seeded synthetic data; weights rotated over
     copies totalling > 1 GiB where one copy fits in the 256 MB MALL."""
     import torch
 
@@ -185,6 +185,40 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
         report(f"cfg4 llama3-8b layer (q|k|v, o, gate|up, down) M={m}",
                _graph_us(layer_shared_step, steps, warmup), wb,
                2.0 * m * sum(n * k for _, n, k in layer))
+        # with its producers: RMSNorm before q|k|v and before gate|up, silu(gate) * up before
+        # down. Unfused: the torch ops, then the projections quantize their inputs; fused: the
+        # producer kernels also write the Q8_K blocks the projections run on
+        norm_w = torch.linspace(0.5, 1.5, 4096, device=dev)
+        xr = xs[4096]
+
+        def rms_torch(x):
+            return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5) * norm_w
+
+        def layer_torch_producers(i):
+            h = rms_torch(xr)
+            gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (0, 1, 2)], h,
+                              out=qkv_out)
+            gemm.matmul(layer[3][0], lw[3][i % 2], xr, 4096, 4096, out=ys[3])
+            h = rms_torch(xr)
+            gate, up = gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (4, 5)],
+                                         h, out=gu_out)
+            act = torch.nn.functional.silu(gate) * up
+            gemm.matmul(layer[6][0], lw[6][i % 2], act, 4096, 14336, out=ys[6])
+
+        def layer_fused_producers(i):
+            _, ws = gemm.rms_norm_q8k(xr, norm_w, 1e-5)
+            gemm.matmul_multi_q8k([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (0, 1, 2)],
+                                  ws, m, 4096, out=qkv_out)
+            gemm.matmul(layer[3][0], lw[3][i % 2], xr, 4096, 4096, out=ys[3])
+            _, ws = gemm.rms_norm_q8k(xr, norm_w, 1e-5)
+            gate, up = gemm.matmul_multi_q8k(
+                [(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (4, 5)], ws, m, 4096, out=gu_out)
+            _, ws = gemm.silu_mul_q8k(gate, up)
+            gemm.matmul_q8k(layer[6][0], lw[6][i % 2], ws, None, ys[6], m, 4096, 14336)
+        for label, fn in (("torch RMSNorm/SwiGLU", layer_torch_producers),
+                          ("fused producers", layer_fused_producers)):
+            report(f"cfg4 llama3-8b layer + {label} M={m}", _graph_us(fn, steps, warmup), wb,
+                   2.0 * m * sum(n * k for _, n, k in layer))
         names = ["q", "k", "v", "o", "gate", "up", "down"]
         for j, (t, n, k) in enumerate(layer):
             if names[j] in ("k", "up"):  # same shapes as v (size) / gate
@@ -215,11 +249,11 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (scale for HBM counters)")
     ap.add_argument("--configs", action="store_true",
-                    help="also time BASELINE configs 1-5 (one JSON line each on stderr)")
+                    help="also time the benchmark configs 1-5 (one JSON line each on stderr)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              "(the kernels shard by output rows; see DESIGN.md)", file=sys.stderr)
+              "(the kernels shard by output rows)", file=sys.stderr)
         return 2
 
     import numpy as np

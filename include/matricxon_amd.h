@@ -84,6 +84,32 @@ int mxa_gemm_multi(int n, const int *types, const void *const *ws, const int *ou
                    const float *x, float *y, int n_tokens, int in_features, void *workspace,
                    size_t workspace_bytes, void *stream);
 
+/* mxa_gemm_multi without its quantization step: `workspace` already holds the Q8_K activations
+ * (mxa_quantize_q8_k, mxa_rms_norm_q8_k or mxa_silu_mul_q8_k for the same n_tokens and
+ * in_features). K-quant and Q8_0 weights only (IQ4_XS reads float activations).
+ * The second half of `mx_gemm_multi` (app/native/src/mx_gemm_multi.c:123-176), for groups whose
+ * input comes from a fused producer. */
+int mxa_gemm_multi_q8k(int n, const int *types, const void *const *ws, const int *outs, float *y,
+                       int n_tokens, int in_features, const void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+/* RMSNorm of x (n_tokens, dim) with weight (dim) and eps, as `mx_rms_norm`
+ * (app/native/src/mx_fused_ops.c:7-18): out = x * (1 / sqrtf(mean(x^2) + eps)) * weight, written
+ * to out (fp32, may be NULL) and, in the same pass, quantized to Q8_K into the workspace (layout of
+ * mxa_quantize_q8_k; the blocks equal those of quantizing out). Replaces `FusedOps.rms_norm`
+ * (app/architectures/layers.py:59-83) followed by the projections' quantization step. */
+int mxa_rms_norm_q8_k(const float *x, const float *weight, float eps, int n_tokens, int dim,
+                      float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* SwiGLU's middle step out = silu(gate) * up = gate / (1 + expf(-gate)) * up, elementwise over
+ * (n_tokens, dim), as `mx_silu_mul` (app/native/src/mx_fused_ops.c:39-45), written to out
+ * (contiguous, may be NULL) and quantized to Q8_K into the workspace in the same pass (the down
+ * projection's input). Rows of gate and of up are `ld` >= dim floats apart, so both may be the
+ * halves of one gate|up output (ld = 2 * dim). Replaces `FusedOps.silu_mul`
+ * (app/architectures/layers.py:52-56) plus that quantization. */
+int mxa_silu_mul_q8_k(const float *gate, const float *up, long long ld, int n_tokens, int dim,
+                      float *out, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Q8_K activation quantization of x (n_tokens, in_features) into the workspace layout
  * q int8 (n_tokens, K) | d fp32 (n_tokens, K/256) | bsums int16 (n_tokens, K/256, 16), each
  * part starting on a 256-byte boundary (see mxa_workspace_bytes).

@@ -21,7 +21,10 @@ EXPORTS = (
     "mxa_gemm",
     "mxa_gemm_q8k",
     "mxa_gemm_multi",
+    "mxa_gemm_multi_q8k",
     "mxa_quantize_q8_k",
+    "mxa_rms_norm_q8_k",
+    "mxa_silu_mul_q8_k",
     "mxa_dequantize",
     "mxa_dequant_rows",
     "mxa_last_error",
@@ -62,8 +65,14 @@ def load() -> ctypes.CDLL:
     lib.mxa_gemm_q8k.restype = _i
     lib.mxa_gemm_multi.argtypes = [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_multi.restype = _i
+    lib.mxa_gemm_multi_q8k.argtypes = [_i, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]
+    lib.mxa_gemm_multi_q8k.restype = _i
     lib.mxa_quantize_q8_k.argtypes = [_vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_quantize_q8_k.restype = _i
+    lib.mxa_rms_norm_q8_k.argtypes = [_vp, _vp, ctypes.c_float, _i, _i, _vp, _vp, _sz, _vp]
+    lib.mxa_rms_norm_q8_k.restype = _i
+    lib.mxa_silu_mul_q8_k.argtypes = [_vp, _vp, _ll, _i, _i, _vp, _vp, _sz, _vp]
+    lib.mxa_silu_mul_q8_k.restype = _i
     lib.mxa_dequantize.argtypes = [_i, _vp, _ll, _vp, _vp]
     lib.mxa_dequantize.restype = _i
     lib.mxa_dequant_rows.argtypes = [_i, _vp, _ll, _vp, _i, _i, _vp, _vp]

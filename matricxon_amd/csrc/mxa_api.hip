@@ -197,6 +197,71 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
   return MXA_OK;
 }
 
+int mxa_gemm_multi_q8k(int n, const int* types, const void* const* ws, const int* outs, float* y,
+                       int n_tokens, int in_features, const void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr || y == nullptr ||
+      n_tokens <= 0 || !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  long long total = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!mxa_supports(types[i], in_features) || !needs_q8k(types[i]) || ws[i] == nullptr ||
+        outs[i] <= 0 || !aligned(ws[i], 4))
+      return MXA_ERR_UNSUPPORTED;
+    total += outs[i];
+  }
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+    return MXA_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  const mxa::ActBuffers buf = mxa::act_layout((void*)workspace, n_tokens, in_features);
+  const mxa::Act act = make_act(nullptr, &buf, in_features);
+  mxa::DecodeSeg seg[4];
+  long long c0 = 0;
+  for (int i = 0; i < n; ++i) {
+    seg[i] = mxa::DecodeSeg{types[i], (const uint8_t*)ws[i],
+                            (long long)mxa_row_bytes(types[i], in_features), y + c0, outs[i]};
+    c0 += outs[i];
+  }
+  if (n > 1 && n_tokens <= 16) {  // one launch for the group
+    int st = n_tokens <= mxa::kDecodeMaxRows ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
+                                             : mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+    if (st != 0 && n_tokens > mxa::kDecodeMaxRows)
+      st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
+    if (st == 0) return check_launch();
+  }
+  for (int i = 0; i < n; ++i) {
+    if (mxa::launch_matmul(types[i], seg[i].w, seg[i].row_bytes, act, seg[i].y, total, n_tokens,
+                           outs[i], s) != 0)
+      return MXA_ERR_UNSUPPORTED;
+    const int st = check_launch();
+    if (st != MXA_OK) return st;
+  }
+  return MXA_OK;
+}
+
+int mxa_rms_norm_q8_k(const float* x, const float* weight, float eps, int n_tokens, int dim,
+                      float* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr || weight == nullptr || n_tokens <= 0 || dim <= 0 || dim % mxa::QK != 0 ||
+      !aligned(x, 16) || !aligned(weight, 4) || !aligned(out, 16) || !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, dim)) return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, dim);
+  mxa::launch_rms_norm_q8k(x, weight, eps, out, a, n_tokens, dim, (hipStream_t)stream);
+  return check_launch();
+}
+
+int mxa_silu_mul_q8_k(const float* gate, const float* up, long long ld, int n_tokens, int dim,
+                      float* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (gate == nullptr || up == nullptr || n_tokens <= 0 || dim <= 0 || dim % mxa::QK != 0 ||
+      ld < dim || !aligned(gate, 4) || !aligned(up, 4) || !aligned(out, 16) ||
+      !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, dim)) return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, dim);
+  mxa::launch_silu_mul_q8k(gate, up, ld, out, a, n_tokens, dim, (hipStream_t)stream);
+  return check_launch();
+}
+
 int mxa_dequantize(int ggml_type, const void* blocks, long long n_blocks, float* out,
                    void* stream) {
   if (!known_type(ggml_type) || blocks == nullptr || out == nullptr || n_blocks <= 0)

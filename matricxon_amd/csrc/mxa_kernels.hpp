@@ -25,6 +25,40 @@ inline size_t act_bytes(int m_rows, int k) {
          align256((size_t)m_rows * nb * 16 * 2);
 }
 
+// Q8_K of one 256-value block held by 16 lanes of a DPP row (lane part p: its values 16p..16p+15
+// in v), restating mx_quantize_row_q8_k (app/native/src/mx_common.c:42-69): amax over the block
+// (fmaxf from 0: a NaN input never becomes amax, as the reference's `ax > amax ? ax : amax`); an
+// all-zero block gives q = 0, bsums = 0, d = 0; otherwise iscale = 127/amax and d = amax/127 are
+// correctly rounded divisions, q = clamp(round-half-even(x * iscale), +-127) (lrintf in the
+// default rounding mode is v_rndne_f32), and bsums are the sums of q over 16 values. Writes the
+// lane's 16 q at qblk + 16p, its bsum at bsblk[p] and, from part 0, d. All 16 lanes must be active.
+__device__ __forceinline__ void q8k_part16(const float (&v)[16], int p, int8_t* qblk, int16_t* bsblk,
+                                           float* dp) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = max16(amax);
+  int qv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) qv[i] = 0;
+  if (amax != 0.0f) {
+    const float iscale = 127.0f / amax;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = (int)fminf(fmaxf(rintf(v[i] * iscale), -127.0f), 127.0f);
+  }
+  uint32_t packed[4];
+  int bsum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    packed[i] = (uint32_t)(qv[4 * i] & 0xFF) | ((uint32_t)(qv[4 * i + 1] & 0xFF) << 8) |
+                ((uint32_t)(qv[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * i + 3] & 0xFF) << 24);
+    bsum += qv[4 * i] + qv[4 * i + 1] + qv[4 * i + 2] + qv[4 * i + 3];
+  }
+  *(uint4*)(qblk + 16 * p) = uint4{packed[0], packed[1], packed[2], packed[3]};
+  bsblk[p] = (int16_t)bsum;
+  if (p == 0) *dp = amax / 127.0f;
+}
+
 inline ActBuffers act_layout(void* ws, int m_rows, int k) {
   const size_t nb = (size_t)k / QK;
   uint8_t* p = (uint8_t*)ws;
@@ -39,6 +73,15 @@ inline ActBuffers act_layout(void* ws, int m_rows, int k) {
 
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream);
+
+// Fused producers: RMSNorm (mx_rms_norm, app/native/src/mx_fused_ops.c:7-18) and SwiGLU's
+// silu(gate) * up (mx_silu_mul, mx_fused_ops.c:39-45) over m_rows rows of k values, writing the fp32
+// result to out (when not nullptr) and its Q8_K blocks to a.
+void launch_rms_norm_q8k(const float* x, const float* w, float eps, float* out, const ActBuffers& a,
+                         int m_rows, int k, hipStream_t stream);
+// gate and up rows are ld floats apart.
+void launch_silu_mul_q8k(const float* gate, const float* up, long long ld, float* out,
+                         const ActBuffers& a, int m_rows, int k, hipStream_t stream);
 
 
 int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long n_src_rows,

@@ -9,10 +9,7 @@
 namespace mxa {
 
 // 16 lanes per (row m, 256-value block b), four blocks per wave; lane part p owns elements
-// 16p..16p+15. Restates mx_quantize_row_q8_k (app/native/src/mx_common.c:42-69): amax over the
-// block; an all-zero block gives q = 0, bsums = 0, d = 0; otherwise iscale = 127/amax and
-// d = amax/127 are correctly rounded divisions, q = clamp(round-half-even(x * iscale), +-127)
-// (lrintf in the default rounding mode is v_rndne_f32), bsums are the sums of q over 16 values.
+// 16p..16p+15 (q8k_part16 in mxa_kernels.hpp does the arithmetic).
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
                                                            int8_t* __restrict__ q,
                                                            float* __restrict__ d,
@@ -29,31 +26,8 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     const float4 f = *(const float4*)(x + base + 4 * i);
     v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
   }
-  // fmaxf ignores a NaN operand and the running maximum starts at 0, as the reference's
-  // `ax > amax ? ax : amax` from 0: a NaN input never becomes amax.
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = max16(amax);
-  int qv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) qv[i] = 0;
-  if (amax != 0.0f) {
-    const float iscale = 127.0f / amax;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) qv[i] = (int)fminf(fmaxf(rintf(v[i] * iscale), -127.0f), 127.0f);
-  }
-  uint32_t packed[4];
-  int bsum = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    packed[i] = (uint32_t)(qv[4 * i] & 0xFF) | ((uint32_t)(qv[4 * i + 1] & 0xFF) << 8) |
-                ((uint32_t)(qv[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * i + 3] & 0xFF) << 24);
-    bsum += qv[4 * i] + qv[4 * i + 1] + qv[4 * i + 2] + qv[4 * i + 3];
-  }
-  *(uint4*)(q + base) = uint4{packed[0], packed[1], packed[2], packed[3]};
-  bsums[((size_t)m * nb + b) * 16 + p] = (int16_t)bsum;
-  if (p == 0) d[(size_t)m * nb + b] = amax / 127.0f;
+  q8k_part16(v, p, q + (size_t)m * k + (size_t)b * QK, bsums + ((size_t)m * nb + b) * 16,
+             d + (size_t)m * nb + b);
 }
 
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,

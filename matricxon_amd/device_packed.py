@@ -13,6 +13,9 @@ dequantizing with torch ops and calling `F.linear`.
   (device_packed.py:14-19).
 * `HipDequantizer`: the `TorchDequantizer` interface (torch_dequant.py:310-325) on the kernels.
 
+A float32 input that a fused producer (`matricxon_amd.fused_ops.HipFusedOps`) just wrote comes
+with its Q8_K blocks; `DevicePackedLinear` then runs the matmul alone on them.
+
 Only Q8_0, Q4_K, Q6_K and IQ4_XS (with in_features % 256 == 0) are computed here; a loader
 asks `HipDequantizer.supports` / `HipGemm.supports` and keeps the reference module for the rest.
 """
@@ -23,8 +26,11 @@ import numpy as np
 import torch
 from torch import nn
 
+from matricxon_amd.fused_ops import HANDOFF
 from matricxon_amd.gemm import HipGemm
 from matricxon_amd.quant_types import GEOMETRY
+
+_IQ4_XS = 23
 
 
 def upload_packed(raw, n_rows: int, device: torch.device) -> torch.Tensor:
@@ -89,12 +95,27 @@ class DevicePackedLinear(nn.Module):
     def ggml_type(self) -> int:
         return self._ggml_type
 
+    @property
+    def dtype(self) -> torch.dtype:
+        return self._dtype
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         # The reference casts x to the layer dtype before its matmul (device_packed.py:54).
         x = x.to(self._dtype)
         lead = x.shape[:-1]
-        y = self._gemm.matmul(self._ggml_type, self.packed, x.reshape(-1, self.in_features),
-                              self.out_features, self.in_features)
+        k = self.in_features
+        ws = HANDOFF.claim(x) if self._ggml_type != _IQ4_XS else None
+        if ws is not None:  # x came from a fused producer that also wrote its Q8_K blocks
+            n = x.numel() // k
+            y = torch.empty((n, self.out_features), dtype=torch.float32, device=self.packed.device)
+            self._gemm.matmul_q8k(self._ggml_type, self.packed, ws, None, y, n, self.out_features, k)
+        else:
+            y = self._gemm.matmul(self._ggml_type, self.packed, x.reshape(-1, k),
+                                  self.out_features, k)
+        return self.finish(y, lead)
+
+    def finish(self, y: torch.Tensor, lead: tuple[int, ...]) -> torch.Tensor:
+        """Float32 result rows (M, N) -> the layer's output (..., N) in its dtype, plus bias."""
         y = y.to(self._dtype).reshape(*lead, self.out_features)
         return y if self.bias is None else y + self.bias
 

@@ -34,6 +34,19 @@ def q8k_bytes(m: int, k: int) -> int:
     return _al256(m * k) + _al256(m * nb * 4) + _al256(m * nb * 32)
 
 
+def q8k_views(workspace: torch.Tensor, m: int, k: int) -> tuple[torch.Tensor, torch.Tensor,
+                                                                  torch.Tensor]:
+    """(q int8 (M, K), d float32 (M, K/256), bsums int16 (M, K/256, 16)) views of the Q8_K part
+    at the start of a workspace: q, then d, then bsums, each starting on a 256-byte boundary."""
+    nb = k // 256
+    q = workspace[: m * k].view(torch.int8).reshape(m, k)
+    off = _al256(m * k)
+    d = workspace[off : off + m * nb * 4].view(torch.float32).reshape(m, nb)
+    off += _al256(m * nb * 4)
+    bs = workspace[off : off + m * nb * 32].view(torch.int16).reshape(m, nb, 16)
+    return q, d, bs
+
+
 def _require_device_tensor(name: str, t: torch.Tensor) -> None:
     if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
         raise ValueError(f"{name} must be a tensor on a HIP device, got {getattr(t, 'device', t)}")
@@ -174,8 +187,9 @@ class HipGemm:
         """`items`: (ggml_type, packed, out_features) per weight sharing input `x`
         (n_tokens, in_features): one activation quantization, one float32 output per weight,
         as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them. For up to 16 tokens
-        and K-quant / Q8_0 weights of up to 16 blocks per row this is a single matmul launch. `out`, if given, is the
-        float32 (n_tokens, sum of out_features) result buffer the outputs are views of."""
+        and K-quant / Q8_0 weights of up to 16 blocks per row this is a single matmul launch.
+        `out`, if given, is the float32 (n_tokens, sum of out_features) result buffer the outputs
+        are views of."""
         import ctypes
 
         if not 1 <= len(items) <= 4:
@@ -217,6 +231,84 @@ class HipGemm:
         self._calls += 1
         return list(torch.split(y, outs, dim=-1))
 
+    # -- fused producers: FusedOps.rms_norm / silu_mul (app/architectures/layers.py:52-83) whose
+    #    result is also written as Q8_K for the projections that consume it ----------------------
+    def rms_norm_q8k(self, x: torch.Tensor, weight: torch.Tensor, eps: float,
+                     want_out: bool = True) -> tuple[torch.Tensor | None, torch.Tensor]:
+        """RMSNorm of the rows of x (..., K) on the device with `weight` (K,), in float32:
+        (out float32 (M, K) or None, workspace) where the workspace holds the Q8_K blocks of out,
+        ready for `matmul_multi_q8k` / `matmul_q8k`. K must be a multiple of 256."""
+        _require_device_tensor("x", x)
+        x32 = x.detach().to(torch.float32).reshape(-1, x.shape[-1]).contiguous()
+        w32 = weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        m, k = x32.shape
+        if w32.shape != (k,):
+            raise ValueError("weight must have shape (K,) for x (..., K)")
+        out = torch.empty_like(x32) if want_out else None
+        ws = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device=x.device)
+        status = self._lib.mxa_rms_norm_q8_k(x32.data_ptr(), w32.data_ptr(), float(eps), m, k,
+                                             None if out is None else out.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), _stream(x.device))
+        self._check(status, "mxa_rms_norm_q8_k", 15)
+        return out, ws
+
+    def silu_mul_q8k(self, gate: torch.Tensor, up: torch.Tensor,
+                     want_out: bool = True) -> tuple[torch.Tensor | None, torch.Tensor]:
+        """silu(gate) * up over (..., K) on the device, in float32: (out (M, K) or None,
+        workspace with the Q8_K blocks of out), the down projection's input. K must be a multiple
+        of 256. Two float32 (M, K) views with unit column stride and one common row stride (the
+        halves of a gate|up output) are read in place."""
+        _require_device_tensor("gate", gate)
+        if gate.shape != up.shape or gate.dim() == 0:
+            raise ValueError("gate and up must have the same shape")
+        k = gate.shape[-1]
+        g2, u2 = gate.detach().reshape(-1, k), up.detach().reshape(-1, k)
+        if not (g2.dtype == u2.dtype == torch.float32 and u2.device == g2.device
+                and g2.stride(-1) == u2.stride(-1) == 1 and g2.stride(0) == u2.stride(0)
+                and g2.stride(0) >= k):
+            g2 = g2.to(torch.float32).contiguous()
+            u2 = u2.to(device=g2.device, dtype=torch.float32).contiguous()
+        m = g2.shape[0]
+        out = torch.empty((m, k), dtype=torch.float32, device=g2.device) if want_out else None
+        ws = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device=g2.device)
+        status = self._lib.mxa_silu_mul_q8_k(g2.data_ptr(), u2.data_ptr(), g2.stride(0), m, k,
+                                             None if out is None else out.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), _stream(g2.device))
+        self._check(status, "mxa_silu_mul_q8_k", 15)
+        return out, ws
+
+    def matmul_multi_q8k(self, items: list[tuple[int, torch.Tensor, int]], workspace: torch.Tensor,
+                         n_tokens: int, in_features: int,
+                         out: torch.Tensor | None = None) -> list[torch.Tensor]:
+        """`matmul_multi` on activations already quantized into `workspace` (by a fused producer
+        or `quantize_into`); K-quant and Q8_0 weights only."""
+        import ctypes
+
+        if not 1 <= len(items) <= 4:
+            raise ValueError("matmul_multi_q8k takes 1 to 4 weights")
+        device = items[0][1].device
+        for t, p, o in items:
+            if not self.supports(t, in_features) or int(t) == 23:
+                raise RuntimeError(f"mxa_gemm_multi_q8k failed with status -1 for type {t}")
+            self._check_packed(int(t), p, o, in_features)
+        outs = [int(o) for _, _, o in items]
+        if out is None:
+            out = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
+        elif (out.dtype != torch.float32 or out.device != device or not out.is_contiguous()
+              or tuple(out.shape) != (n_tokens, sum(outs))):
+            raise ValueError("out must be a contiguous float32 (n_tokens, sum of out_features) "
+                             "tensor on the weights' device")
+        n = len(items)
+        types = (ctypes.c_int * n)(*[int(t) for t, _, _ in items])
+        ptrs = (ctypes.c_void_p * n)(*[p.data_ptr() for _, p, _ in items])
+        couts = (ctypes.c_int * n)(*outs)
+        status = self._lib.mxa_gemm_multi_q8k(n, types, ptrs, couts, out.data_ptr(), n_tokens,
+                                              in_features, workspace.data_ptr(), workspace.numel(),
+                                              _stream(device))
+        self._check(status, "mxa_gemm_multi_q8k", int(items[0][0]))
+        self._calls += 1
+        return list(torch.split(out, outs, dim=-1))
+
     def quantize_q8_k(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """Q8_K activations of x (M, K) float32 on the device: (q int8 (M, K), d float32
         (M, K/256), bsums int16 (M, K/256, 16))."""
@@ -231,13 +323,7 @@ class HipGemm:
         status = self._lib.mxa_quantize_q8_k(x32.data_ptr(), m, k, ws.data_ptr(), ws_bytes,
                                              _stream(x.device))
         self._check(status, "mxa_quantize_q8_k", 15)
-
-        q = ws[: m * k].view(torch.int8).reshape(m, k)
-        off = _al256(m * k)
-        d = ws[off : off + m * nb * 4].view(torch.float32).reshape(m, nb)
-        off += _al256(m * nb * 4)
-        bs = ws[off : off + m * nb * 32].view(torch.int16).reshape(m, nb, 16)
-        return q, d, bs
+        return q8k_views(ws, m, k)
 
     def dequantize(self, blocks: torch.Tensor, ggml_type: int) -> torch.Tensor:
         """`TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:323-325): blocks

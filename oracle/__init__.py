@@ -7,6 +7,8 @@ never routes through it: when the HIP library is missing, the product fails loud
 Contents:
 * `dequant.py`  numpy float32 restatement of the reference's bit-exact dequantizers
   (Q8_0, Q4_K, Q6_K, IQ4_XS) and of the Q8_K activation quantizer.
+* `fused.py`    numpy restatement of the fused producer ops (RMSNorm, silu * up) whose results
+  feed the projections.
 * `mx_oracle.c` plain-C restatement of the reference `mx_gemm` semantics (Q8_K activations,
   integer block dots, per-block fp32 folds; fp32 dot for IQ4_XS), built by `Makefile` into
   `oracle/_build/libmx_oracle.so`.
@@ -25,4 +27,9 @@ How each function is pinned (what a plausible mistake would fail):
                   compared element-wise with this one.
 * mx_oracle gemm  the reference C `mx_gemm` (same results up to fp32 fold rounding), and
                   float64 products of the dequantized weights on integer activations.
+* rms_norm        the reference C `mx_rms_norm` (a few ulps: its SIMD sum has no fixed order),
+                  closed forms (a constant row c gives c / sqrt(c^2 + eps) * w; a zero row gives
+                  0; scaling x by 2^k leaves it unchanged when eps is 0).
+* silu_mul        the reference C `mx_silu_mul` (a few ulps: expf), silu(0) = 0, and the limits
+                  silu(g) -> g for large g, -> 0 for very negative g.
 """

@@ -108,6 +108,10 @@ class RefGemm:
         lib.mx_dequant_rows.argtypes = [_i, _vp, _vp, _i, _i, _vp, _i]
         lib.mx_dequant_rows.restype = _i
         lib.mx_build_info.restype = ctypes.c_char_p
+        lib.mx_rms_norm.argtypes = [_vp, _vp, _vp, _i, _i, ctypes.c_float]
+        lib.mx_rms_norm.restype = None
+        lib.mx_silu_mul.argtypes = [_vp, _vp, _vp, _i]
+        lib.mx_silu_mul.restype = None
         self._lib = lib
         self.build_info = lib.mx_build_info().decode()
 
@@ -151,6 +155,21 @@ class RefGemm:
                                            row_width, _ptr(out), 1)
         if status != 0:
             raise RuntimeError(f"mx_dequant_rows failed with status {status}")
+        return out
+
+
+    def rms_norm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.empty_like(x)
+        self._lib.mx_rms_norm(_ptr(x), _ptr(w), _ptr(out), x.shape[0], x.shape[1], float(eps))
+        return out
+
+    def silu_mul(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(gate, dtype=np.float32)
+        u = np.ascontiguousarray(up, dtype=np.float32)
+        out = np.empty_like(g)
+        self._lib.mx_silu_mul(_ptr(g), _ptr(u), _ptr(out), g.size)
         return out
 
 

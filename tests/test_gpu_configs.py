@@ -1,4 +1,4 @@
-"""Parity at the five benchmark configurations' real shapes (BASELINE.json `configs`), seeded
+"""Parity at the five benchmark configurations' real shapes, seeded
 synthetic inputs as in bench.py. The oracle checks every output where it runs in seconds, and a
 spread of rows (first, last, every 97th) of the 128256-row vocab head and of the prefill chunks."""
 

@@ -1,0 +1,223 @@
+"""Fused producers on the GPU: RMSNorm and silu(gate) * up writing their float32 result and its
+Q8_K blocks in one kernel (`mxa_rms_norm_q8_k`, `mxa_silu_mul_q8_k`), the projections that run
+on those blocks (`mxa_gemm_multi_q8k`, `mxa_gemm_q8k`) and the host hand-off between them
+(`HipFusedOps`, `project_shared`, `DevicePackedLinear`).
+
+Tolerances: the float32 result is within 4e-6 relative per element of the oracle (the sum of
+squares is reduced in another order; 4e-6 bounds that rounding for rows of up to 14336 values).
+The Q8_K blocks equal, bit for bit, those `mxa_quantize_q8_k` writes for that float32 result, and
+every matmul on them equals, bit for bit, the matmul of that result through the unfused path."""
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from matricxon_amd import synthetic as S
+from matricxon_amd.device_packed import DevicePackedLinear
+from matricxon_amd.fused_ops import HANDOFF, HipFusedOps, project_shared
+from matricxon_amd.gemm import q8k_views
+from oracle import dequant as D
+from oracle import fused as F
+from tests.conftest import GOLDEN
+from tests.test_gpu_kernels import assert_within_tolerance, bits, dev, host
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 4e-6
+
+
+def assert_q8k_equal(gpu, ws: torch.Tensor, out: torch.Tensor) -> None:
+    m, k = out.shape
+    got = q8k_views(ws, m, k)
+    want = gpu.quantize_q8_k(out)
+    for name, g, w in zip(("q", "d", "bsums"), got, want):
+        assert torch.equal(g, w), name
+
+
+SHAPES = [(1, 4096), (3, 4096), (16, 4096), (5, 256), (7, 2304), (2, 14336), (130, 1024)]
+
+
+@pytest.mark.parametrize("m,k", SHAPES)
+def test_rms_norm_q8k(gpu, m, k) -> None:
+    rng = np.random.default_rng(m * 7 + k)
+    x = rng.standard_normal((m, k), dtype=np.float32) * np.float32(2.5)
+    if m > 2:
+        x[1] = 0.0  # a zero row: scale 1/sqrt(eps), out 0, all-zero Q8_K blocks
+    w = (rng.standard_normal(k, dtype=np.float32) * np.float32(0.2) + np.float32(1)).astype(np.float32)
+    out, ws = gpu.rms_norm_q8k(dev(x), dev(w), 1e-5)
+    np.testing.assert_allclose(host(out), F.rms_norm(x, w, 1e-5), rtol=RTOL, atol=0)
+    assert_q8k_equal(gpu, ws, out)
+    none, ws2 = gpu.rms_norm_q8k(dev(x), dev(w), 1e-5, want_out=False)
+    assert none is None
+    for a, b in zip(q8k_views(ws2, m, k), q8k_views(ws, m, k)):  # the padding is not written
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("m,k", SHAPES)
+def test_silu_mul_q8k(gpu, m, k) -> None:
+    rng = np.random.default_rng(m * 11 + k)
+    g = rng.standard_normal((m, k), dtype=np.float32) * np.float32(4)
+    u = rng.standard_normal((m, k), dtype=np.float32)
+    g[0, :6] = [0.0, 30.0, -30.0, 90.0, -90.0, -0.0]
+    out, ws = gpu.silu_mul_q8k(dev(g), dev(u))
+    np.testing.assert_allclose(host(out), F.silu_mul(g, u), rtol=RTOL, atol=1e-37)
+    assert_q8k_equal(gpu, ws, out)
+
+
+def test_silu_mul_q8k_reads_gate_up_halves_in_place(gpu) -> None:
+    """gate and up as the two halves of one (M, 2K) gate|up output: the same result as on
+    contiguous copies."""
+    m, k = 5, 1280
+    gu = torch.randn(m, 2 * k, device="cuda") * 3
+    gate, up = torch.split(gu, k, dim=-1)
+    out, ws = gpu.silu_mul_q8k(gate, up)
+    out_c, ws_c = gpu.silu_mul_q8k(gate.contiguous(), up.contiguous())
+    assert torch.equal(out, out_c)
+    for a, b in zip(q8k_views(ws, m, k), q8k_views(ws_c, m, k)):
+        assert torch.equal(a, b)
+    np.testing.assert_allclose(host(out), F.silu_mul(host(gate.contiguous()), host(up.contiguous())),
+                               rtol=RTOL, atol=1e-37)
+
+
+def test_fused_ops_match_reference_fixtures(gpu) -> None:
+    with np.load(GOLDEN / "fused_cases.npz") as z:
+        c = {k: z[k] for k in z.files}
+    out, ws = gpu.rms_norm_q8k(dev(c["rms_x"]), dev(c["rms_w"]), float(c["rms_eps"][0]))
+    np.testing.assert_allclose(host(out), c["rms_y"], rtol=RTOL, atol=0)
+    assert_q8k_equal(gpu, ws, out)
+    out, ws = gpu.silu_mul_q8k(dev(c["silu_g"]), dev(c["silu_u"]))
+    np.testing.assert_allclose(host(out), c["silu_y"], rtol=RTOL, atol=1e-37)
+    assert_q8k_equal(gpu, ws, out)
+
+
+# groups of projections fed by a producer: q|k|v and gate|up of the layer config at reduced N,
+# token counts on each kernel path (decode, batched decode, matrix-core prefill)
+Q8K_GROUPS = [
+    ([(D.Q4_K, 512), (D.Q4_K, 128), (D.Q6_K, 128)], 4096, 1),
+    ([(D.Q4_K, 700), (D.Q4_K, 700)], 4096, 3),
+    ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65)], 2048, 4),
+    ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 9),
+    ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 16),
+    ([(D.Q4_K, 300), (D.Q6_K, 200)], 1024, 70),
+    ([(D.Q6_K, 256)], 14336, 16),
+]
+
+
+@pytest.mark.parametrize("items,k,m", Q8K_GROUPS)
+def test_gemm_multi_q8k_equals_unfused(gpu, oracle, items, k, m) -> None:
+    rng = np.random.default_rng(k + m)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w_norm = rng.standard_normal(k, dtype=np.float32)
+    ws_np = [S.packed_weight(t, o, k, seed=40 + i) for i, (t, o) in enumerate(items)]
+    packed = [(t, dev(w), o) for (t, o), w in zip(items, ws_np)]
+    out, ws = gpu.rms_norm_q8k(dev(x), dev(w_norm), 1e-6)
+    fused = gpu.matmul_multi_q8k(packed, ws, m, k)
+    unfused = gpu.matmul_multi(packed, out)
+    xo = host(out)
+    for (t, o), w, yf, yu in zip(items, ws_np, fused, unfused):
+        assert torch.equal(yf, yu), f"type {t} ({o} x {k}), {m} tokens"
+        assert_within_tolerance(host(yf), oracle.gemm(t, w, xo, o, k))
+        y1 = torch.empty((m, o), dtype=torch.float32, device="cuda")
+        gpu.matmul_q8k(t, dev(w), ws, None, y1, m, o, k)
+        assert torch.equal(y1, yf.contiguous())
+
+
+def test_fused_producer_error_paths(gpu) -> None:
+    x = dev(np.ones((2, 300), np.float32))
+    with pytest.raises(RuntimeError, match="status -1"):
+        gpu.rms_norm_q8k(x, dev(np.ones(300, np.float32)), 1e-5)  # 300 is not a multiple of 256
+    with pytest.raises(ValueError):
+        gpu.rms_norm_q8k(dev(np.ones((2, 256), np.float32)), dev(np.ones(512, np.float32)), 1e-5)
+    with pytest.raises(ValueError):
+        gpu.silu_mul_q8k(dev(np.ones((2, 256), np.float32)), dev(np.ones((1, 256), np.float32)))
+    _, ws = gpu.rms_norm_q8k(dev(np.ones((2, 256), np.float32)), dev(np.ones(256, np.float32)), 0.0)
+    w = dev(S.packed_weight(D.IQ4_XS, 8, 256, seed=1))
+    with pytest.raises(RuntimeError, match="status -1"):
+        gpu.matmul_multi_q8k([(D.IQ4_XS, w, 8)], ws, 2, 256)  # IQ4_XS reads float32 x
+    wq = dev(S.packed_weight(D.Q4_K, 8, 256, seed=1))
+    with pytest.raises(RuntimeError, match="status -2"):
+        gpu.matmul_multi_q8k([(D.Q4_K, wq, 8)], ws[:100], 2, 256)  # workspace too small
+
+
+class _Layer(nn.Module):
+    """The caller shape of RMSNorm -> q|k|v and SwiGLU gate|up -> down
+    (app/architectures/layers.py:52-83) on packed device modules."""
+
+    def __init__(self, k: int, ffn: int, dtype: torch.dtype) -> None:
+        super().__init__()
+        def mk(t: int, n: int, kk: int, seed: int) -> DevicePackedLinear:
+            return DevicePackedLinear(dev(S.packed_weight(t, n, kk, seed=seed)), kk, t, dtype=dtype)
+
+        self.q_proj, self.k_proj = mk(D.Q4_K, 512, k, 1), mk(D.Q4_K, 128, k, 2)
+        self.v_proj = mk(D.Q6_K, 128, k, 3)
+        self.gate_proj, self.up_proj = mk(D.Q4_K, ffn, k, 4), mk(D.Q4_K, ffn, k, 5)
+        self.down_proj = mk(D.Q6_K, k, ffn, 6)
+        self.norm_w = dev(np.linspace(0.5, 1.5, k, dtype=np.float32))
+
+    def forward(self, x: torch.Tensor, ops: HipFusedOps) -> list[torch.Tensor]:
+        h = ops.rms_norm(x, self.norm_w, 1e-5)
+        q, kk, v = project_shared(self, ("q_proj", "k_proj", "v_proj"), h)
+        gate, up = project_shared(self, ("gate_proj", "up_proj"), h)
+        hidden = ops.silu_mul(gate, up)
+        return [h, q, kk, v, gate, up, hidden, self.down_proj(hidden)]
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 16, 40])
+def test_layer_with_handoff_equals_unfused_modules(gpu, tokens) -> None:
+    """With HipFusedOps active the projections take the producers' Q8_K blocks; each result
+    equals, bit for bit, the module's own forward on the producer's float32 output."""
+    torch.manual_seed(tokens)
+    k, ffn = 1024, 2048
+    layer = _Layer(k, ffn, torch.float32)
+    x = torch.randn(1, tokens, k, device="cuda")
+    HipFusedOps.configure(True)
+    try:
+        h, q, kk, v, gate, up, hidden, down = layer(x, HipFusedOps.active())
+        assert HANDOFF.claim(hidden) is not None  # the last producer's blocks are on offer
+    finally:
+        HipFusedOps.configure(False)
+    assert HANDOFF.claim(hidden) is None
+    assert torch.equal(q, layer.q_proj(h)) and torch.equal(kk, layer.k_proj(h))
+    assert torch.equal(v, layer.v_proj(h))
+    assert torch.equal(gate, layer.gate_proj(h)) and torch.equal(up, layer.up_proj(h))
+    np.testing.assert_allclose(host(hidden.reshape(tokens, ffn)),
+                               F.silu_mul(host(gate.reshape(tokens, ffn)), host(up.reshape(tokens, ffn))),
+                               rtol=RTOL, atol=1e-37)
+    assert torch.equal(down, layer.down_proj(hidden))
+    np.testing.assert_allclose(host(h.reshape(tokens, k)), F.rms_norm(host(x.reshape(tokens, k)),
+                               host(layer.norm_w), 1e-5), rtol=RTOL, atol=0)
+
+
+def test_handoff_refuses_modified_or_other_tensors(gpu) -> None:
+    HipFusedOps.configure(True)
+    try:
+        ops = HipFusedOps.active()
+        x = torch.randn(2, 512, device="cuda")
+        h = ops.rms_norm(x, torch.ones(512, device="cuda"), 1e-5)
+        assert HANDOFF.claim(h) is not None and HANDOFF.claim(h.view(1, 2, 512)) is not None
+        assert HANDOFF.claim(h[:1]) is None and HANDOFF.claim(h.clone()) is None
+        assert HANDOFF.claim(h.to(torch.bfloat16)) is None
+        h.view(-1)[3] += 1.0  # an in-place write through a view moves the shared version
+        assert HANDOFF.claim(h) is None
+        # unsupported inputs return None, as the reference's FusedOps does
+        assert ops.rms_norm(x.cpu(), torch.ones(512), 1e-5) is None
+        assert ops.rms_norm(x[:, :300].contiguous(), torch.ones(300, device="cuda"), 1e-5) is None
+        assert ops.silu_mul(x, x[:1]) is None
+        assert ops.silu_mul(x.to(torch.bfloat16), x.to(torch.bfloat16)) is None
+    finally:
+        HipFusedOps.configure(False)
+
+
+def test_project_shared_bf16_and_bias(gpu) -> None:
+    """A bf16 group casts x first, as each module does; a bias is added per module."""
+    k = 512
+    mods = nn.Module()
+    mods.a = DevicePackedLinear(dev(S.packed_weight(D.Q4_K, 64, k, seed=1)), k, D.Q4_K,
+                                bias=torch.randn(64), dtype=torch.bfloat16)
+    mods.b = DevicePackedLinear(dev(S.packed_weight(D.Q6_K, 32, k, seed=2)), k, D.Q6_K,
+                                dtype=torch.bfloat16)
+    x = torch.randn(2, 3, k, device="cuda")
+    ya, yb = project_shared(mods, ("a", "b"), x)
+    assert ya.dtype == torch.bfloat16 and ya.shape == (2, 3, 64)
+    assert torch.equal(ya, mods.a(x)) and torch.equal(yb, mods.b(x))

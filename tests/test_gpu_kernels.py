@@ -1,6 +1,6 @@
 """GPU parity of the HIP kernels against the CPU oracle (oracle/), through the C ABI.
 
-Bars: dequantized values bit-exact; matmul outputs within rel-L2 <= 1e-4 and
+Bars (the benchmark's stated tolerances): dequantized values bit-exact; matmul outputs within rel-L2 <= 1e-4 and
 max|diff| <= 2e-3 * max|ref| of the reference C kernel semantics. K-quant and Q8_0 outputs are
 additionally checked for bit-equality with the oracle: integer block dots are exact and the
 kernels fold blocks in the oracle's order with the oracle's fused steps, so any difference there
