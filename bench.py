@@ -236,6 +236,43 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
             report(f"{name} prefill M={m}", us, n * row_bytes(t, 4096), 2.0 * m * n * 4096)
 
 
+def bench_load(dev) -> None:
+    """Host -> HBM upload of the config 3 packed weight (128256 x 4096 Q6_K, 431 MB) from
+    pageable host memory already in the page cache: the reference's `upload_packed`
+    (frombuffer + `.to(device, copy=True)`) against `PackedUploader` (pinned, overlapped)."""
+    import numpy as np
+    import torch
+
+    from matricxon_amd.loading import PackedUploader
+
+    n, row = 128256, 3360
+    raw = np.random.default_rng(7).integers(0, 256, n * row, dtype=np.uint8)
+    mv = memoryview(raw)
+
+    def timed(fn, reps=3):
+        best = float("inf")
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+            del out
+        return best
+
+    t_ref = timed(lambda: torch.frombuffer(mv, dtype=torch.uint8).reshape(n, row)
+                  .to(dev, copy=True))
+    with PackedUploader(dev) as up:
+        up.upload(mv, n)  # first use: pinned pages touched
+        t_up = timed(lambda: up.upload(mv, n))
+        got = up.upload(mv, n)
+        ok = bool(torch.equal(got[::997].cpu(), torch.from_numpy(raw.reshape(n, row)[::997])))
+    print(json.dumps({"config": "load Q6_K 128256x4096 host->HBM", "bytes": n * row,
+                      "pageable_gbs": round(n * row / t_ref / 1e9, 1),
+                      "staged_gbs": round(n * row / t_up / 1e9, 1), "rows_checked": ok}),
+          file=sys.stderr, flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +285,9 @@ def main() -> int:
                     help="only the per-launch kernel timing loop (for rocprofv3 --pmc runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (scale for HBM counters)")
+    ap.add_argument("--load", action="store_true",
+                    help="also time the load path: the config 3 weight (431 MB) from host memory "
+                         "into HBM, the reference's pageable copy vs the staged uploader")
     ap.add_argument("--configs", action="store_true",
                     help="also time the benchmark configs 1-5 (one JSON line each on stderr)")
     args = ap.parse_args()
@@ -363,6 +403,9 @@ def main() -> int:
 
     if args.configs:
         bench_configs(gemm, dev, max(20, args.steps // 4), args.warmup)
+
+    if args.load:
+        bench_load(dev)
 
     if args.calibrate_copy:
         nbytes = args.calibrate_copy << 20

@@ -131,6 +131,14 @@ int mxa_dequantize(int ggml_type, const void *blocks, long long n_blocks, float 
 int mxa_dequant_rows(int ggml_type, const void *w, long long n_src_rows, const int32_t *rows,
                      int n_rows, int row_width, float *out, void *stream);
 
+/* Reorders packed rows on the device: dst row i = src row order[i] for i < n_rows, rows of
+ * row_bytes bytes (any GGUF type: a row is whole blocks); `order` is a device int32 array; an
+ * index outside [0, n_src_rows) gives a row of zero bytes. src and dst must not overlap.
+ * Replaces `PackedRows.reordered` (app/gguf/packed_rows.py:24-28), the host-side row permutation
+ * the loader applies to packed attn_q / attn_k before `upload_packed`. */
+int mxa_gather_rows(const void *src, long long n_src_rows, long long row_bytes,
+                    const int32_t *order, int n_rows, void *dst, void *stream);
+
 /* Text of the last HIP error seen by this library on the calling thread ("" if none). */
 const char *mxa_last_error(void);
 

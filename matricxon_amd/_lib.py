@@ -27,6 +27,7 @@ EXPORTS = (
     "mxa_silu_mul_q8_k",
     "mxa_dequantize",
     "mxa_dequant_rows",
+    "mxa_gather_rows",
     "mxa_last_error",
 )
 
@@ -77,6 +78,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_dequantize.restype = _i
     lib.mxa_dequant_rows.argtypes = [_i, _vp, _ll, _vp, _i, _i, _vp, _vp]
     lib.mxa_dequant_rows.restype = _i
+    lib.mxa_gather_rows.argtypes = [_vp, _ll, _ll, _vp, _i, _vp, _vp]
+    lib.mxa_gather_rows.restype = _i
     lib.mxa_last_error.argtypes = []
     lib.mxa_last_error.restype = ctypes.c_char_p
     _lib = lib

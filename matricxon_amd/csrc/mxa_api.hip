@@ -285,6 +285,15 @@ int mxa_dequant_rows(int ggml_type, const void* w, long long n_src_rows, const i
   return check_launch();
 }
 
+int mxa_gather_rows(const void* src, long long n_src_rows, long long row_bytes,
+                    const int32_t* order, int n_rows, void* dst, void* stream) {
+  if (src == nullptr || order == nullptr || dst == nullptr || n_src_rows <= 0 || row_bytes <= 0 ||
+      n_rows <= 0 || !aligned(order, 4))
+    return MXA_ERR_UNSUPPORTED;
+  mxa::launch_gather_rows(src, n_src_rows, row_bytes, order, n_rows, dst, (hipStream_t)stream);
+  return check_launch();
+}
+
 const char* mxa_last_error(void) { return g_last_error; }
 
 }  // extern "C"

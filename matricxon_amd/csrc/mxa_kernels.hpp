@@ -83,6 +83,11 @@ void launch_rms_norm_q8k(const float* x, const float* w, float eps, float* out, 
 void launch_silu_mul_q8k(const float* gate, const float* up, long long ld, float* out,
                          const ActBuffers& a, int m_rows, int k, hipStream_t stream);
 
+// dst row i = src row order[i] for i < n_rows (rows of row_bytes bytes); an index outside
+// [0, n_src_rows) gives a zero row.
+void launch_gather_rows(const void* src, long long n_src_rows, long long row_bytes,
+                        const int32_t* order, int n_rows, void* dst, hipStream_t stream);
+
 
 int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long n_src_rows,
                    long long row_bytes, int blocks_per_row, long long n_blocks, float* out,

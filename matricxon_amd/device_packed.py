@@ -33,8 +33,32 @@ from matricxon_amd.quant_types import GEOMETRY
 _IQ4_XS = 23
 
 
+_UPLOADERS: dict[torch.device, "PackedUploader"] = {}
+STAGED_UPLOAD_MIN_BYTES = 16 << 20
+
+
+def _host_nbytes(raw) -> int | None:
+    """Bytes of a host source; None for a device tensor."""
+    if isinstance(raw, torch.Tensor):
+        return None if raw.device.type != "cpu" else raw.numel() * raw.element_size()
+    return memoryview(raw).nbytes
+
+
 def upload_packed(raw, n_rows: int, device: torch.device) -> torch.Tensor:
-    """`(n_rows, row_bytes)` uint8 copy of packed bytes on `device` (never aliases `raw`)."""
+    """`(n_rows, row_bytes)` uint8 copy of packed bytes on `device` (never aliases `raw`).
+    Host sources of 16 MiB or more go to a GPU through the pinned, overlapped staging of
+    `matricxon_amd.loading.PackedUploader`."""
+    device = torch.device(device)
+    nbytes = _host_nbytes(raw)
+    if device.type == "cuda" and nbytes is not None and nbytes >= STAGED_UPLOAD_MIN_BYTES:
+        from matricxon_amd.loading import PackedUploader
+
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        up = _UPLOADERS.get(device)
+        if up is None:
+            up = _UPLOADERS[device] = PackedUploader(device)
+        return up.upload(raw, n_rows)
     if isinstance(raw, torch.Tensor):
         flat = raw.reshape(-1).to(torch.uint8)
     else:

@@ -342,6 +342,28 @@ class HipGemm:
         self._check(status, "mxa_dequantize", ggml_type)
         return out
 
+    def gather_rows(self, packed: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
+        """A new (len(order), row_bytes) uint8 device tensor whose row i is `packed` row
+        `order[i]` (`PackedRows.reordered`, app/gguf/packed_rows.py:24-28, on the device).
+        Indices are checked on the host: an index outside [0, n_rows) raises IndexError."""
+        _require_device_tensor("packed", packed)
+        if packed.dtype != torch.uint8 or packed.dim() != 2 or not packed.is_contiguous():
+            raise ValueError("packed must be a contiguous uint8 (n_rows, row_bytes) tensor")
+        idx = order.detach().reshape(-1).to(torch.int64)
+        n = idx.numel()
+        out = torch.empty((n, packed.shape[1]), dtype=torch.uint8, device=packed.device)
+        if n == 0:
+            return out
+        lo, hi = int(idx.min()), int(idx.max())
+        if lo < 0 or hi >= packed.shape[0]:
+            raise IndexError(f"row index out of range [0, {packed.shape[0]}): {lo if lo < 0 else hi}")
+        idx32 = idx.to(device=packed.device, dtype=torch.int32)
+        status = self._lib.mxa_gather_rows(packed.data_ptr(), packed.shape[0], packed.shape[1],
+                                           idx32.data_ptr(), n, out.data_ptr(),
+                                           _stream(packed.device))
+        self._check(status, "mxa_gather_rows", 0)
+        return out
+
     def dequant_rows(self, ggml_type: int, packed: torch.Tensor, row_indices: torch.Tensor,
                      row_width: int) -> torch.Tensor:
         """Rows `row_indices` of the packed (n_rows, row_bytes) matrix, dequantized bit-exactly
