@@ -108,6 +108,13 @@ constexpr int kFusedQuantMaxRows = 4;
 int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Decode GEMV for one activation row on a workgroup-resident weight share (mxa_gemv_res.hip):
+// y[n] for n < n_rows. Quantizes act.x to Q8_K in the kernel when act.q == nullptr (IQ4_XS reads
+// it as floats). -1 when the weight is larger than the kernel is used for, or the shape or
+// alignment does not suit it.
+int launch_gemv_res(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                     int n_rows, hipStream_t stream);
+
 // One of several packed weights that share the activations of a multi-weight launch.
 struct DecodeSeg {
   int type;

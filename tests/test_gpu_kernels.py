@@ -254,6 +254,40 @@ def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None
     check_gemm(gpu, oracle, ggml_type, w, x, n, k)
 
 
+# Shapes for the one-row decode kernel (quad-per-block, whole ranges in LDS): K = 4096 at the
+# headline N (four rows per wave, 16 waves) and at small N (fewer waves per workgroup); K = 14336
+# and 2304 (groups of a unit cross row ends: 56 and 9 blocks per row); K = 512 (eight rows per
+# unit); K = 16640 (more activation groups than waves); Q6_K rows of odd block counts start on
+# 2-byte boundaries; N not a multiple of a workgroup's rows leaves idle waves.
+ONE_ROW_SHAPES = [(14336, 4096), (1024, 4096), (4096, 14336), (37, 2304), (1000, 512), (9, 768),
+                  (5, 16640), (4100, 4096), (1, 256), (300, 1280)]
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("n,k", ONE_ROW_SHAPES)
+def test_one_row_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k) -> None:
+    w = S.packed_weight(ggml_type, n, k, seed=n * 3 + k)
+    x = S.activations(1, k, seed=n + 11)
+    check_gemm(gpu, oracle, ggml_type, w, x, n, k)
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+def test_one_row_decode_weight_off_16_byte_boundary(gpu, oracle, ggml_type) -> None:
+    """A packed weight that starts 4 bytes past a 16-byte boundary (a slice of a larger buffer):
+    every wave's range then starts mid-chunk."""
+    n, k = 700, 1024
+    w = S.packed_weight(ggml_type, n, k, seed=41)
+    buf = torch.zeros(w.size + 4, dtype=torch.uint8, device="cuda")
+    buf[4:] = dev(w.reshape(-1))
+    wt = buf[4:].view(n, -1)
+    x = S.activations(1, k, seed=42)
+    y = host(gpu.matmul(ggml_type, wt, dev(x), n, k))
+    want = oracle.gemm(ggml_type, w, x, n, k)
+    assert_within_tolerance(y, want)
+    if ggml_type != D.IQ4_XS:
+        assert np.array_equal(bits(y), bits(want))
+
+
 # Shapes for the batched-decode streaming kernel (5..16 tokens): rows per workgroup = max(16,
 # N / CUs), so N = 4100 leaves a one-row tile and a three-row last workgroup, N = 5000 a four-row
 # tile; K = 2304 gives an odd block count (the last wave owns one block), K = 768 three waves;
