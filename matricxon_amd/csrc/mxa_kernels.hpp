@@ -142,6 +142,13 @@ int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act
 int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Batched decode (m_rows <= 16, rows of up to 16 blocks) with the workgroup's whole weight share
+// resident in LDS, streamed in by copy waves while compute waves run the matrix cores
+// (mxa_bflow.hip): Q4_K, Q6_K, Q8_0 on Q8_K activations in the workspace, 16-byte aligned weight
+// and rows. -1 when the share does not fit LDS (the caller uses launch_bres).
+int launch_bflow(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 // Batched decode (m_rows <= 16, rows of up to 16 blocks) with each workgroup's weight rows
 // streamed through LDS in 16-row tiles, in order: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
 // workspace. -1 when the geometry does not fit (the caller uses launch_bstream).

@@ -324,6 +324,7 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
                    int M, int N, hipStream_t stream) {
   // M <= 16: the streaming kernel, else the block-split kernel unless the 64-row tiles alone give
   // >= 512 workgroups
+  if (M <= 16 && launch_bflow(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && launch_bres(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && launch_bstream(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && N < 512 * 64) {

@@ -147,12 +147,15 @@ struct TileQ4 {
   }
   template <bool kFresh = false, class S>
   __device__ static void value(const P& p, const F& f, int, S&& sink) {
-    i32x4 sum = {0, 0, 0, 0};
+    // the two planes accumulate in independent chains (half the dependent MFMA latency); the
+    // integer result 8 * sh + sl is the same exact sum
+    i32x4 sh = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bh[t], sum, 0, 0, 0);
-    sum = sum * 8;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bl[t], sum, 0, 0, 0);
+    for (int t = 0; t < 4; ++t) {
+      sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bh[t], sh, 0, 0, 0);
+      sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], p.bl[t], sl, 0, 0, 0);
+    }
+    const i32x4 sum = sh * 8 + sl;
     // summ = sum over the 16 bsums of min_{s/2} * bsum: A = bsums (k = 4g..4g+3), B = mins
     const f32x4 summ = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bmin, f32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
