@@ -401,6 +401,16 @@ def main() -> int:
             f"matmul kernel {kern_us:.2f} us/launch (HIP events over the replay), "
             f"{results[m]['kernel_alg_gbs']:.0f} GB/s algorithmic")
 
+    # The read floor: one launch that only reads the same 33 MB (mxa_stream_read), over the same
+    # rotated copies, timed the same way. No single-launch kernel over these bytes can be faster.
+    floor_us = None
+    if not args.kernel_only:
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        floor_us = _graph_us(lambda i: gemm.stream_read(weights[i % copies], sink), args.steps,
+                             args.warmup)
+        log(f"read floor: {floor_us:.2f} us/launch for the same bytes, "
+            f"{weight_bytes() / floor_us / 1e3:.0f} GB/s")
+
     if args.configs:
         bench_configs(gemm, dev, max(20, args.steps // 4), args.warmup)
 
@@ -465,6 +475,11 @@ def main() -> int:
             "kernel": "gemv_pipe_kernel<Q4_K, M=1, fused Q8_K>",
             "kernel_us": round(r1["kernel_us"], 3),
             "bytes_per_launch": algorithmic_bytes(1),
+            # one launch that only reads the weight bytes (mxa_stream_read), timed the same way
+            "read_floor": {"us": round(floor_us, 3),
+                           "weight_gbs": round(weight_bytes() / floor_us / 1e3, 1),
+                           "frac_of_peak": round(weight_bytes() / floor_us / 1e3 / HBM_PEAK_GBS, 4),
+                           "kernel_vs_floor": round(floor_us / r1["kernel_us"], 4)},
         },
         "cpu_baseline": cpu,
     }

@@ -139,6 +139,12 @@ int mxa_dequant_rows(int ggml_type, const void *w, long long n_src_rows, const i
 int mxa_gather_rows(const void *src, long long n_src_rows, long long row_bytes,
                     const int32_t *order, int n_rows, void *dst, void *stream);
 
+/* Measurement aid, with no counterpart in the reference: reads `bytes` bytes at `src` (device,
+ * 16-byte aligned, a multiple of 16) once from HBM in one launch and computes nothing from them;
+ * `sink` is a device word it may write. The time of this launch is the floor of any one-launch
+ * kernel over the same bytes; bench.py reports the decode GEMV against it. */
+int mxa_stream_read(const void *src, long long bytes, void *sink, void *stream);
+
 /* Text of the last HIP error seen by this library on the calling thread ("" if none). */
 const char *mxa_last_error(void);
 

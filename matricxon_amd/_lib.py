@@ -28,6 +28,7 @@ EXPORTS = (
     "mxa_dequantize",
     "mxa_dequant_rows",
     "mxa_gather_rows",
+    "mxa_stream_read",
     "mxa_last_error",
 )
 
@@ -80,6 +81,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_dequant_rows.restype = _i
     lib.mxa_gather_rows.argtypes = [_vp, _ll, _ll, _vp, _i, _vp, _vp]
     lib.mxa_gather_rows.restype = _i
+    lib.mxa_stream_read.argtypes = [_vp, _ll, _vp, _vp]
+    lib.mxa_stream_read.restype = _i
     lib.mxa_last_error.argtypes = []
     lib.mxa_last_error.restype = ctypes.c_char_p
     _lib = lib

@@ -294,6 +294,14 @@ int mxa_gather_rows(const void* src, long long n_src_rows, long long row_bytes,
   return check_launch();
 }
 
+int mxa_stream_read(const void* src, long long bytes, void* sink, void* stream) {
+  if (src == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || !aligned(src, 16) ||
+      !aligned(sink, 4))
+    return MXA_ERR_UNSUPPORTED;
+  mxa::launch_stream_read(src, bytes, (uint32_t*)sink, (hipStream_t)stream);
+  return check_launch();
+}
+
 const char* mxa_last_error(void) { return g_last_error; }
 
 }  // extern "C"

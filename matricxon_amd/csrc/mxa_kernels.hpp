@@ -83,6 +83,9 @@ void launch_rms_norm_q8k(const float* x, const float* w, float eps, float* out, 
 void launch_silu_mul_q8k(const float* gate, const float* up, long long ld, float* out,
                          const ActBuffers& a, int m_rows, int k, hipStream_t stream);
 
+// Reads bytes (a multiple of 16) at src once and discards them; may write one word to sink.
+void launch_stream_read(const void* src, long long bytes, uint32_t* sink, hipStream_t stream);
+
 // dst row i = src row order[i] for i < n_rows (rows of row_bytes bytes); an index outside
 // [0, n_src_rows) gives a zero row.
 void launch_gather_rows(const void* src, long long n_src_rows, long long row_bytes,

@@ -364,6 +364,19 @@ class HipGemm:
         self._check(status, "mxa_gather_rows", 0)
         return out
 
+    def stream_read(self, data: torch.Tensor, sink: torch.Tensor) -> None:
+        """Measurement aid (no reference counterpart): one launch that reads every byte of the
+        contiguous device tensor `data` once and computes nothing from them; `sink` is a device
+        int32 word it may write. Its time is the floor of a one-launch kernel over those bytes."""
+        _require_device_tensor("data", data)
+        _require_device_tensor("sink", sink)
+        nbytes = data.numel() * data.element_size()
+        if not data.is_contiguous() or nbytes % 16 or data.data_ptr() % 16:
+            raise ValueError("data must be contiguous, 16-byte aligned, a multiple of 16 bytes")
+        status = self._lib.mxa_stream_read(data.data_ptr(), nbytes, sink.data_ptr(),
+                                           _stream(data.device))
+        self._check(status, "mxa_stream_read", 0)
+
     def dequant_rows(self, ggml_type: int, packed: torch.Tensor, row_indices: torch.Tensor,
                      row_width: int) -> torch.Tensor:
         """Rows `row_indices` of the packed (n_rows, row_bytes) matrix, dequantized bit-exactly
