@@ -236,6 +236,29 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
             report(f"{name} prefill M={m}", us, n * row_bytes(t, 4096), 2.0 * m * n * 4096)
 
 
+def prefill_eager(gemm, dev, steps: int) -> None:
+    """Eager launches of the config 5 prefill calls (the same weights and activations as
+    `--configs`), each call's mean time printed on stderr: the workload of the MFMA counter runs."""
+    import torch
+
+    from matricxon_amd import synthetic as S
+
+    for t, name, n in ((12, "Q4_K 14336x4096", 14336), (23, "IQ4_XS 4096x4096", 4096)):
+        w = torch.from_numpy(S.packed_weight(t, n, 4096, seed=60 + t)).to(dev)
+        for m in (512, 2048):
+            x = torch.from_numpy(S.activations(m, 4096, seed=70 + m)).to(dev)
+            y = torch.empty((m, n), dtype=torch.float32, device=dev)
+            gemm.matmul(t, w, x, n, 4096, out=y)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                gemm.matmul(t, w, x, n, 4096, out=y)
+            torch.cuda.synchronize()
+            us = (time.perf_counter() - t0) / steps * 1e6
+            log(f"prefill {name} M={m}: {us:.1f} us per call (eager, {steps} calls), "
+                f"{2.0 * m * n * 4096 / us / 1e6:.1f} TFLOP/s-equivalent")
+
+
 def bench_load(dev) -> None:
     """Host -> HBM upload of the config 3 packed weight (128256 x 4096 Q6_K, 431 MB) from
     pageable host memory already in the page cache: the reference's `upload_packed`
@@ -283,6 +306,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the per-launch kernel timing loop (for rocprofv3 --pmc runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only eager launches of the config 5 prefill calls (Q4_K 14336x4096 and "
+                         "IQ4_XS 4096x4096 at M=512 and 2048; for rocprofv3 --pmc runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (scale for HBM counters)")
     ap.add_argument("--load", action="store_true",
@@ -307,6 +333,10 @@ def main() -> int:
     gemm = HipGemm.get()
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    if args.prefill_only:
+        prefill_eager(gemm, dev, args.steps)
+        return 0
 
     w_np = S.packed_weight(Q4_K, N, K, seed=SEED_W)
     w0 = torch.from_numpy(w_np).to(dev)
