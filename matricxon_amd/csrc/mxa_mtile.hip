@@ -165,7 +165,9 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
             Tile::value(pp[nt], f, g, [&](int e, float v, float dd) {
               acc[mt][nt][e] = Tile::fold(acc[mt][nt][e], Ad[i * kRows + 16 * mt + 4 * g + e], v, dd);
             });
-          if constexpr (MT > 4) __builtin_amdgcn_sched_barrier(0);  // one tile's A operands at a time
+          // no scheduling barrier between tiles: the compiler overlaps one tile's fold with the
+          // next tile's A reads and MFMAs (222 VGPRs at MT = 8, no spills; measured 7% faster at
+          // M = 512 and 6% at M = 2048 than one tile at a time)
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) cur[nt] = nxt[nt];
