@@ -317,7 +317,9 @@ def test_batched_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m)
 # (K = 2304: 9 blocks, 14336: 56).
 PREFILL_SHAPES = [(129, 768, 128), (260, 2048, 200), (300, 4096, 130), (50, 14336, 140),
                   (513, 2304, 257), (1000, 4096, 320), (300, 2048, 1030), (129, 1024, 1100),
-                  (50, 4352, 1024), (513, 2304, 1089)]
+                  (50, 4352, 1024), (513, 2304, 1089),
+                  # one block per row, hundreds of workgroups (64- and 128-row activation tiles)
+                  (4096, 256, 480), (4096, 256, 800)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
