@@ -260,7 +260,7 @@ def test_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None
 # unit); K = 16640 (more activation groups than waves); Q6_K rows of odd block counts start on
 # 2-byte boundaries; N not a multiple of a workgroup's rows leaves idle waves.
 ONE_ROW_SHAPES = [(14336, 4096), (1024, 4096), (4096, 14336), (37, 2304), (1000, 512), (9, 768),
-                  (5, 16640), (4100, 4096), (1, 256), (300, 1280)]
+                  (5, 16640), (4100, 4096), (1, 256), (300, 1280), (13001, 4096)]
 
 
 @pytest.mark.parametrize("ggml_type", TYPES)
