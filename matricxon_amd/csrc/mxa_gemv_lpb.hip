@@ -819,9 +819,12 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   constexpr bool kFloatAct = TYPE == T_IQ4_XS;
   constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
   constexpr int kLdsMax = 160 * 1024;
-  constexpr int kBufKb = (15 + 64 * L::kBytes + 1023) / 1024;  // copies of a full stage, worst case
   const int nb = act.nb;
   if (nb > kWaveLanes) return -1;
+  // copies of a full stage: with 16-byte aligned rows every range starts on a copy boundary,
+  // else up to 15 bytes past one
+  const int mis_max = (((uintptr_t)w & 15) == 0 && row_bytes % 16 == 0) ? 0 : 15;
+  const int kBufKb = (mis_max + 64 * L::kBytes + 1023) / 1024;
   const int total = M * nb;
   const int act_lds = total * (kActBlk + 32 + 4) + 16;
   if (act_lds > 80 * 1024) return -1;  // the rest of LDS must still hold 2+ waves' buffers
