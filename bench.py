@@ -5,21 +5,30 @@ Q4_K GEMV 14336x4096 at M=1 (the `value`) and M=16, on seeded synthetic packed w
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 A step is one projection call through the public entry point `mxa_gemm`: Q8_K quantization of
-the activations and the fused dequantize-and-multiply over the packed weight (for M <= 4 both in
-one kernel; for M = 16 a quantization kernel, then the matmul kernel). The timed region replays a HIP graph
-of exactly K captured steps (so Python launch overhead is not measured), bracketed by
+the activations and the fused dequantize-and-multiply over the packed weight (for M <= 3 both in
+one kernel; for M = 16 a quantization kernel, then the matmul kernel). The timed region replays a
+HIP graph of exactly K captured steps (so Python launch overhead is not measured), bracketed by
 synchronizations. Each step reads a different copy of the weight (the copies together exceed
 1 GiB), so the 256 MB Infinity Cache cannot serve repeats: every weight byte comes from HBM.
 
+Timing: `ms_per_step` is device time, HIP events recorded on the replay stream around the K-step
+replay, divided by K. A GPU-side wait is queued before the first event, so the whole replay is
+submitted before the timed interval starts and the host's submission cost stays out of it (it
+would otherwise be spread over K steps and make the figure depend on K). The host wall time of a
+separate replay of the same K steps, synchronization included, is `host_ms_per_step`.
+
 roofline: the dominant kernel is the M=1 matmul kernel (it also quantizes x): every M=1 step is
-exactly one launch of it, so its average launch duration is the time between two HIP events
-recorded on the replay stream around the timed graph replay, divided by K (gaps between
-launches included); achieved = algorithmic bytes per launch / that duration. For M=16 the
-matmul kernel alone (activations quantized beforehand) is timed the same way in a graph of its
-own.
+exactly one launch of it, so its average launch duration is the event interval of the timed
+replay divided by K (gaps between launches included); achieved = algorithmic bytes per launch /
+that duration. For M=16 the matmul kernel alone (activations quantized beforehand) is timed the
+same way in a graph of its own. `traffic` is the HBM bytes per launch from rocprofv3 counters,
+read from profiles/*_traffic.json only when that file was measured on the current kernel sources
+(its `sources_sha16` equals the hash of matricxon_amd/csrc/*), else null.
 
 cpu_baseline: the reference's own C kernel `mx_gemm` (built from its sources into
-oracle/_ref/libmx_ref.so) on the host cores, M=1, same weight, ~10 s of repeated calls.
+oracle/_ref/libmx_ref.so) on the host cores, same weight: M=1 with all usable threads (the
+reference's default, the `value`), M=1 on one thread, and M=16 with all threads; the median of
+timed calls after two warm-up calls each (the pattern of tools/benchmark_kernels.py:44-57).
 """
 
 import argparse
@@ -62,11 +71,33 @@ def cpu_has_avx2() -> bool:
     return all(f in flags for f in (" avx2", " fma", " f16c"))
 
 
-def cpu_baseline(w_np, x_np, seconds: float):
-    """Reference C kernel on the host: median call time over ~`seconds` of repeats."""
+def host_layout() -> str:
+    """The host CPU's model, sockets, cores and NUMA nodes (lscpu), and the CPUs this process may
+    use."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return (f"{info.get('Model name', '?')}; {info.get('Socket(s)', '?')} socket(s) x "
+            f"{info.get('Core(s) per socket', '?')} cores x {info.get('Thread(s) per core', '?')} "
+            f"threads, {info.get('NUMA node(s)', '?')} NUMA node(s); "
+            f"{len(os.sched_getaffinity(0))} CPUs usable by this process")
+
+
+def cpu_baseline(w_np, seconds: float):
+    """The reference C kernel on the host, ~`seconds` of calls in all: M=1 on all usable threads
+    (the reference's default thread count), M=1 on one thread, M=16 on all threads. Each leg: two
+    warm-up calls, then the median of timed calls over its share of the time."""
     if not cpu_has_avx2():
         log("host CPU lacks AVX2/FMA/F16C: no CPU baseline")
         return None
+    from matricxon_amd import synthetic as S
     from oracle.native import REF_LIB, OracleGemm, RefGemm, default_threads
 
     threads = default_threads()
@@ -74,32 +105,67 @@ def cpu_baseline(w_np, x_np, seconds: float):
         impl, kind = RefGemm(), "reference"
     else:
         impl, kind = OracleGemm(), "port"
-    # as on the GPU, rotate over copies larger than the host caches (the box's CPU has 48 MiB
-    # of L2 + L3), so every call streams its weight from DRAM
+    # as on the GPU, rotate over copies larger than the host caches, so every call streams its
+    # weight from DRAM
     copies = [w_np] + [w_np.copy() for _ in range(3)]
-    for c in copies:  # warm-up (thread pool, page faults)
-        impl.gemm(Q4_K, c, x_np, N, K, threads)
-    times = []
-    start = time.perf_counter()
-    while time.perf_counter() - start < seconds and len(times) < 100000:
-        c = copies[len(times) % len(copies)]
-        t0 = time.perf_counter()
-        impl.gemm(Q4_K, c, x_np, N, K, threads)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+
+    def leg(m: int, n_threads: int, budget: float) -> tuple[float, int]:
+        x = S.activations(m, K, seed=SEED_X + m)
+        for i in range(2):
+            impl.gemm(Q4_K, copies[i], x, N, K, n_threads)
+        times = []
+        start = time.perf_counter()
+        while time.perf_counter() - start < budget and len(times) < 100000:
+            c = copies[len(times) % len(copies)]
+            t0 = time.perf_counter()
+            impl.gemm(Q4_K, c, x, N, K, n_threads)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    med1, n1 = leg(1, threads, 0.4 * seconds)
+    med1_1t, n1_1t = leg(1, 1, 0.3 * seconds)
+    med16, n16 = leg(16, threads, 0.3 * seconds)
+    wb = weight_bytes()
     return {
-        "value": round(weight_bytes() / med / 1e9, 2),
+        "value": round(wb / med1 / 1e9, 2),
         "unit": "weight GB/s",
         "cores": threads,
         "kind": kind,
-        "sample": f"Q4_K 14336x4096 M=1 x {len(times)} calls of mx_gemm (4 host copies "
-                  f"rotated, 132 MB > host L2+L3) over "
-                  f"{time.perf_counter() - start:.1f} s, median {med * 1e3:.3f} ms/call",
+        "rows_per_s": round(N / med1),
+        "one_thread_value": round(wb / med1_1t / 1e9, 2),
+        "m16_value": round(wb / med16 / 1e9, 2),
+        "m16_rows_per_s": round(N / med16),
+        "layout": host_layout(),
+        "sample": f"Q4_K 14336x4096 through mx_gemm, 4 host copies rotated (132 MB): M=1 on "
+                  f"{threads} threads {n1} calls, median {med1 * 1e3:.3f} ms; M=1 on 1 thread "
+                  f"{n1_1t} calls, median {med1_1t * 1e3:.3f} ms; M=16 on {threads} threads "
+                  f"{n16} calls, median {med16 * 1e3:.3f} ms",
     }
 
 
-def _graph_us(fn, steps: int, warmup: int) -> float:
-    """Microseconds per step of a HIP-graph replay of `steps` calls of fn(i)."""
+# GPU-side wait queued ahead of a timed replay (torch.cuda._sleep spins this many clock cycles,
+# about a millisecond): the host submits the whole replay meanwhile, so the events around it time
+# the device alone.
+LEAD_CYCLES = 3_000_000
+
+
+def replay_ms(graph) -> float:
+    """HIP-event milliseconds of one replay of `graph` on the current stream, with the replay fully
+    queued before the first event fires."""
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(LEAD_CYCLES)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
+def capture(fn, steps: int, warmup: int):
+    """A HIP graph of fn(0) .. fn(steps - 1), after `warmup` eager calls and one untimed replay."""
     import torch
 
     for i in range(warmup):
@@ -115,13 +181,15 @@ def _graph_us(fn, steps: int, warmup: int) -> float:
     torch.cuda.current_stream().wait_stream(s)
     graph.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
+    return graph
+
+
+def _graph_us(fn, steps: int, warmup: int) -> float:
+    """Device microseconds per step of a HIP-graph replay of `steps` calls of fn(i)."""
+    graph = capture(fn, steps, warmup)
+    us = replay_ms(graph) * 1e3 / steps
     del graph
-    return e0.elapsed_time(e1) * 1e3 / steps
+    return us
 
 
 def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
@@ -159,14 +227,15 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
     # q, k (Q4_K), v (Q6_K), o, gate, up (Q4_K), down (Q6_K)
     layer = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096), (12, 4096, 4096),
              (12, 14336, 4096), (12, 14336, 4096), (14, 4096, 14336)]
-    lw = [weights(t, n, k, 40 + i)[:2] for i, (t, n, k) in enumerate(layer)]
+    # four copies of the layer (556 MB > the 256 MB MALL), one per step in turn
+    lw = [weights(t, n, k, 40 + i)[:4] for i, (t, n, k) in enumerate(layer)]
     for m in (1, 16):
         xs = {k: torch.from_numpy(S.activations(m, k, seed=50 + k)).to(dev) for k in (4096, 14336)}
         ys = [torch.empty((m, n), dtype=torch.float32, device=dev) for _, n, _ in layer]
 
         def layer_step(i):
             for j, (t, n, k) in enumerate(layer):
-                gemm.matmul(t, lw[j][i % 2], xs[k], n, k, out=ys[j])
+                gemm.matmul(t, lw[j][i % 4], xs[k], n, k, out=ys[j])
         wb = sum(n * row_bytes(t, k) for t, n, k in layer)
         report(f"cfg4 llama3-8b layer (7 projections) M={m}", _graph_us(layer_step, steps, warmup),
                wb, 2.0 * m * sum(n * k for _, n, k in layer))
@@ -176,12 +245,12 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
         gu_out = torch.empty((m, 28672), dtype=torch.float32, device=dev)
 
         def layer_shared_step(i):
-            gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (0, 1, 2)],
+            gemm.matmul_multi([(layer[j][0], lw[j][i % 4], layer[j][1]) for j in (0, 1, 2)],
                               xs[4096], out=qkv_out)
-            gemm.matmul(layer[3][0], lw[3][i % 2], xs[4096], 4096, 4096, out=ys[3])
-            gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (4, 5)],
+            gemm.matmul(layer[3][0], lw[3][i % 4], xs[4096], 4096, 4096, out=ys[3])
+            gemm.matmul_multi([(layer[j][0], lw[j][i % 4], layer[j][1]) for j in (4, 5)],
                               xs[4096], out=gu_out)
-            gemm.matmul(layer[6][0], lw[6][i % 2], xs[14336], 4096, 14336, out=ys[6])
+            gemm.matmul(layer[6][0], lw[6][i % 4], xs[14336], 4096, 14336, out=ys[6])
         report(f"cfg4 llama3-8b layer (q|k|v, o, gate|up, down) M={m}",
                _graph_us(layer_shared_step, steps, warmup), wb,
                2.0 * m * sum(n * k for _, n, k in layer))
@@ -196,25 +265,25 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
 
         def layer_torch_producers(i):
             h = rms_torch(xr)
-            gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (0, 1, 2)], h,
+            gemm.matmul_multi([(layer[j][0], lw[j][i % 4], layer[j][1]) for j in (0, 1, 2)], h,
                               out=qkv_out)
-            gemm.matmul(layer[3][0], lw[3][i % 2], xr, 4096, 4096, out=ys[3])
+            gemm.matmul(layer[3][0], lw[3][i % 4], xr, 4096, 4096, out=ys[3])
             h = rms_torch(xr)
-            gate, up = gemm.matmul_multi([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (4, 5)],
+            gate, up = gemm.matmul_multi([(layer[j][0], lw[j][i % 4], layer[j][1]) for j in (4, 5)],
                                          h, out=gu_out)
             act = torch.nn.functional.silu(gate) * up
-            gemm.matmul(layer[6][0], lw[6][i % 2], act, 4096, 14336, out=ys[6])
+            gemm.matmul(layer[6][0], lw[6][i % 4], act, 4096, 14336, out=ys[6])
 
         def layer_fused_producers(i):
             _, ws = gemm.rms_norm_q8k(xr, norm_w, 1e-5)
-            gemm.matmul_multi_q8k([(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (0, 1, 2)],
+            gemm.matmul_multi_q8k([(layer[j][0], lw[j][i % 4], layer[j][1]) for j in (0, 1, 2)],
                                   ws, m, 4096, out=qkv_out)
-            gemm.matmul(layer[3][0], lw[3][i % 2], xr, 4096, 4096, out=ys[3])
+            gemm.matmul(layer[3][0], lw[3][i % 4], xr, 4096, 4096, out=ys[3])
             _, ws = gemm.rms_norm_q8k(xr, norm_w, 1e-5)
             gate, up = gemm.matmul_multi_q8k(
-                [(layer[j][0], lw[j][i % 2], layer[j][1]) for j in (4, 5)], ws, m, 4096, out=gu_out)
+                [(layer[j][0], lw[j][i % 4], layer[j][1]) for j in (4, 5)], ws, m, 4096, out=gu_out)
             _, ws = gemm.silu_mul_q8k(gate, up)
-            gemm.matmul_q8k(layer[6][0], lw[6][i % 2], ws, None, ys[6], m, 4096, 14336)
+            gemm.matmul_q8k(layer[6][0], lw[6][i % 4], ws, None, ys[6], m, 4096, 14336)
         for label, fn in (("torch RMSNorm/SwiGLU", layer_torch_producers),
                           ("fused producers", layer_fused_producers)):
             report(f"cfg4 llama3-8b layer + {label} M={m}", _graph_us(fn, steps, warmup), wb,
@@ -223,7 +292,7 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
         for j, (t, n, k) in enumerate(layer):
             if names[j] in ("k", "up"):  # same shapes as v (size) / gate
                 continue
-            us = _graph_us(lambda i: gemm.matmul(t, lw[j][i % 2], xs[k], n, k, out=ys[j]), steps, warmup)
+            us = _graph_us(lambda i: gemm.matmul(t, lw[j][i % 4], xs[k], n, k, out=ys[j]), steps, warmup)
             report(f"cfg4   {names[j]} {'Q4_K' if t == 12 else 'Q6_K'} {n}x{k} M={m}", us,
                    n * row_bytes(t, k), 2.0 * m * n * k)
     del lw
@@ -296,6 +365,153 @@ def bench_load(dev) -> None:
           file=sys.stderr, flush=True)
 
 
+def sources_sha16(files: tuple[str, ...]) -> str:
+    """Hash of the kernel sources a measurement depends on: the named files of
+    matricxon_amd/csrc and every shared header there (*.hpp). The stamp ties a counter measurement
+    to the kernels it was taken on."""
+    import hashlib
+
+    csrc = REPO / "matricxon_amd" / "csrc"
+    h = hashlib.sha256()
+    for f in sorted(csrc.iterdir()):
+        if f.suffix == ".hpp" or f.name in files:
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def traffic_of(name: str) -> int | None:
+    """HBM bytes per launch from profiles/<name>_traffic.json when it was measured on the current
+    sources of its kernel; None (and a note on stderr) when it is missing or stale."""
+    f = REPO / "profiles" / f"{name}_traffic.json"
+    if not f.exists():
+        log(f"traffic: {f.name} missing")
+        return None
+    d = json.loads(f.read_text())
+    files = next(files for prof, _, _, _, files in TRAFFIC_KERNELS if prof == name)
+    if d.get("sources_sha16") != sources_sha16(files):
+        log(f"traffic: {f.name} was measured on other kernel sources: reported as null")
+        return None
+    return int(d["hbm_bytes_per_launch"])
+
+
+def q8k_act_bytes(m: int, k: int) -> int:
+    """Bytes of m rows of Q8_K activations as the matrix-core kernels read them: int8 values, one
+    float scale and sixteen int16 sums per 256 values."""
+    return m * (k + (k // 256) * (4 + 32))
+
+
+HEAD_N = 128256
+# Workloads of `--kernel-only [--head]` whose HBM traffic `--traffic-summary` reports:
+# (profile name, kernel-name pattern, algorithmic bytes per launch, workload, kernel source files)
+TRAFFIC_KERNELS = [
+    ("gemv_pipe_q4k_14336x4096_m1", r"gemv_pipe_kernel<12, 1, ", algorithmic_bytes(1),
+     "Q4_K 14336x4096, M=1, x quantized in the kernel (weight + fp32 x + fp32 y)",
+     ("mxa_gemv_lpb.hip",)),
+    ("bflow_q4k_14336x4096_m16", r"bflow_kernel<12, ",
+     weight_bytes() + q8k_act_bytes(16, K) + 16 * N * 4,
+     "Q4_K 14336x4096, M=16, on Q8_K activations (weight + Q8_K x + fp32 y)",
+     ("mxa_bflow.hip",)),
+    ("q6k_head_128256x4096_m1", r"gemv_pipe_kernel<14, 1, ", HEAD_N * 3360 + K * 4 + HEAD_N * 4,
+     "Q6_K 128256x4096 (config 3 head), M=1 (weight + fp32 x + fp32 y)", ("mxa_gemv_lpb.hip",)),
+    ("q6k_head_128256x4096_m16", r"(bflow|bres|bstream)_kernel<14, ",
+     HEAD_N * 3360 + q8k_act_bytes(16, K) + 16 * HEAD_N * 4,
+     "Q6_K 128256x4096 (config 3 head), M=16, on Q8_K activations",
+     ("mxa_bflow.hip", "mxa_bres.hip", "mxa_bstream.hip")),
+]
+
+
+def kernel_only_head(gemm, dev, steps: int) -> None:
+    """Eager launches of the config 3 head's matmul kernel at M=1 and M=16 (431 MB, larger than
+    the MALL on its own), for counter runs."""
+    import torch
+
+    from matricxon_amd import synthetic as S
+    from matricxon_amd.gemm import q8k_bytes
+
+    w = torch.from_numpy(S.packed_weight(14, HEAD_N, K, seed=13)).to(dev)
+    for m in (1, 16):
+        x = torch.from_numpy(S.activations(m, K, seed=13 + m)).to(dev)
+        y = torch.empty((m, HEAD_N), dtype=torch.float32, device=dev)
+        ws = torch.empty(q8k_bytes(m, K), dtype=torch.uint8, device=dev)
+        fused = gemm.workspace_bytes(14, m, K) == 0
+        if not fused:
+            gemm.quantize_into(x, ws)
+        for _ in range(steps):
+            if fused:
+                gemm.matmul(14, w, x, HEAD_N, K, out=y)
+            else:
+                gemm.matmul_q8k(14, w, ws, None, y, m, HEAD_N, K)
+        torch.cuda.synchronize()
+        log(f"head M={m}: {steps} launches")
+
+
+def _pmc_values(directory: str, counter: str) -> dict[str, list[float]]:
+    """Values of `counter` per kernel name, one per dispatch, from a rocprofv3 --pmc CSV output
+    directory."""
+    import csv
+
+    vals: dict[str, list[float]] = {}
+    files = sorted(Path(directory).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {directory}")
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") == counter:
+                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return vals
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, cal_mib: int) -> int:
+    """Counter passes -> profiles/<name>_traffic.json plus a Markdown table on stdout. Each counter
+    is scaled by true / counted bytes of the calibration copy (the copy kernel with the largest
+    reading: cal_mib MiB read and written)."""
+    import re
+
+    if cal_mib <= 0:
+        raise SystemExit("--traffic-summary needs --calibrate-copy MIB (the calibration size)")
+    fetch, write = _pmc_values(fetch_dir, "FETCH_SIZE"), _pmc_values(write_dir, "WRITE_SIZE")
+    true_kib = cal_mib * 1024.0
+
+    def scale(vals: dict[str, list[float]]) -> tuple[float, str]:
+        # the calibration copy: the largest copy dispatches (the same copy kernel also moves the
+        # smaller weight uploads and clones, which are not calibrations)
+        copies = [(v, k) for k, vs in vals.items() if "copy" in k.lower() for v in vs]
+        if not copies:
+            raise SystemExit("no calibration copy kernel in the counter output")
+        top = max(v for v, _ in copies)
+        cal = [v for v, _ in copies if v >= 0.95 * top]
+        return true_kib / (sum(cal) / len(cal)), max(copies)[1]
+
+    fscale, fname = scale(fetch)
+    wscale, wname = scale(write)
+    print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch | "
+          "algorithmic bytes | ratio |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    print(f"| calibration `{fname[:40]}` ({cal_mib} MiB copy) | | scale {fscale:.4f} | "
+          f"scale {wscale:.4f} | | | |")
+    for prof, pattern, alg, workload, files in TRAFFIC_KERNELS:
+        fk = [v for k, vs in fetch.items() if re.search(pattern, k) for v in vs]
+        wk = [v for k, vs in write.items() if re.search(pattern, k) for v in vs]
+        if not fk or not wk:
+            continue
+        names = sorted(k for k in fetch if re.search(pattern, k))
+        f_kib, w_kib = sum(fk) / len(fk), sum(wk) / len(wk)
+        hbm = round((f_kib * fscale + w_kib * wscale) * 1024)
+        m = re.search(r"(\w+<[^<>]*>)\(", names[0])
+        d = {"kernel": m.group(1) if m else names[0], "workload": workload,
+             "hbm_bytes_per_launch": hbm, "fetch_kib": round(f_kib, 1),
+             "write_kib": round(w_kib, 1), "fetch_scale": round(fscale, 4),
+             "write_scale": round(wscale, 4), "dispatches": len(fk),
+             "algorithmic_bytes": alg, "ratio": round(hbm / alg, 4),
+             "sources_sha16": sources_sha16(files), "sources": list(files)}
+        (REPO / "profiles" / f"{prof}_traffic.json").write_text(json.dumps(d, indent=1) + "\n")
+        print(f"| `{d['kernel']}` ({workload}) | {d['dispatches']} | "
+              f"{f_kib:.1f} | {w_kib:.1f} | {hbm} | {alg} | {hbm / alg:.3f} |")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -316,7 +532,17 @@ def main() -> int:
                          "into HBM, the reference's pageable copy vs the staged uploader")
     ap.add_argument("--configs", action="store_true",
                     help="also time the benchmark configs 1-5 (one JSON line each on stderr)")
+    ap.add_argument("--head", action="store_true",
+                    help="with --kernel-only: also the config 3 Q6_K 128256x4096 head at M=1 "
+                         "and M=16 (for rocprofv3 --pmc runs)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU work: read the rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE CSVs of "
+                         "a --kernel-only [--head] --calibrate-copy MIB run, write "
+                         "profiles/<kernel>_traffic.json stamped with the kernel sources' hash, "
+                         "and print the summary table")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary, args.calibrate_copy)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the kernels shard by output rows)", file=sys.stderr)
@@ -358,7 +584,7 @@ def main() -> int:
             gemm.matmul(Q4_K, weights[i % copies], x, N, K, out=y)
 
         def kernel(i: int) -> None:
-            """The matmul kernel alone (for M <= 4 the same call as `step`)."""
+            """The matmul kernel alone (the same call as `step` when that kernel quantizes x)."""
             if fused:
                 gemm.matmul(Q4_K, weights[i % copies], x, N, K, out=y)
             else:
@@ -375,61 +601,43 @@ def main() -> int:
             results[m] = {"launches": args.steps}
             continue
 
-        def capture(fn):
-            for i in range(args.warmup):
-                fn(i)
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                with torch.cuda.graph(graph, stream=s):
-                    for i in range(args.steps):
-                        fn(i)
-            torch.cuda.current_stream().wait_stream(s)
-            torch.cuda.synchronize()
-            graph.replay()  # untimed replay, checked against the eager result
-            torch.cuda.synchronize()
+        def check(what: str) -> None:
             if not torch.equal(y, ref_y):
-                raise SystemExit(f"M={m}: graph replay result differs from the eager call")
-            return graph
-
-        def timed(graph):
-            """Host seconds and HIP-event milliseconds of one replay of K captured steps."""
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            e0.record()
-            graph.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            elapsed = time.perf_counter() - t0
-            if not torch.equal(y, ref_y):
-                raise SystemExit(f"M={m}: timed replay result differs from the eager call")
-            return elapsed, e0.elapsed_time(e1)
+                raise SystemExit(f"M={m}: {what} result differs from the eager call")
 
         # -- timed region: a graph of exactly K steps ------------------------------------
-        graph = capture(step)
-        elapsed, ev_ms = timed(graph)
+        graph = capture(step, args.steps, args.warmup)
+        check("graph replay")
+        torch.cuda.synchronize()  # host wall time of one replay, synchronization included
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        ev_ms = replay_ms(graph)  # the timed replay: device time of exactly K steps
+        check("timed replay")
         del graph
-        ms_step = elapsed * 1e3 / args.steps
-        kern_us = ev_ms * 1e3 / args.steps
+        ms_step = ev_ms / args.steps
+        kern_us = ms_step * 1e3
         if not fused:  # the matmul kernel alone in a graph of its own
-            graph = capture(kernel)
-            _, ev_ms = timed(graph)
+            graph = capture(kernel, args.steps, args.warmup)
+            kern_us = replay_ms(graph) * 1e3 / args.steps
+            check("kernel-only replay")
             del graph
-            kern_us = ev_ms * 1e3 / args.steps
         results[m] = {
             "ms_per_step": ms_step,
+            "host_ms_per_step": host_ms / args.steps,
             "weight_gbs": weight_bytes() / (ms_step * 1e-3) / 1e9,
             "rows_per_s": N / (ms_step * 1e-3),
             "kernel_us": kern_us,
             "kernel_weight_gbs": weight_bytes() / (kern_us * 1e-6) / 1e9,
             "kernel_alg_gbs": algorithmic_bytes(m) / (kern_us * 1e-6) / 1e9,
         }
-        log(f"M={m}: {ms_step * 1e3:.2f} us/step, {results[m]['weight_gbs']:.0f} weight GB/s; "
-            f"matmul kernel {kern_us:.2f} us/launch (HIP events over the replay), "
+        log(f"M={m}: {ms_step * 1e3:.2f} us/step (device; host {host_ms * 1e3 / args.steps:.2f}), "
+            f"{results[m]['weight_gbs']:.0f} weight GB/s; matmul kernel {kern_us:.2f} us/launch, "
             f"{results[m]['kernel_alg_gbs']:.0f} GB/s algorithmic")
+
+    if args.kernel_only and args.head:
+        kernel_only_head(gemm, dev, args.steps)
 
     # The read floor: one launch that only reads the same 33 MB (mxa_stream_read), over the same
     # rotated copies, timed the same way. No single-launch kernel over these bytes can be faster.
@@ -462,12 +670,10 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(w_np, S.activations(1, K, seed=SEED_X + 1), args.cpu_seconds)
+        cpu = cpu_baseline(w_np, args.cpu_seconds)
 
-    traffic = None
-    tf = REPO / "profiles" / "q4k_gemv_14336x4096_m1_traffic.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    traffic1 = traffic_of("gemv_pipe_q4k_14336x4096_m1")
+    traffic16 = traffic_of("bflow_q4k_14336x4096_m16")
 
     r1, r16 = results[1], results[16]
     line = {
@@ -478,6 +684,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r1["ms_per_step"], 5),
+        "host_ms_per_step": round(r1["host_ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -489,11 +696,13 @@ def main() -> int:
             "type": "Q4_K", "N": N, "K": K, "M": 1,
             "pct_of_hbm_peak": round(100 * r1["weight_gbs"] / HBM_PEAK_GBS, 1),
             "rows_per_s": round(r1["rows_per_s"]),
-            "m16": {"weight_gbs": round(r16["weight_gbs"], 1),
-                    "pct_of_hbm_peak": round(100 * r16["weight_gbs"] / HBM_PEAK_GBS, 1),
-                    "ms_per_step": round(r16["ms_per_step"], 5),
-                    "kernel_us": round(r16["kernel_us"], 2),
-                    "rows_per_s": round(r16["rows_per_s"])},
+            "m16_weight_gbs": round(r16["weight_gbs"], 1),
+            "m16_pct_of_hbm_peak": round(100 * r16["weight_gbs"] / HBM_PEAK_GBS, 1),
+            "m16_ms_per_step": round(r16["ms_per_step"], 5),
+            "m16_host_ms_per_step": round(r16["host_ms_per_step"], 5),
+            "m16_kernel_us": round(r16["kernel_us"], 3),
+            "m16_kernel_alg_gbs": round(r16["kernel_alg_gbs"], 1),
+            "m16_rows_per_s": round(r16["rows_per_s"]),
         },
         "roofline": {
             "bound": "hbm",
@@ -501,15 +710,17 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(r1["kernel_alg_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+            "traffic": traffic1,
             "kernel": "gemv_pipe_kernel<Q4_K, M=1, fused Q8_K>",
             "kernel_us": round(r1["kernel_us"], 3),
             "bytes_per_launch": algorithmic_bytes(1),
+            "m16_traffic": traffic16,
+            "m16_kernel": "bflow_kernel<Q4_K> (after quantize_q8k_kernel)",
             # one launch that only reads the weight bytes (mxa_stream_read), timed the same way
-            "read_floor": {"us": round(floor_us, 3),
-                           "weight_gbs": round(weight_bytes() / floor_us / 1e3, 1),
-                           "frac_of_peak": round(weight_bytes() / floor_us / 1e3 / HBM_PEAK_GBS, 4),
-                           "kernel_vs_floor": round(floor_us / r1["kernel_us"], 4)},
+            "read_floor_us": round(floor_us, 3),
+            "read_floor_weight_gbs": round(weight_bytes() / floor_us / 1e3, 1),
+            "read_floor_frac_of_peak": round(weight_bytes() / floor_us / 1e3 / HBM_PEAK_GBS, 4),
+            "kernel_vs_floor": round(floor_us / r1["kernel_us"], 4),
         },
         "cpu_baseline": cpu,
     }

@@ -9,7 +9,7 @@
  * Alignment: packed weights start on a 4-byte boundary; float activations `x` and `workspace`
  * on a 16-byte boundary (every allocation of the HIP allocator is); otherwise -1.
  *
- * Status codes (the reference's convention, app/native/src/mx_gemm.c:217-218, extended):
+ * Status codes (the reference's convention, app/native/src/mx_gemm.c:123-124, extended):
  *   0  ok
  *  -1  unsupported type or shape (the caller keeps another path; app/native/gemm.py:94-103)
  *  -2  workspace missing or too small (the reference's "out of memory")
@@ -38,13 +38,32 @@ extern "C" {
 #define MXA_ERR_LAUNCH (-3)
 
 /* Build description for the startup log.
- * Replaces `mx_build_info` (app/native/src/mx_gemm.c:291-314). Host-only, no GPU call. */
+ * Replaces `mx_build_info` (app/native/src/mx_gemm.c:196-220). Host-only, no GPU call. */
 const char *mxa_build_info(void);
 
 /* 1 when mxa_gemm handles (ggml_type, in_features): one of the four types and in_features a
  * positive multiple of 256; 0 otherwise.
- * Replaces `mx_supports` (app/native/src/mx_gemm.c:209-215). Host-only. */
+ * Replaces `mx_supports` (app/native/src/mx_gemm.c:114-121). Host-only. */
 int mxa_supports(int ggml_type, int in_features);
+
+/* 1 when mxa_dequant_rows handles (ggml_type, row_width): one of the four types and row_width a
+ * positive multiple of 256; 0 otherwise. (The reference's row dequantizer covers only the K-quants
+ * with an unpack routine; this one covers all four types here.)
+ * Replaces `mx_supports_dequant_rows` (app/native/src/mx_dequant_rows.c:49-56). Host-only. */
+int mxa_supports_dequant_rows(int ggml_type, int row_width);
+
+/* Activation rows up to which mxa_gemm / mxa_gemm_multi run a K-quant or Q8_0 weight on the decode
+ * kernel, which quantizes x itself (no workspace); larger calls quantize into the workspace and run
+ * on the matrix cores. Default 3, clamped to [0, 4]. Both kernels give the same bits, so this only
+ * moves the speed crossover. Process-wide; mxa_workspace_bytes follows it, so query workspace
+ * sizes after changing it.
+ * Replaces `mx_set_fused_max_tokens` (app/native/src/mx_gemm.c:11-16), the reference's crossover
+ * between its fused per-token kernel and the unpack-once path. Host-only. */
+void mxa_set_fused_max_tokens(int n_tokens);
+
+/* The current value of that crossover. No counterpart in the reference (its value is write-only
+ * there). Host-only. */
+int mxa_fused_max_tokens(void);
 
 /* Bytes of one packed row of `in_features` values (0 when unsupported). Host-only. */
 size_t mxa_row_bytes(int ggml_type, int in_features);
@@ -60,7 +79,7 @@ size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features);
  * (out_features, row_bytes) in GGUF order. The activations are quantized to Q8_K exactly as the
  * reference C kernel does (except IQ4_XS, which uses them as floats): into `workspace` first,
  * or, for n_tokens <= 3, inside the matmul kernel (one launch, no workspace).
- * Replaces `mx_gemm` (app/native/src/mx_gemm.c:219-288) and, on the GPU, the dequantize +
+ * Replaces `mx_gemm` (app/native/src/mx_gemm.c:123-194) and, on the GPU, the dequantize +
  * F.linear of `DevicePackedLinear.forward` (app/architectures/device_packed.py:53-63). */
 int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_tokens,
              int out_features, int in_features, void *workspace, size_t workspace_bytes,
@@ -70,7 +89,7 @@ int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_token
  * (written by mxa_quantize_q8_k for the same n_tokens and in_features), so only the matmul
  * kernel runs. `x` is read only for IQ4_XS (float activations) and may be NULL otherwise.
  * The reference has no separate entry: this is the second half of `mx_gemm`
- * (app/native/src/mx_gemm.c:252-284), for callers that quantize once for several weights. */
+ * (app/native/src/mx_gemm.c:158-190), for callers that quantize once for several weights. */
 int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_tokens,
                  int out_features, int in_features, const void *workspace,
                  size_t workspace_bytes, void *stream);
@@ -78,7 +97,7 @@ int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_t
 /* Up to 4 packed weights sharing one input (q/k/v, gate/up): one activation quantization, then
  * each weight's output columns written after the previous weight's, y (n_tokens, sum outs).
  * `types`, `ws` (device pointers) and `outs` are HOST arrays of n entries.
- * Replaces `mx_gemm_multi` (app/native/src/mx_gemm_multi.c:123-176); unlike the reference it
+ * Replaces `mx_gemm_multi` (app/native/src/mx_gemm_multi.c:8-62); unlike the reference it
  * also accepts prefill-sized n_tokens (the reference returns -1 there). */
 int mxa_gemm_multi(int n, const int *types, const void *const *ws, const int *outs,
                    const float *x, float *y, int n_tokens, int in_features, void *workspace,
@@ -87,26 +106,26 @@ int mxa_gemm_multi(int n, const int *types, const void *const *ws, const int *ou
 /* mxa_gemm_multi without its quantization step: `workspace` already holds the Q8_K activations
  * (mxa_quantize_q8_k, mxa_rms_norm_q8_k or mxa_silu_mul_q8_k for the same n_tokens and
  * in_features). K-quant and Q8_0 weights only (IQ4_XS reads float activations).
- * The second half of `mx_gemm_multi` (app/native/src/mx_gemm_multi.c:123-176), for groups whose
+ * The second half of `mx_gemm_multi` (app/native/src/mx_gemm_multi.c:8-62), for groups whose
  * input comes from a fused producer. */
 int mxa_gemm_multi_q8k(int n, const int *types, const void *const *ws, const int *outs, float *y,
                        int n_tokens, int in_features, const void *workspace,
                        size_t workspace_bytes, void *stream);
 
 /* RMSNorm of x (n_tokens, dim) with weight (dim) and eps, as `mx_rms_norm`
- * (app/native/src/mx_fused_ops.c:7-18): out = x * (1 / sqrtf(mean(x^2) + eps)) * weight, written
+ * (app/native/src/mx_fused_ops.c:6-17): out = x * (1 / sqrtf(mean(x^2) + eps)) * weight, written
  * to out (fp32, may be NULL) and, in the same pass, quantized to Q8_K into the workspace (layout of
  * mxa_quantize_q8_k; the blocks equal those of quantizing out). Replaces `FusedOps.rms_norm`
- * (app/architectures/layers.py:59-83) followed by the projections' quantization step. */
+ * (app/architectures/layers.py:72-76) followed by the projections' quantization step. */
 int mxa_rms_norm_q8_k(const float *x, const float *weight, float eps, int n_tokens, int dim,
                       float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /* SwiGLU's middle step out = silu(gate) * up = gate / (1 + expf(-gate)) * up, elementwise over
- * (n_tokens, dim), as `mx_silu_mul` (app/native/src/mx_fused_ops.c:39-45), written to out
+ * (n_tokens, dim), as `mx_silu_mul` (app/native/src/mx_fused_ops.c:36-42), written to out
  * (contiguous, may be NULL) and quantized to Q8_K into the workspace in the same pass (the down
  * projection's input). Rows of gate and of up are `ld` >= dim floats apart, so both may be the
  * halves of one gate|up output (ld = 2 * dim). Replaces `FusedOps.silu_mul`
- * (app/architectures/layers.py:52-56) plus that quantization. */
+ * (app/architectures/layers.py:53-57) plus that quantization. */
 int mxa_silu_mul_q8_k(const float *gate, const float *up, long long ld, int n_tokens, int dim,
                       float *out, void *workspace, size_t workspace_bytes, void *stream);
 
@@ -118,7 +137,7 @@ int mxa_quantize_q8_k(const float *x, int n_tokens, int in_features, void *works
                       size_t workspace_bytes, void *stream);
 
 /* Bit-exact dequantization of n_blocks packed blocks to fp32 (block_size values each).
- * Replaces `TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:323-325), itself a
+ * Replaces `TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:235-236), itself a
  * mirror of the numpy `QuantStrategy.dequantize`. */
 int mxa_dequantize(int ggml_type, const void *blocks, long long n_blocks, float *out,
                    void *stream);
@@ -126,7 +145,7 @@ int mxa_dequantize(int ggml_type, const void *blocks, long long n_blocks, float 
 /* Rows `rows[0..n_rows)` (device int32 indices into the n_src_rows packed rows of `w`) of a
  * packed matrix with row_width values per row, dequantized bit-exactly to out (n_rows,
  * row_width) fp32; an index outside [0, n_src_rows) gives a row of NaN.
- * Replaces `mx_dequant_rows` (app/native/src/mx_dequant_rows.c:253-281) and the per-lookup
+ * Replaces `mx_dequant_rows` (app/native/src/mx_dequant_rows.c:72-105) and the per-lookup
  * dequant of `DevicePackedEmbedding.forward` (app/architectures/device_packed.py:81-84). */
 int mxa_dequant_rows(int ggml_type, const void *w, long long n_src_rows, const int32_t *rows,
                      int n_rows, int row_width, float *out, void *stream);

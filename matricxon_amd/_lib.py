@@ -16,6 +16,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libmatricxon_amd.so"
 EXPORTS = (
     "mxa_build_info",
     "mxa_supports",
+    "mxa_supports_dequant_rows",
+    "mxa_set_fused_max_tokens",
+    "mxa_fused_max_tokens",
     "mxa_row_bytes",
     "mxa_workspace_bytes",
     "mxa_gemm",
@@ -57,6 +60,12 @@ def load() -> ctypes.CDLL:
     lib.mxa_build_info.restype = ctypes.c_char_p
     lib.mxa_supports.argtypes = [_i, _i]
     lib.mxa_supports.restype = _i
+    lib.mxa_supports_dequant_rows.argtypes = [_i, _i]
+    lib.mxa_supports_dequant_rows.restype = _i
+    lib.mxa_set_fused_max_tokens.argtypes = [_i]
+    lib.mxa_set_fused_max_tokens.restype = None
+    lib.mxa_fused_max_tokens.argtypes = []
+    lib.mxa_fused_max_tokens.restype = _i
     lib.mxa_row_bytes.argtypes = [_i, _i]
     lib.mxa_row_bytes.restype = _sz
     lib.mxa_workspace_bytes.argtypes = [_i, _i, _i]

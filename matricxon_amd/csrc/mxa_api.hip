@@ -10,6 +10,14 @@ namespace {
 
 thread_local char g_last_error[256] = "";
 
+}  // namespace
+
+namespace mxa {
+void set_last_error(const char* text) { snprintf(g_last_error, sizeof g_last_error, "%s", text); }
+}  // namespace mxa
+
+namespace {
+
 int check_launch() {
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return MXA_OK;
@@ -38,8 +46,9 @@ bool needs_q8k(int t) { return t != MXA_TYPE_IQ4_XS; }
 // The kernels read packed blocks as dwords and activations / workspace as 16-byte vectors.
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// Up to this many activation rows the matmul kernel quantizes x itself (no workspace).
-bool fused_quant(int n_tokens) { return n_tokens <= mxa::kDecodeMaxRows; }
+// Up to fmax activation rows (the crossover, read once per call) the matmul kernel quantizes x
+// itself (no workspace).
+bool fused_quant(int n_tokens, int fmax) { return n_tokens <= fmax; }
 
 mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
   mxa::Act act;
@@ -54,9 +63,9 @@ mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
 }
 
 // Workspace parts, each 256-byte aligned: the Q8_K activations (types other than IQ4_XS, more than
-// kDecodeMaxRows rows), then the bf16 split of x (IQ4_XS, kIq4MfmaMinRows rows or more).
-size_t q8k_part(bool any_q8k, int n_tokens, int k) {
-  return any_q8k && !fused_quant(n_tokens) ? mxa::align256(mxa::act_bytes(n_tokens, k)) : 0;
+// fmax rows), then the bf16 split of x (IQ4_XS, kIq4MfmaMinRows rows or more).
+size_t q8k_part(bool any_q8k, int n_tokens, int k, int fmax) {
+  return any_q8k && !fused_quant(n_tokens, fmax) ? mxa::align256(mxa::act_bytes(n_tokens, k)) : 0;
 }
 size_t split_part(bool any_iq4, int n_tokens, int k) {
   return any_iq4 && n_tokens >= mxa::kIq4MfmaMinRows ? mxa::iq4_prefill_workspace(n_tokens, k) : 0;
@@ -76,6 +85,14 @@ int mxa_supports(int ggml_type, int in_features) {
   return known_type(ggml_type) && in_features > 0 && in_features % mxa::QK == 0;
 }
 
+int mxa_supports_dequant_rows(int ggml_type, int row_width) {
+  return mxa_supports(ggml_type, row_width);
+}
+
+void mxa_set_fused_max_tokens(int n_tokens) { mxa::set_fused_max_rows(n_tokens); }
+
+int mxa_fused_max_tokens(void) { return mxa::fused_max_rows(); }
+
 size_t mxa_row_bytes(int ggml_type, int in_features) {
   if (!mxa_supports(ggml_type, in_features)) return 0;
   return (size_t)(in_features / block_elems(ggml_type)) * block_bytes(ggml_type);
@@ -84,7 +101,7 @@ size_t mxa_row_bytes(int ggml_type, int in_features) {
 size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features) {
   if (!mxa_supports(ggml_type, in_features) || n_tokens <= 0) return 0;
   if (needs_q8k(ggml_type))
-    return q8k_part(true, n_tokens, in_features);
+    return q8k_part(true, n_tokens, in_features, mxa::fused_max_rows());
   return split_part(true, n_tokens, in_features);
 }
 
@@ -152,7 +169,8 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
     total += outs[i];
   }
   hipStream_t s = (hipStream_t)stream;
-  const size_t q8k_bytes = q8k_part(any_q8k, n_tokens, in_features);
+  const int fmax = mxa::fused_max_rows();
+  const size_t q8k_bytes = q8k_part(any_q8k, n_tokens, in_features, fmax);
   const size_t split_bytes = split_part(any_iq4, n_tokens, in_features);
   const size_t need = q8k_bytes + split_bytes;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MXA_ERR_WORKSPACE;
@@ -176,7 +194,7 @@ int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* ou
       c0 += outs[i];
     }
     int st = -1;
-    if (n_tokens <= mxa::kDecodeMaxRows) {
+    if (n_tokens <= fmax) {
       st = mxa::launch_decode_multi(seg, n, act, total, n_tokens, s);
     } else {
       st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
@@ -223,9 +241,10 @@ int mxa_gemm_multi_q8k(int n, const int* types, const void* const* ws, const int
     c0 += outs[i];
   }
   if (n > 1 && n_tokens <= 16) {  // one launch for the group
-    int st = n_tokens <= mxa::kDecodeMaxRows ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
-                                             : mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
-    if (st != 0 && n_tokens > mxa::kDecodeMaxRows)
+    const int fmax = mxa::fused_max_rows();
+    int st = n_tokens <= fmax ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
+                              : mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+    if (st != 0 && n_tokens > fmax)
       st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
     if (st == 0) return check_launch();
   }

@@ -22,11 +22,13 @@
 // its own blocks' bytes in the row slots (no other wave reads those bytes, and every copy into
 // them has landed), then counts computed[t]. One tile later (and after the last tile) every
 // compute wave folds its share of a finished tile: output (weight row, activation row) over
-// blocks 0..nb-1 in order with the oracle's fused steps (app/native/src/mx_gemm.c:241-261), so
+// blocks 0..nb-1 in order with the oracle's fused steps (app/native/src/mx_dot_k_ssse3.c:115-154), so
 // the results equal the other decode kernels and the oracle bit for bit.
 //
 // Every counter only grows and every wait is for a value the other waves always reach; each wait
-// also gives up after a bounded number of polls, so no wave can spin forever.
+// also gives up after a bounded number of polls, so no wave can spin forever. A wait that gave up
+// turns what its wave writes next (block values or outputs) into NaN, so such a trip cannot pass
+// for a result.
 #include "mxa_kernels.hpp"
 #include "mxa_tiles.hpp"
 
@@ -171,7 +173,7 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
     bf_store(cnt + cw, T);  // also published by a wave with no copies
     // Folds: tile by tile as the compute waves finish them; lane l of copy wave cw takes output
     // o = 64 cw + l = (row slot o / 16, activation row o % 16) over blocks 0..nb-1 in order
-    // (mx_gemm.c:241-261), 256 lanes for the 256 outputs of a tile.
+    // (mx_dot_k_ssse3.c:115-154), 256 lanes for the 256 outputs of a tile.
     // The folds of all but the last tile overlap the compute waves' work and yield to it; the last
     // one is all that is left, at high priority.
     __builtin_amdgcn_s_setprio(0);
@@ -179,8 +181,9 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
     float xd[16];  // the lane's activation scales, the same in every tile (nb <= 16)
     bool xd_loaded = false;
     for (int t = 0; t < T; ++t) {
-      for (int spin = 0; bf_load(computed + t) < ncw && spin < kBfSpinLimit; ++spin)
-        __builtin_amdgcn_s_sleep(1);
+      int spin = 0;
+      while (bf_load(computed + t) < ncw && ++spin < kBfSpinLimit) __builtin_amdgcn_s_sleep(1);
+      const bool gave_up = spin >= kBfSpinLimit;
       asm volatile("" ::: "memory");
       if (t == T - 1) __builtin_amdgcn_s_setprio(3);
       if (!xd_loaded) {  // written by the compute waves before they counted tile 0
@@ -204,7 +207,7 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
 #pragma unroll
         for (int b = 0; b < 16; ++b)
           if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
-        y[(size_t)m * ldy + r0 + j] = acc;
+        y[(size_t)m * ldy + r0 + j] = gave_up ? __builtin_nanf("") : acc;
       }
     }
     return;
@@ -221,10 +224,12 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
   __builtin_amdgcn_s_waitcnt(0xC07F);
 
   for (int t = 0; t < T; ++t) {
-    for (int spin = 0; spin < kBfSpinLimit; ++spin) {  // the four copy waves' tiles in one read
+    int spin = 0;
+    for (; spin < kBfSpinLimit; ++spin) {  // the four copy waves' tiles in one read
       if (bf_frontier(cnt) > t) break;
       __builtin_amdgcn_s_sleep(2);
     }
+    const bool gave_up = spin == kBfSpinLimit;
     asm volatile("" ::: "memory");
     const int j = 16 * t + min(ln, rows - 16 * t - 1);  // lanes past the rows compute its last row
     float v[C][4], dv[C];
@@ -246,8 +251,8 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
       for (int c = 0; c < C; ++c) {
         if (wave * C + c < nb) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) dst[c * 16 + 4 * g + e] = v[c][e];
-          if (g == 0) dst[C * 16 + c] = dv[c];
+          for (int e = 0; e < 4; ++e) dst[c * 16 + 4 * g + e] = gave_up ? __builtin_nanf("") : v[c][e];
+          if (g == 0) dst[C * 16 + c] = gave_up ? __builtin_nanf("") : dv[c];
         }
       }
     }
@@ -286,12 +291,7 @@ int launch_bf(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
   geo.ctrl_off = T * 16 * geo.rs * 16;
   const int lds = geo.ctrl_off + nb * 16 * 4 + (kBfCopyWaves + kBfMaxTiles) * 4;
   if (lds > kBfLds) return -1;
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)bflow_kernel<TYPE, C>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kBfLds);
-    lds_set = true;
-  }
+  allow_lds((const void*)bflow_kernel<TYPE, C>, kBfLds);
   const int grid = (int)((N + (long long)R - 1) / R);
   hipLaunchKernelGGL((bflow_kernel<TYPE, C>), dim3(grid), dim3(64 * (geo.ncw + kBfCopyWaves)), lds,
                      stream, w, row_bytes, act, y, ldy, M, N, geo);

@@ -19,7 +19,7 @@
 //
 // Fold. Once every compute wave has counted computed[t], the tile's copy group folds a quarter of
 // its outputs per wave: (weight row, activation row) over blocks 0..nb-1 in order with the oracle's
-// fused steps (app/native/src/mx_gemm.c:241-261), so the results equal the other decode kernels
+// fused steps (app/native/src/mx_dot_k_ssse3.c:115-154), so the results equal the other decode kernels
 // and the oracle bit for bit; then it counts folded[t], which frees the slot. A group folds
 // whatever is computed while it waits to request, so neither group waits on the other for long.
 // Every counter only grows and every wait is for an earlier event of another wave, so the waits
@@ -313,12 +313,7 @@ int launch_br(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
   BrGeo geo;
   int lds = 0;
   if (!br_geometry(geo, row_bytes, act.nb, C, R, kBrLdsMax, &lds)) return -1;
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)bres_kernel<TYPE, C>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kBrLdsMax);
-    lds_set = true;
-  }
+  allow_lds((const void*)bres_kernel<TYPE, C>, kBrLdsMax);
   const int grid = (int)((N + (long long)R - 1) / R);
   hipLaunchKernelGGL((bres_kernel<TYPE, C>), dim3(grid), dim3(64 * (geo.ncw + kBrCopyWaves)), lds,
                      stream, w, row_bytes, act, y, ldy, M, N, geo);
@@ -354,12 +349,7 @@ int launch_br_multi(const DecodeSeg* seg, int count, const Act& act, long long l
     lds = max(lds, l);
     wg0 += (seg[i].n + R - 1) / R;
   }
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)bres_multi_kernel<C>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kBrLdsMax);
-    lds_set = true;
-  }
+  allow_lds((const void*)bres_multi_kernel<C>, kBrLdsMax);
   const int ncw = (act.nb + C - 1) / C;
   hipLaunchKernelGGL((bres_multi_kernel<C>), dim3(wg0), dim3(64 * (ncw + kBrCopyWaves)), lds, stream,
                      segs, act, ldy, M);

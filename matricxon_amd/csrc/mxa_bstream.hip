@@ -27,7 +27,7 @@
 // are built from the LDS copy with the tile builders of mxa_tiles.hpp (lane = weight row).
 //
 // Fold. One copy-wave lane per (weight row, activation row) folds the block values in order
-// 0..nb-1, part after part, with the oracle's fused steps (app/native/src/mx_gemm.c:241-261), so
+// 0..nb-1, part after part, with the oracle's fused steps (app/native/src/mx_dot_k_ssse3.c:115-154), so
 // results equal the decode kernels and the oracle bit for bit. Outputs wait in an LDS ring of
 // tiles that the compute waves write out, coalesced.
 #include "mxa_kernels.hpp"
@@ -403,12 +403,7 @@ int launch_bs(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
   geo.buf_bytes = stage_buffer_bytes<TYPE>(geo.kb);
   if (geo.buf_bytes < 0 || !bs_buffers(geo, geo.buf_bytes, geo.kb, nb)) return -1;
   const int lds = bs_lds_bytes(geo.nbuf, geo.buf_bytes, geo.ntp, geo.kb, nb);
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)bstream_kernel<TYPE, C>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    lds_set = true;
-  }
+  allow_lds((const void*)bstream_kernel<TYPE, C>, 160 * 1024);
   const int grid = (int)((N + (long long)geo.rows_per_wg - 1) / geo.rows_per_wg);
   hipLaunchKernelGGL((bstream_kernel<TYPE, C>), dim3(grid), dim3(64 * (geo.ncw + kCopyWaves)), lds,
                      stream, w, row_bytes, act, y, ldy, M, N, geo);
@@ -457,12 +452,7 @@ int launch_bs_multi(const DecodeSeg* seg, int count, const Act& act, long long l
     wg0 += (seg[i].n + R - 1) / R;
   }
   const int lds = bs_lds_bytes(geo.nbuf, buf_max, geo.ntp, geo.kb, nb);
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)bstream_multi_kernel<C>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    lds_set = true;
-  }
+  allow_lds((const void*)bstream_multi_kernel<C>, 160 * 1024);
   hipLaunchKernelGGL((bstream_multi_kernel<C>), dim3(wg0), dim3(64 * (geo.ncw + kCopyWaves)), lds,
                      stream, segs, act, ldy, M, geo);
   return 0;

@@ -3,7 +3,7 @@
 // that consume it (q|k|v and gate|up after a norm, down after SwiGLU) skip the quantize launch.
 //
 // RMSNorm: one workgroup (256 threads) per row; silu * up: one per 16 blocks of a row. The elementwise steps are the reference's, in its order
-// (app/native/src/mx_fused_ops.c:7-18, 39-45): out = x * scale * w with scale = 1 / sqrtf(sum of
+// (app/native/src/mx_fused_ops.c:6-17, 36-42): out = x * scale * w with scale = 1 / sqrtf(sum of
 // squares / dim + eps), and out = g / (1 + expf(-g)) * u. The sum of squares is a tree over the
 // workgroup (the reference's SIMD reduction has no fixed order either). Each 256-value block of the
 // result is then quantized by 16 lanes with q8k_part16, the quantize kernel's own steps, so the

@@ -11,7 +11,7 @@
 // blocks are read as dwords and realigned with v_alignbyte). The workgroup quantizes the float
 // activations to Q8_K once into LDS (the arithmetic of quantize_q8k_kernel; IQ4_XS keeps floats).
 //
-// Numerics (app/native/src/mx_gemm.c:241-261): exact integer block dots, then the per-block float
+// Numerics (app/native/src/mx_dot_k_ssse3.c:115-154): exact integer block dots, then the per-block float
 // value goes to a wave-private LDS buffer and one lane per (row, activation row) folds the blocks
 // in order 0..nb-1 with the CPU oracle's fused multiply-adds: results equal it bit for bit (IQ4_XS:
 // float activations, within tolerance).
@@ -490,11 +490,7 @@ int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, float* y, 
   const int tile_rows = geo.rows_per_wave * nw;
   const int grid = (N + tile_rows - 1) / tile_rows;
   auto kern = gemv_lpb_kernel<TYPE, MAXM, FUSEQ>;
-  static int lds_set = 0;  // the attribute only grows; one call per instantiation and size class
-  if (lds > 64 * 1024 && lds > lds_set) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    lds_set = 160 * 1024;
-  }
+  if (lds > 64 * 1024) allow_lds((const void*)kern, 160 * 1024);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, row_bytes, act, y, ldy, M, N, geo);
   return 0;
 }
@@ -863,14 +859,8 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   constexpr bool kRegOk = MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0);
   const bool actreg = kRegOk && 64 % nb == 0;
   auto kern = actreg ? gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk> : gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>;
-  static bool lds_set = false;  // both variants may be launched: allow the full LDS for each
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
-    (void)hipFuncSetAttribute((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
-    lds_set = true;
-  }
+  allow_lds((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk>, kLdsMax);
+  allow_lds((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>, kLdsMax);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (nw + na)), lds, stream, w, row_bytes, act, y,
                      ldy, M, N, geo);
   return 0;
@@ -933,14 +923,8 @@ int launch_pipe_multi(const DecodeSeg* seg, int count, const Act& act, long long
   if (!ok) return -1;
   const bool actreg = MAXM == 1 && 64 % nb == 0;
   auto kern = actreg ? gemv_pipe_multi_kernel<MAXM, FUSEQ, MAXM == 1> : gemv_pipe_multi_kernel<MAXM, FUSEQ, false>;
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)gemv_pipe_multi_kernel<MAXM, FUSEQ, MAXM == 1>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
-    (void)hipFuncSetAttribute((const void*)gemv_pipe_multi_kernel<MAXM, FUSEQ, false>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
-    lds_set = true;
-  }
+  allow_lds((const void*)gemv_pipe_multi_kernel<MAXM, FUSEQ, MAXM == 1>, kLdsMax);
+  allow_lds((const void*)gemv_pipe_multi_kernel<MAXM, FUSEQ, false>, kLdsMax);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (geo.weight_waves + na)), lds, stream, segs, act,
                      ldy, M, geo);
   return 0;

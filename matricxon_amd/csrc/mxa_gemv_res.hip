@@ -13,7 +13,7 @@
 // integer dot products of that half, summed over the pair through DPP (exact), then the group's
 // float value, which goes into LDS over the group's own bytes.
 //
-// Numerics (app/native/src/mx_gemm.c:241-261, mx_dot_k_ssse3.c:109-209, mx_dot_q8_0.c:5-22): the
+// Numerics (app/native/src/mx_dot_k_ssse3.c:115-154, mx_dot_k_ssse3.c:109-209, mx_dot_q8_0.c:5-22): the
 // per-group float steps are the CPU oracle's, and after its units a wave folds each of its rows
 // over the row's groups in order 0..nb-1 (one lane per row), so results equal the oracle bit for
 // bit. IQ4_XS keeps float activations and uses the summation order of every other IQ4_XS kernel.
@@ -311,7 +311,7 @@ __device__ __forceinline__ int fold_slot(int j) {
 }
 
 // Row r of the workgroup's rows: its groups' fold operands (left in LDS by the units) folded
-// in order 0..nb-1 with the oracle's fused steps (mx_gemm.c:241-261); y points at row 0's output.
+// in order 0..nb-1 with the oracle's fused steps (mx_dot_k_ssse3.c:115-154); y points at row 0's output.
 template <int GB>
 __device__ __forceinline__ void fold_row(const uint8_t* reg, int r, int nb, float* y) {
   float acc = 0.0f;
@@ -343,7 +343,8 @@ constexpr int kCounters = 64;  // LDS bytes of the hand-over counters at the sta
 constexpr int kUnit = 32;      // groups per unit: one per lane pair of a wave
 // Every wait on a counter gives up after this many polls (about 0.1 s): the published values
 // always reach what is waited for, and the limit only guarantees that a wave cannot spin forever
-// should that ever not hold (the outputs are then wrong, and the tests say so).
+// should that ever not hold. A wave whose wait gave up writes NaN as its groups' fold operands, so
+// every output it touched is NaN rather than a plausible wrong value.
 constexpr int kSpinLimit = 1 << 22;
 constexpr int kXReady = 8;     // counter index: activation groups ready as operands
 
@@ -506,8 +507,12 @@ __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restric
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     if (done > 0 && lane == 0) lds_add(cnt + kXReady, done);
-    for (int spin = 0; lds_load(cnt + kXReady) < nb && spin < kSpinLimit; ++spin)
-      __builtin_amdgcn_s_sleep(2);
+    bool gave_up = false;  // some wait of this wave ran out of polls
+    {
+      int spin = 0;
+      while (lds_load(cnt + kXReady) < nb && ++spin < kSpinLimit) __builtin_amdgcn_s_sleep(2);
+      gave_up |= spin >= kSpinLimit;
+    }
     asm volatile("" ::: "memory");
 
     // 3. units v = cw, cw + NW, ... of kUnit groups of the workgroup's rows
@@ -521,7 +526,8 @@ __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restric
     for (int v = cw; v < units; v += NW) {
       const int gcount = min(kUnit, groups - kUnit * v);
       const int lastc = ((kUnit * v + gcount) * GB - 1) >> 10;  // copy holding the unit's last byte
-      for (int spin = 0; spin < kSpinLimit; ++spin) {  // the four frontiers in one LDS read
+      int spin = 0;
+      for (; spin < kSpinLimit; ++spin) {  // the four frontiers in one LDS read
         const int f = frontier(cnt);
         if (f > lastc) break;
         // a copy lands about every 40 ns per CU: sleep longer when the unit is further away, so
@@ -531,6 +537,7 @@ __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restric
         else
           __builtin_amdgcn_s_sleep(1);
       }
+      gave_up |= spin == kSpinLimit;
       asm volatile("" ::: "memory");
       const int j = kUnit * v + min(g, gcount - 1);  // lanes past the rows redo their last group
       float A, B;
@@ -551,6 +558,7 @@ __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restric
       }
       // the group's fold operands go over its own bytes, which no lane reads again and no later
       // copy writes (later copies start past the unit's last byte)
+      if (gave_up) A = B = __builtin_nanf("");
       if (c == 0 && g < gcount) *(float2*)(reg + fold_slot<GB>(j)) = float2{A, B};
     }
     if constexpr (ACTREG) {
@@ -565,7 +573,7 @@ __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restric
   }
   if constexpr (ACTREG) return;
   lds_barrier();
-  // 4. fold: one thread per row takes the row's groups in order 0..nb-1 (mx_gemm.c:241-261)
+  // 4. fold: one thread per row takes the row's groups in order 0..nb-1 (mx_dot_k_ssse3.c:115-154)
   for (int r = threadIdx.x; r < nrows; r += blockDim.x) fold_row<GB>(reg, r, nb, y + n0);
 }
 
@@ -600,14 +608,8 @@ int launch_res_t(const uint8_t* w, long long row_bytes, const Act& act, float* y
   const int grid = (N + RW - 1) / RW;
   const bool actreg = Q::kQ8K && kUnit % nb == 0;
   auto kern = actreg ? gemv_res_kernel<TYPE, XQ8K, Q::kQ8K> : gemv_res_kernel<TYPE, XQ8K, false>;
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)gemv_res_kernel<TYPE, XQ8K, Q::kQ8K>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kResLds);
-    (void)hipFuncSetAttribute((const void*)gemv_res_kernel<TYPE, XQ8K, false>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kResLds);
-    lds_set = true;
-  }
+  allow_lds((const void*)gemv_res_kernel<TYPE, XQ8K, Q::kQ8K>, kResLds);
+  allow_lds((const void*)gemv_res_kernel<TYPE, XQ8K, false>, kResLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (NC + NWc)), lds, stream, w, row_bytes, act, y, N,
                      geo);
   return 0;

@@ -189,11 +189,7 @@ int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, vo
                      lo, n4);
   constexpr int MT = 4;
   constexpr int kLds = 2 * 2 * 16 * MT * kXStride;
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)iq4_mtile_kernel<MT>, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-    lds_set = true;
-  }
+  allow_lds((const void*)iq4_mtile_kernel<MT>, kLds);
   const dim3 grid((n_rows + kIq4WgRows - 1) / kIq4WgRows, (m_rows + 16 * MT - 1) / (16 * MT));
   hipLaunchKernelGGL(iq4_mtile_kernel<MT>, grid, dim3(64 * kIq4Waves), kLds, stream, w, row_bytes, hi,
                      lo, k, y, ldy, m_rows, n_rows);

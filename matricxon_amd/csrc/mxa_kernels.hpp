@@ -74,8 +74,8 @@ inline ActBuffers act_layout(void* ws, int m_rows, int k) {
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream);
 
-// Fused producers: RMSNorm (mx_rms_norm, app/native/src/mx_fused_ops.c:7-18) and SwiGLU's
-// silu(gate) * up (mx_silu_mul, mx_fused_ops.c:39-45) over m_rows rows of k values, writing the fp32
+// Fused producers: RMSNorm (mx_rms_norm, app/native/src/mx_fused_ops.c:6-17) and SwiGLU's
+// silu(gate) * up (mx_silu_mul, mx_fused_ops.c:36-42) over m_rows rows of k values, writing the fp32
 // result to out (when not nullptr) and its Q8_K blocks to a.
 void launch_rms_norm_q8k(const float* x, const float* w, float eps, float* out, const ActBuffers& a,
                          int m_rows, int k, hipStream_t stream);
@@ -96,14 +96,27 @@ int launch_dequant(int type, const uint8_t* base, const int32_t* rows, long long
                    long long row_bytes, int blocks_per_row, long long n_blocks, float* out,
                    hipStream_t stream);
 
-// Compute units of the current device (cached after the first call).
+// Text that mxa_last_error() returns on the calling thread until the next error.
+void set_last_error(const char* text);
+
+// Compute units of the current device (cached per device after the first call; thread-safe).
 int cu_count();
 
-// Activation rows up to which the pipelined decode kernel takes a matrix, quantizing x itself (no
-// workspace): K-quant / Q8_0 weights, and IQ4_XS (which reads x as floats; larger decode batches
-// run in passes of this many rows).
+// Lets `kernel` use `bytes` of dynamic LDS on the current device: the attribute is set once per
+// (kernel, device, size), under a lock, so concurrent host threads may launch.
+void allow_lds(const void* kernel, int bytes);
+
+// Activation rows up to which the pipelined decode kernel takes a K-quant / Q8_0 matrix by
+// default, quantizing x itself (no workspace); IQ4_XS (which reads x as floats) always takes up to
+// kFusedQuantMaxRows rows there, larger decode batches in passes of that many rows.
 constexpr int kDecodeMaxRows = 3;
 constexpr int kFusedQuantMaxRows = 4;
+
+// The current crossover (kDecodeMaxRows unless changed by set_fused_max_rows, clamped to
+// [0, kFusedQuantMaxRows]): rows up to it take the decode kernel, more rows the matrix cores.
+// Process-wide, read atomically by every launch.
+int fused_max_rows();
+void set_fused_max_rows(int n);
 
 // Decode GEMV for 1 <= m_rows <= 4: y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of
 // one packed weight, lane-per-block compute on weight rows staged into LDS by coalesced copies. A

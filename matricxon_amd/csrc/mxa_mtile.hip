@@ -308,12 +308,7 @@ template <int TYPE, int MT, int NT, int WAVES>
 int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
               int N, hipStream_t stream) {
   constexpr int kLds = 2 * kMtBuf<MT>;
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)mtile_kernel<TYPE, MT, NT, WAVES>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-    lds_set = true;
-  }
+  allow_lds((const void*)mtile_kernel<TYPE, MT, NT, WAVES>, kLds);
   const int rows = WAVES * 16 * NT;
   const dim3 grid((N + rows - 1) / rows, (M + 16 * MT - 1) / (16 * MT));
   hipLaunchKernelGGL((mtile_kernel<TYPE, MT, NT, WAVES>), grid, dim3(64 * WAVES), kLds, stream, w,

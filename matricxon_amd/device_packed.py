@@ -11,7 +11,7 @@ dequantizing with torch ops and calling `F.linear`.
   bytes (device_packed.py:86-89).
 * `upload_packed(raw, n_rows, device)`: (n_rows, row_bytes) uint8 device copy of packed bytes
   (device_packed.py:14-19).
-* `HipDequantizer`: the `TorchDequantizer` interface (torch_dequant.py:310-325) on the kernels.
+* `HipDequantizer`: the `TorchDequantizer` interface (torch_dequant.py:221-236) on the kernels.
 
 A float32 input that a fused producer (`matricxon_amd.fused_ops.HipFusedOps`) just wrote comes
 with its Q8_K blocks; `DevicePackedLinear` then runs the matmul alone on them.
@@ -90,7 +90,7 @@ class DevicePackedLinear(nn.Module):
     """`nn.Linear` whose weight stays quantized in device memory and is multiplied in place by
     the fused HIP kernels: x is quantized to Q8_K (IQ4_XS: kept in float32) and multiplied
     against the packed blocks with float32 accumulation, as the reference's native C kernel does
-    (app/native/src/mx_gemm.c:219-288)."""
+    (app/native/src/mx_gemm.c:123-194)."""
 
     def __init__(
         self,
@@ -164,8 +164,12 @@ class DevicePackedEmbedding(nn.Module):
         self.register_buffer("packed", packed, persistent=False)
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
-        rows = self._gemm.dequant_rows(self._ggml_type, self.packed, ids.reshape(-1),
-                                       self.embedding_dim)
+        # torch indexing semantics of the reference's `self.packed[ids]` (device_packed.py:81-84):
+        # negative ids count from the end. The wrap runs on the device (no host sync); an id
+        # outside [-num_embeddings, num_embeddings) gives a row of NaN instead of an error.
+        flat = ids.reshape(-1).to(torch.int64)
+        flat = torch.where(flat < 0, flat + self.num_embeddings, flat)
+        rows = self._gemm.dequant_rows(self._ggml_type, self.packed, flat, self.embedding_dim)
         return rows.reshape(*ids.shape, self.embedding_dim).to(self.dtype)
 
     def as_linear(self) -> DevicePackedLinear:

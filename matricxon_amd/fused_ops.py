@@ -3,19 +3,22 @@ weights on the GPU:
 
 * `HipFusedOps.rms_norm(x, weight, eps)` / `.silu_mul(gate, up)`: the `FusedOps` methods that
   `RMSNorm.forward` and `SwiGLUMLP.forward` call (app/native/fused_ops.py:152-158, 201-208;
-  app/architectures/layers.py:52-56, 76-83), same contract: the float32 result, or None when the
+  app/architectures/layers.py:53-57, 72-76), same contract: the float32 result, or None when the
   inputs are not handled (not float32 on a GPU, mismatched shapes, a last dimension that is not
   a multiple of 256) so the caller runs its torch code. Each also writes the Q8_K blocks of its
   result in the same kernel and hands them to the packed projections that read that result.
 * `project_shared(owner, names, x)`: `owner.<name>(x)` for each name, as one
   `mxa_gemm_multi` call when every module is a `DevicePackedLinear` over the same input (the
-  device side of app/architectures/shared_projection.py:36-46).
+  device side of app/architectures/shared_projection.py:33-43).
 
-The hand-off keeps the most recent producer result and its Q8_K blocks. A projection takes them
-only when its input is that very result: the same storage and element count, float32, unmodified
-since (a tensor's version counter, shared by its views, moves on any in-place write). Holding the
-result keeps its memory from being reused by another tensor while the blocks are offered.
+The hand-off keeps, per host thread, the most recent producer result and its Q8_K blocks. A
+projection takes them only when its input is that very result: the same storage and element count,
+float32, unmodified since (a tensor's version counter, shared by its views, moves on any in-place
+write), on the device and stream the producer ran on. Holding the result keeps its memory from
+being reused by another tensor while the blocks are offered.
 """
+
+import threading
 
 import torch
 from torch import nn
@@ -25,30 +28,41 @@ from matricxon_amd.gemm import HipGemm
 _IQ4_XS = 23
 
 
+def _stream_of(device: torch.device) -> int | None:
+    return torch.cuda.current_stream(device).cuda_stream if device.type == "cuda" else None
+
+
 class _Handoff:
-    """The last producer result and the workspace holding its Q8_K blocks."""
+    """The calling thread's last producer result and the workspace holding its Q8_K blocks.
+
+    One slot per host thread: the reference runs one worker thread per loaded model
+    (app/models/worker.py:15-46), so two models' forwards can interleave, and a thread must only
+    ever claim blocks it offered itself. The slot is one tuple, replaced whole, so a claim never
+    sees the parts of two different offers.
+    """
 
     def __init__(self) -> None:
-        self._out: torch.Tensor | None = None
-        self._version = -1
-        self._workspace: torch.Tensor | None = None
+        self._local = threading.local()
 
     def offer(self, out: torch.Tensor, workspace: torch.Tensor) -> None:
-        self._out, self._version, self._workspace = out, out._version, workspace
+        self._local.slot = (out, out._version, workspace, out.device, _stream_of(out.device))
 
     def clear(self) -> None:
-        self._out, self._workspace = None, None
+        """Drops the calling thread's offer."""
+        self._local.slot = None
 
     def claim(self, x: torch.Tensor) -> torch.Tensor | None:
-        """The Q8_K workspace of x if x is the offered result, unchanged, else None."""
-        out = self._out
-        if out is None or x.dtype != torch.float32 or not x.is_contiguous():
+        """The Q8_K workspace of x if x is this thread's offered result, unchanged, on the stream
+        it was produced on; else None."""
+        slot = getattr(self._local, "slot", None)
+        if slot is None or x.dtype != torch.float32 or not x.is_contiguous():
             return None
-        if (x.data_ptr() != out.data_ptr() or x.numel() != out.numel()
-                or x.shape[-1] != out.shape[-1] or x._version != self._version
-                or out._version != self._version):
+        out, version, workspace, device, stream = slot
+        if (x.device != device or x.data_ptr() != out.data_ptr() or x.numel() != out.numel()
+                or x.shape[-1] != out.shape[-1] or x._version != version
+                or out._version != version or _stream_of(device) != stream):
             return None
-        return self._workspace
+        return workspace
 
 
 HANDOFF = _Handoff()
@@ -77,7 +91,7 @@ class HipFusedOps:
         return cls._active
 
     def rms_norm(self, x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor | None:
-        """x * (1 / sqrt(mean(x^2) + eps)) * weight over the last dimension (layers.py:69-83)."""
+        """x * (1 / sqrt(mean(x^2) + eps)) * weight over the last dimension (layers.py:72-81)."""
         if (not _handled(x, weight) or weight.dim() != 1 or x.shape[-1] != weight.shape[0]
                 or x.shape[-1] % 256 != 0 or x.numel() == 0):
             return None
@@ -87,7 +101,7 @@ class HipFusedOps:
         return out
 
     def silu_mul(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor | None:
-        """silu(gate) * up elementwise (layers.py:52-56)."""
+        """silu(gate) * up elementwise (layers.py:53-57)."""
         if (not _handled(gate, up) or gate.shape != up.shape or gate.dim() == 0
                 or gate.shape[-1] % 256 != 0 or gate.numel() == 0):
             return None
@@ -99,7 +113,7 @@ class HipFusedOps:
 
 def project_shared(owner: nn.Module, names: tuple[str, ...], x: torch.Tensor) -> list[torch.Tensor]:
     """`owner.<name>(x)` for each name: one launch group for up to 4 `DevicePackedLinear` modules
-    of one input width and dtype, else each module on its own (shared_projection.py:36-46)."""
+    of one input width and dtype, else each module on its own (shared_projection.py:33-43)."""
     from matricxon_amd.device_packed import DevicePackedLinear
 
     mods = [getattr(owner, name) for name in names]

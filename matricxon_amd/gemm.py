@@ -93,7 +93,20 @@ class HipGemm:
         return supported
 
     def supports_dequant_rows(self, ggml_type: int, row_width: int) -> bool:
-        return bool(self._lib.mxa_supports(int(ggml_type), int(row_width)))
+        """Whether `dequant_rows` handles (type, row_width) (`mx_supports_dequant_rows`,
+        app/native/gemm.py:105-109): the four types here, row_width a multiple of 256."""
+        return bool(self._lib.mxa_supports_dequant_rows(int(ggml_type), int(row_width)))
+
+    def set_fused_max_tokens(self, n_tokens: int) -> None:
+        """Up to this many tokens per call a K-quant / Q8_0 matmul runs on the decode kernel, which
+        quantizes x itself; more tokens quantize into a workspace and run on the matrix cores
+        (`NativeGemm.set_fused_max_tokens`, app/native/gemm.py:156-159). Clamped to [0, 4]; both
+        kernels give the same bits, so only the speed crossover moves. Process-wide."""
+        self._lib.mxa_set_fused_max_tokens(int(n_tokens))
+
+    @property
+    def fused_max_tokens(self) -> int:
+        return int(self._lib.mxa_fused_max_tokens())
 
     def row_bytes(self, ggml_type: int, in_features: int) -> int:
         return int(self._lib.mxa_row_bytes(int(ggml_type), int(in_features)))
@@ -231,7 +244,7 @@ class HipGemm:
         self._calls += 1
         return list(torch.split(y, outs, dim=-1))
 
-    # -- fused producers: FusedOps.rms_norm / silu_mul (app/architectures/layers.py:52-83) whose
+    # -- fused producers: FusedOps.rms_norm / silu_mul (app/architectures/layers.py:53-81) whose
     #    result is also written as Q8_K for the projections that consume it ----------------------
     def rms_norm_q8k(self, x: torch.Tensor, weight: torch.Tensor, eps: float,
                      want_out: bool = True) -> tuple[torch.Tensor | None, torch.Tensor]:
@@ -326,7 +339,7 @@ class HipGemm:
         return q8k_views(ws, m, k)
 
     def dequantize(self, blocks: torch.Tensor, ggml_type: int) -> torch.Tensor:
-        """`TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:323-325): blocks
+        """`TorchDequantizer.dequantize` (app/gguf/dequant/torch_dequant.py:235-236): blocks
         (n_blocks, type_size) uint8 on the device -> (n_blocks * block_size,) float32,
         bit-exact."""
         ggml_type = int(ggml_type)
@@ -381,13 +394,16 @@ class HipGemm:
                      row_width: int) -> torch.Tensor:
         """Rows `row_indices` of the packed (n_rows, row_bytes) matrix, dequantized bit-exactly
         to (len(row_indices), row_width) float32 (NativeGemm.dequant_rows,
-        app/native/gemm.py:111-132, on the device)."""
+        app/native/gemm.py:111-132, on the device). An index outside [0, n_rows), also one past
+        the int32 range, gives a row of NaN: the kernel never reads outside the table, and the
+        call never waits for the host to check."""
         ggml_type = int(ggml_type)
         if not self.supports_dequant_rows(ggml_type, row_width):
             raise RuntimeError(f"mxa_dequant_rows failed with status -1 for type {ggml_type}")
         self._check_packed(ggml_type, packed, packed.shape[0], row_width)
-        idx = row_indices.detach().reshape(-1).to(device=packed.device,
-                                                  dtype=torch.int32).contiguous()
+        n_rows = packed.shape[0]
+        idx = row_indices.detach().reshape(-1).to(device=packed.device, dtype=torch.int64)
+        idx = idx.clamp(-1, n_rows).to(torch.int32).contiguous()
         out = torch.empty((idx.shape[0], row_width), dtype=torch.float32, device=packed.device)
         if idx.shape[0] == 0:
             return out

@@ -23,7 +23,7 @@ GEOMETRY: dict[int, tuple[int, int]] = {
 }
 
 # Every type here needs in_features % 256 == 0, Q8_0 included: its activations are quantized in
-# 256-value Q8_K blocks (app/native/src/mx_gemm.c:119-126,209-215).
+# 256-value Q8_K blocks (app/native/src/mx_gemm.c:114-121).
 SUPER_BLOCK = 256
 
 

@@ -12,7 +12,7 @@ import numpy as np
 
 def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     """out[r] = x[r] * (1 / sqrtf(sum(x[r]^2) / dim + eps)) * w, as `mx_rms_norm`
-    (app/native/src/mx_fused_ops.c:7-18): the product (x * scale) * w in that order."""
+    (app/native/src/mx_fused_ops.c:6-17): the product (x * scale) * w in that order."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     w = np.ascontiguousarray(w, dtype=np.float32)
     dim = x.shape[-1]
@@ -23,7 +23,7 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
 
 
 def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
-    """out = g / (1 + expf(-g)) * u elementwise, as `mx_silu_mul` (mx_fused_ops.c:39-45)."""
+    """out = g / (1 + expf(-g)) * u elementwise, as `mx_silu_mul` (mx_fused_ops.c:36-42)."""
     g = np.ascontiguousarray(gate, dtype=np.float32)
     u = np.ascontiguousarray(up, dtype=np.float32)
     with np.errstate(over="ignore"):

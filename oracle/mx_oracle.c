@@ -1,6 +1,6 @@
 /*
  * CPU oracle: a plain-C restatement of the reference quantized matmul `mx_gemm`
- * (app/native/src/mx_gemm.c:219-288). TEST INFRASTRUCTURE ONLY: tests, the smoke check and the
+ * (app/native/src/mx_gemm.c:123-194). TEST INFRASTRUCTURE ONLY: tests, the smoke check and the
  * CPU-baseline leg of bench.py load it as a checker; the product never links it.
  *
  * Semantics restated (file:line into the reference):
@@ -14,7 +14,7 @@
  *     32-value blocks; sumf += y.d * block_sum.
  *   - IQ4_XS on raw fp32 activations, no Q8_K (mx_dot_f32.c:32-58):
  *     acc += x[j]*(dl*K[lo]) + x[j+16]*(dl*K[hi]) sequentially.
- *   - every output row is the sequential fold over blocks 0..nb-1 (mx_gemm.c:253-261).
+ *   - every output row is the sequential fold over blocks 0..nb-1 (mx_gemm.c:158-167).
  *
  * The fp32 fold points are written with explicit fmaf() where an FMA-contracting compiler fuses
  * the reference expression (x86-64 gcc with FMA, the reference's -march=native default), and

@@ -3,9 +3,9 @@
 * `OracleGemm`  this repo's C restatement (`_build/libmx_oracle.so`).
 * `RefGemm`     the reference's own C kernels compiled from /root/reference
                 (`_ref/libmx_ref.so`, or `_ref/libmx_ref_nofma.so` with contraction off): the
-                functions bound are the reference's `mx_gemm` (app/native/src/mx_gemm.c:219),
+                functions bound are the reference's `mx_gemm` (app/native/src/mx_gemm.c:125),
                 `mx_supports` (:209), `mx_quantize_row_q8_k` (mx_common.c:42) and
-                `mx_dequant_rows` (mx_dequant_rows.c:253), with the argument types the
+                `mx_dequant_rows` (mx_dequant_rows.c:77), with the argument types the
                 reference's own binding declares (app/native/gemm.py:31-61).
 """
 

@@ -104,3 +104,31 @@ def test_modules_fail_loudly_off_gpu() -> None:
     w = torch.zeros((4, 288), dtype=torch.uint8)
     with pytest.raises(ValueError, match="HIP device"):
         g.matmul(12, w, torch.zeros(1, 512), 4, 512)
+
+
+def test_dequant_rows_support_query(lib) -> None:
+    for t in (8, 12, 14, 23):
+        assert lib.mxa_supports_dequant_rows(t, 4096) == 1
+    assert lib.mxa_supports_dequant_rows(12, 4000) == 0
+    assert lib.mxa_supports_dequant_rows(10, 4096) == 0
+
+
+def test_fused_max_tokens_moves_the_workspace_crossover(lib) -> None:
+    """`mx_set_fused_max_tokens` (app/native/src/mx_gemm.c:11-16): rows up to the crossover take
+    the decode kernel (no Q8_K workspace), more rows quantize into the workspace."""
+    assert lib.mxa_fused_max_tokens() == 3
+    try:
+        lib.mxa_set_fused_max_tokens(1)
+        assert lib.mxa_fused_max_tokens() == 1
+        assert lib.mxa_workspace_bytes(12, 1, 4096) == 0
+        assert lib.mxa_workspace_bytes(12, 2, 4096) == 8192 + 256 + 1024
+        lib.mxa_set_fused_max_tokens(0)
+        assert lib.mxa_workspace_bytes(12, 1, 4096) == 4096 + 256 + 512
+        lib.mxa_set_fused_max_tokens(99)  # clamped to the decode kernel's 4 rows
+        assert lib.mxa_fused_max_tokens() == 4
+        assert lib.mxa_workspace_bytes(12, 4, 4096) == 0
+        assert lib.mxa_workspace_bytes(23, 17, 4096) == 17 * 4096 * 4  # IQ4_XS unaffected
+        lib.mxa_set_fused_max_tokens(-5)
+        assert lib.mxa_fused_max_tokens() == 0
+    finally:
+        lib.mxa_set_fused_max_tokens(3)

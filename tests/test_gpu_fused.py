@@ -142,7 +142,7 @@ def test_fused_producer_error_paths(gpu) -> None:
 
 class _Layer(nn.Module):
     """The caller shape of RMSNorm -> q|k|v and SwiGLU gate|up -> down
-    (app/architectures/layers.py:52-83) on packed device modules."""
+    (app/architectures/layers.py:53-81) on packed device modules."""
 
     def __init__(self, k: int, ffn: int, dtype: torch.dtype) -> None:
         super().__init__()

@@ -1,5 +1,5 @@
 """Pins of the fused producer ops' oracle (oracle/fused.py): against the reference C
-(`mx_rms_norm`, `mx_silu_mul`, app/native/src/mx_fused_ops.c:7-45) through the committed
+(`mx_rms_norm`, `mx_silu_mul`, app/native/src/mx_fused_ops.c:6-42) through the committed
 fixtures and live where oracle/_ref is built, and against closed forms.
 
 Tolerance: the reference sums squares in a SIMD order of its compiler's choosing and calls libm's
