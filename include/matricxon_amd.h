@@ -85,6 +85,19 @@ int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_token
              int out_features, int in_features, void *workspace, size_t workspace_bytes,
              void *stream);
 
+/* Bytes of the static scratch array behind mxa_gemm_static (one per device). */
+#define MXA_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* mxa_gemm with no workspace argument and no device allocation anywhere on its path, for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it). No counterpart in the reference, whose mx_gemm mallocs its scratch per call. The workspace
+ * mxa_gemm would take (mxa_workspace_bytes) is a file-scope device array of
+ * MXA_STATIC_SCRATCH_BYTES per device, kept until the process ends; a call that needs more
+ * returns -2. Calls on one device share that array: calls that overlap on one device (other
+ * streams, other host threads) race and must be ordered by the caller. */
+int mxa_gemm_static(int ggml_type, const void *w, const float *x, float *y, int n_tokens,
+                    int out_features, int in_features, void *stream);
+
 /* mxa_gemm without its first step: `workspace` already holds the Q8_K activations of x
  * (written by mxa_quantize_q8_k for the same n_tokens and in_features), so only the matmul
  * kernel runs. `x` is read only for IQ4_XS (float activations) and may be NULL otherwise.

@@ -22,6 +22,7 @@ EXPORTS = (
     "mxa_row_bytes",
     "mxa_workspace_bytes",
     "mxa_gemm",
+    "mxa_gemm_static",
     "mxa_gemm_q8k",
     "mxa_gemm_multi",
     "mxa_gemm_multi_q8k",
@@ -72,6 +73,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_workspace_bytes.restype = _sz
     lib.mxa_gemm.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm.restype = _i
+    lib.mxa_gemm_static.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mxa_gemm_static.restype = _i
     lib.mxa_gemm_q8k.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_q8k.restype = _i
     lib.mxa_gemm_multi.argtypes = [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]
