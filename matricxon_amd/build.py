@@ -31,6 +31,9 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     # no packed-FP32 instructions (v_pk_*_f32) anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar / pointer kernel arguments arrive preloaded in SGPRs, so a kernel's first
+    # memory requests need no kernel-argument load (measured: -0.25 us per 33 MB launch)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -181,6 +181,12 @@ constexpr int kMaxCopies = 63;  // the largest vmcnt: copies a weight wave may h
 __device__ __forceinline__ void copy16_to_lds(const void* g, uint32_t lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr) : "memory");
 }
+// The same with the non-temporal cache policy: for bytes read exactly once per launch, so that the
+// stream does not evict from the caches what the launch reads again (its own code, the
+// activations).
+__device__ __forceinline__ void copy16_to_lds_nt(const void* g, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds_addr) : "memory");
+}
 // The same from a wave-uniform base plus a 32-bit per-lane byte offset (no 64-bit address math).
 __device__ __forceinline__ void copy16_to_lds_s(const void* base, uint32_t off, uint32_t lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
