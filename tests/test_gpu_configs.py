@@ -69,3 +69,13 @@ def test_config5_iq4_xs_prefill(gpu, oracle, m) -> None:
     w = S.packed_weight(D.IQ4_XS, 4096, 4096, seed=5)
     x = S.activations(m, 4096, seed=2005 + m)
     compare(gpu, oracle, D.IQ4_XS, w, x, 4096, 4096, rows=spread(4096)[::2])
+
+
+@pytest.mark.parametrize("t,m", [(D.Q4_K, 3), (D.IQ4_XS, 4), (D.Q8_0, 2)])
+def test_large_weight_decode_rows(gpu, oracle, t, m) -> None:
+    """Decode of weights above 64 MB (the ring-buffer streaming kernel, whose LDS slots are reused
+    many times per workgroup) at several activation rows, checked on a spread of rows."""
+    k = 4096
+    n = (72 << 20) // (k // 256 * {D.Q4_K: 144, D.IQ4_XS: 136, D.Q8_0: 272}[t])
+    w = S.packed_weight(t, n, k, seed=7)
+    compare(gpu, oracle, t, w, S.activations(m, k, seed=2000 + m), n, k, rows=spread(n))
