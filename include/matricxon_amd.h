@@ -85,6 +85,17 @@ int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_token
              int out_features, int in_features, void *workspace, size_t workspace_bytes,
              void *stream);
 
+/* y (n_tokens, out_features) = x @ W.T with x kept in float32 (never quantized to Q8_K): each
+ * weight value is its dequantized float (d * sc * q - dmin * m) meeting an unquantized activation,
+ * the numerics of the reference's fp32-activation GEMV backend. Decode-sized calls: the
+ * activation rows go through the kernel four at a time. No workspace. x must be 16-byte aligned.
+ * Replaces the Numba GEMVs `qgemv_q4_k` (app/gguf/dequant/quantized_gemv.py:51-112),
+ * `qgemv_q6_k` (quantized_gemv.py:115-180), `qgemv_q8_0`
+ * (app/gguf/dequant/quantized_gemv_legacy.py:167-194) and `qgemv_iq4_xs`
+ * (app/gguf/dequant/quantized_gemv_iq_ternary.py:65-107), which take one row (n_tokens == 1). */
+int mxa_gemv_f32(int ggml_type, const void *w, const float *x, float *y, int n_tokens,
+                 int out_features, int in_features, void *stream);
+
 /* Bytes of the static scratch array behind mxa_gemm_static (one per device). */
 #define MXA_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
 

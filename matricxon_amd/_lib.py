@@ -23,6 +23,7 @@ EXPORTS = (
     "mxa_workspace_bytes",
     "mxa_gemm",
     "mxa_gemm_static",
+    "mxa_gemv_f32",
     "mxa_gemm_q8k",
     "mxa_gemm_multi",
     "mxa_gemm_multi_q8k",
@@ -75,6 +76,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_gemm.restype = _i
     lib.mxa_gemm_static.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp]
     lib.mxa_gemm_static.restype = _i
+    lib.mxa_gemv_f32.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp]
+    lib.mxa_gemv_f32.restype = _i
     lib.mxa_gemm_q8k.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_q8k.restype = _i
     lib.mxa_gemm_multi.argtypes = [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]

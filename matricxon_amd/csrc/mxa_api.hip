@@ -127,6 +127,22 @@ int mxa_gemm(int ggml_type, const void* w, const float* x, float* y, int n_token
                         workspace_bytes, stream);
 }
 
+int mxa_gemv_f32(int ggml_type, const void* w, const float* x, float* y, int n_tokens,
+                 int out_features, int in_features, void* stream) {
+  if (!mxa_supports(ggml_type, in_features) || w == nullptr || x == nullptr || y == nullptr ||
+      n_tokens <= 0 || out_features <= 0 || !aligned(w, 4) || !aligned(x, 16))
+    return MXA_ERR_UNSUPPORTED;
+  const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
+  for (int m0 = 0; m0 < n_tokens; m0 += 4) {  // activation rows m0 .. m0 + 3
+    const int rows = n_tokens - m0 < 4 ? n_tokens - m0 : 4;
+    if (mxa::launch_gemv_f32(ggml_type, (const uint8_t*)w, rb, x + (size_t)m0 * in_features,
+                             in_features, y + (size_t)m0 * out_features, out_features, rows,
+                             out_features, (hipStream_t)stream) != 0)
+      return MXA_ERR_UNSUPPORTED;
+  }
+  return check_launch();
+}
+
 int mxa_gemm_q8k(int ggml_type, const void* w, const float* x, float* y, int n_tokens,
                  int out_features, int in_features, const void* workspace,
                  size_t workspace_bytes, void* stream) {

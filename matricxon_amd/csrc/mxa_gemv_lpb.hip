@@ -27,6 +27,24 @@ namespace {
 //   [act]  per activation row m and staged block bb: 256 q8 + kActPad | ... then bsums (32 B each)
 //          and scales (4 B each); IQ4_XS: 1024 B of floats + kActPad per block
 //   [wave] per wave: the weight bytes region (reg_bytes), then V / D buffers
+// One 16-byte piece (four floats, piece pc of 64) of a float activation block staged at `blk`. For
+// the fp32-activation types the quad of lanes holding pieces 4j .. 4j + 3 also writes sum j of the
+// block's sixteen sums of 16 ((x0 + x1) + (x2 + x3) per lane, then across the quad); every lane
+// of that quad must be active.
+template <int TYPE>
+__device__ __forceinline__ void stage_float_piece(uint8_t* blk, int pc, const uint8_t* src) {
+  const u32x4a4 u = ld16(src);
+  *(u32x4a4*)(blk + 16 * pc) = u;
+  if constexpr (ActTraits<TYPE>::kSums) {
+    // the elements are copied to scalars first: this compiler bit-casts an element expression of
+    // an ext_vector (u.y) as element 0
+    const uint32_t e0 = u[0], e1 = u[1], e2 = u[2], e3 = u[3];
+    const float s = quad_sum((__builtin_bit_cast(float, e0) + __builtin_bit_cast(float, e1)) +
+                             (__builtin_bit_cast(float, e2) + __builtin_bit_cast(float, e3)));
+    if ((pc & 3) == 0) *(float*)(blk + 4 * QK + pc) = s;  // sum pc / 4
+  }
+}
+
 struct Geometry {
   int rows_per_wave;    // R
   int blocks_per_pass;  // blocks of one row in a pass (nb when R > 1)
@@ -40,8 +58,8 @@ __global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict
                                                        float* __restrict__ y, long long ldy,
                                                        int M, int N, Geometry geo) {
   using L = Lpb<TYPE>;
-  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
-  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
+  constexpr int kActBlk = ActTraits<TYPE>::kBlk;
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
@@ -119,10 +137,11 @@ __global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict
         if (p == 0) act_d[m * ab + bb] = amax / 127.0f;
       }
     } else if constexpr (kFloatAct) {
-      for (int i = tid; i < M * cb * 64; i += blockDim.x) {  // 16-byte pieces of float rows
+      // 16-byte pieces of float rows; whole waves take part (M * cb * 64 is a multiple of 64)
+      for (int i = tid; i < M * cb * 64; i += blockDim.x) {
         const int m = i / (cb * 64), o = i - m * cb * 64, bb = o >> 6, pc = o & 63;
-        *(u32x4a4*)(act_q + (m * ab + bb) * kActBlk + 16 * pc) =
-            ld16((const uint8_t*)(act.x + (size_t)m * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
+        stage_float_piece<TYPE>(act_q + (m * ab + bb) * kActBlk, pc,
+                                (const uint8_t*)(act.x + (size_t)m * act.k + (size_t)(c0 + bb) * QK) + 16 * pc);
       }
     } else {
       for (int i = tid; i < M * cb * 16; i += blockDim.x) {  // 16-byte pieces of q8 rows
@@ -194,8 +213,8 @@ template <int TYPE, int MAXM, bool FUSEQ>
 int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                int M, int N, hipStream_t stream) {
   using L = Lpb<TYPE>;
-  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
-  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
+  constexpr int kActBlk = ActTraits<TYPE>::kBlk;
   const int nb = act.nb;
   Geometry geo;
   // blocks staged per pass: a wave's 64 lanes, and (float activations, 1 KB per block and row)
@@ -265,8 +284,8 @@ __device__ __forceinline__ int stage_copies(int s, int nblk, int mis) {
 template <int TYPE, bool FUSEQ>
 __device__ __forceinline__ void stage_activations(const Act& act, int M, int aw, int na, int lane,
                                                   uint8_t* act_q, int16_t* act_bs, float* act_d) {
-  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
-  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
+  constexpr int kActBlk = ActTraits<TYPE>::kBlk;
   const int nb = act.nb, total = M * nb;
   if constexpr (FUSEQ) {
     // 16 lanes per (m, block): lane part p holds values 16p..16p+15; kBatch groups per lane are
@@ -330,10 +349,11 @@ __device__ __forceinline__ void stage_activations(const Act& act, int M, int aw,
   } else {
     __builtin_amdgcn_s_barrier();  // first barrier
     if constexpr (kFloatAct) {
-      for (int i = aw * 64 + lane; i < total * 64; i += na * 64) {  // 16-byte pieces of float rows
+      // 16-byte pieces of float rows; whole waves take part
+      for (int i = aw * 64 + lane; i < total * 64; i += na * 64) {
         const int g = i >> 6, pc = i & 63, m = g / nb, b = g - m * nb;
-        *(u32x4a4*)(act_q + g * kActBlk + 16 * pc) =
-            ld16((const uint8_t*)(act.x + (size_t)m * act.k + (size_t)b * QK) + 16 * pc);
+        stage_float_piece<TYPE>(act_q + g * kActBlk, pc,
+                                (const uint8_t*)(act.x + (size_t)m * act.k + (size_t)b * QK) + 16 * pc);
       }
     } else {
       for (int i = aw * 64 + lane; i < total * 16; i += na * 64) {  // 16-byte pieces of q8 rows
@@ -363,8 +383,8 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
   static_assert(!ACTREG || (MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0)),
                 "register activations: one Q8_K row, types whose compute leaves room for them");
   using L = Lpb<TYPE>;
-  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
-  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
+  constexpr int kActBlk = ActTraits<TYPE>::kBlk;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar control flow
@@ -572,8 +592,7 @@ template <int TYPE, int MAXM, bool FUSEQ>
 int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                 int M, int N, hipStream_t stream) {
   using L = Lpb<TYPE>;
-  constexpr bool kFloatAct = TYPE == T_IQ4_XS;
-  constexpr int kActBlk = kFloatAct ? QK * 4 + kActPad : QK + kActPad;
+  constexpr int kActBlk = ActTraits<TYPE>::kBlk;
   constexpr int kLdsMax = 160 * 1024;
   const int nb = act.nb;
   if (nb > kWaveLanes) return -1;
@@ -702,7 +721,7 @@ int launch_decode(const uint8_t* w, long long row_bytes, const Act& act, float* 
 template <int TYPE>
 int launch_lpb_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                     int M, int N, hipStream_t stream) {
-  constexpr bool kQ8K = TYPE != T_IQ4_XS;
+  constexpr bool kQ8K = !ActTraits<TYPE>::kFloat;
   const bool fuse = kQ8K && act.q == nullptr;
   if (M == 1) return fuse ? launch_decode<TYPE, 1, kQ8K>(w, row_bytes, act, y, ldy, M, N, stream)
                           : launch_decode<TYPE, 1, false>(w, row_bytes, act, y, ldy, M, N, stream);
@@ -734,6 +753,21 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
     case T_Q4_K: return launch_lpb_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q6_K: return launch_lpb_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q8_0: return launch_lpb_type<T_Q8_0>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_IQ4_XS: return launch_lpb_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    default: return -1;
+  }
+}
+
+int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float* x, int k,
+                    float* y, long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+  if (m_rows < 1 || m_rows > 4) return -1;
+  Act act;
+  act.q = nullptr, act.d = nullptr, act.bsums = nullptr, act.x = x;
+  act.k = k, act.nb = k / QK, act.xsplit = nullptr;
+  switch (type) {
+    case T_Q4_K: return launch_lpb_type<T_Q4_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q6_K: return launch_lpb_type<T_Q6_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q8_0: return launch_lpb_type<T_Q8_0_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_IQ4_XS: return launch_lpb_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }

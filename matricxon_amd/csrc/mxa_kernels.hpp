@@ -124,6 +124,12 @@ void set_fused_max_rows(int n);
 int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// The same GEMV on float activations (x is not quantized; the K-quants and Q8_0 take each block
+// as d * sc * q - dmin * m in float against x, IQ4_XS as always): y[m * ldy + n] for
+// m < m_rows <= 4, n < n_rows, from x (m_rows, k) row-major.
+int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float* x, int k,
+                    float* y, long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 // Decode GEMV for one activation row on a workgroup-resident weight share (mxa_gemv_res.hip):
 // y[n] for n < n_rows. Quantizes act.x to Q8_K in the kernel when act.q == nullptr (IQ4_XS reads
 // it as floats). -1 when the weight is larger than the kernel is used for, or the shape or

@@ -21,6 +21,21 @@ typedef __attribute__((address_space(3))) void lds_void;
 template <int TYPE>
 struct Lpb;
 
+// Block arithmetic on float activations for the K-quants and Q8_0 (the fp32-activation GEMV: x is
+// not quantized to Q8_K): the type ids with this flag added.
+constexpr int kF32Act = 0x100;
+constexpr int T_Q8_0_F = T_Q8_0 | kF32Act, T_Q4_K_F = T_Q4_K | kF32Act, T_Q6_K_F = T_Q6_K | kF32Act;
+
+// How a block type's activations sit in LDS: Q8_K (256 int8 + padding; bsums and the scale
+// separately), or floats (256 fp32 + padding) for IQ4_XS and the fp32-activation types, which
+// also keep the sixteen sums of 16 consecutive activations after the floats.
+template <int TYPE>
+struct ActTraits {
+  static constexpr bool kFloat = TYPE == T_IQ4_XS || (TYPE & kF32Act) != 0;
+  static constexpr bool kSums = (TYPE & kF32Act) != 0;
+  static constexpr int kBlk = kFloat ? QK * 4 + (kSums ? 64 : 0) + kActPad : QK + kActPad;
+};
+
 // NW dwords of LDS from byte `off` of the 4-byte aligned `base` (off 2-byte aligned at worst).
 // LDS addresses stay base + integer offset in every kernel using these: an LDS pointer that passes
 // through an integer cast becomes a flat pointer, and flat loads are counted by vmcnt too.
@@ -35,7 +50,8 @@ __device__ __forceinline__ void lds_words(const uint8_t* base, int off, uint32_t
   for (int i = 0; i < NW; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
 }
 
-// Activations of one 256-value block of row m in LDS: q8 values, 16 bsums (or 256 floats).
+// Activations of one 256-value block of row m in LDS: q8 values, 16 bsums (or 256 floats, and for
+// the fp32-activation types the sums of their 16 runs of 16).
 struct ActBlock {
   const int8_t* q;
   const int16_t* bsums;
@@ -45,6 +61,8 @@ struct ActBlock {
   __device__ u32x4a4 bs8(int h) const { return *(const u32x4a4*)(bsums + 8 * h); }  // bsums 8h .. 8h + 7
   __device__ uint32_t bs2(int j) const { return *(const uint32_t*)(bsums + 2 * j); }  // bsums 2j, 2j + 1
   __device__ float4 x4(int off) const { return *(const float4*)(x + off); }
+  __device__ float4 s4(int c) const { return *(const float4*)(x + QK + 4 * c); }  // sums 4c .. 4c + 3
+  __device__ float s1(int j) const { return x[QK + j]; }                           // sum j
 };
 
 // The same block held in registers (one activation row): the arrays are only ever indexed with
@@ -278,6 +296,170 @@ struct Lpb<T_IQ4_XS> {
         V[m] = (L[0] + L[1]) + (L[2] + L[3]);
       }
     }
+    D = 0.0f;
+  }
+  __device__ static float fold(float acc, float, float v, float) { return acc + v; }
+};
+
+
+// ------------------------------------------------------------------ fp32 activations
+// The decode GEMV on float activations for the K-quants and Q8_0, the device counterpart of the
+// reference's fp32-activation GEMVs (app/gguf/dequant/quantized_gemv.py:51-180,
+// quantized_gemv_legacy.py:167-194): every weight value is d * sc * q (minus dmin * m for Q4_K) in
+// float and meets an unquantized activation. A sub-block's terms factor as
+// (d * sc) * sum(x * q) - (dmin * m) * sum(x): the codes q become floats exactly (one conversion
+// per value), sum(x * q) is a chain of fmaf over the sub-block in element order, and sum(x) comes
+// from the sums of 16 activations staged with them (the same for every row). The block value
+// sums its sub-block terms pairwise; rows add block values in order. Float rounding differs from
+// the reference's fastmath order; results are held to the float64 product within tolerance.
+
+template <int K>
+__device__ __forceinline__ float ubyte_f(uint32_t w) {
+  return (float)((w >> (8 * K)) & 0xFFu);
+}
+
+// p + x . (four unsigned bytes of w as floats), in element order
+__device__ __forceinline__ float dot4_f(float4 x, uint32_t w, float p) {
+  p = fmaf(x.x, ubyte_f<0>(w), p);
+  p = fmaf(x.y, ubyte_f<1>(w), p);
+  p = fmaf(x.z, ubyte_f<2>(w), p);
+  return fmaf(x.w, ubyte_f<3>(w), p);
+}
+
+template <>
+struct Lpb<T_Q4_K_F> {
+  static constexpr int kBytes = 144;
+  static constexpr bool kHasD = false;
+  // sub-block sb: (d * sc_sb) * sum(x * q) - (dmin * m_sb) * sum(x); high nibbles are taken as
+  // 16 q (one bit operation), whose exact factor 1/16 goes into their scale
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
+    const uint8_t* blk = wb + off;  // 4-byte aligned
+    const u32x4a4 h = *(const u32x4a4*)blk;
+    uint32_t q[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x4a4 v = *(const u32x4a4*)(blk + 16 + 16 * i);
+      q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
+    }
+    const float d = half_to_float(h.x), dmin = half_to_float(h.x >> 16);
+    const K4Scales s = k4_scales(h.y, h.z, h.w);
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      if (m < M) {
+        float t[8];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float plo = 0.0f, phi = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t w = q[8 * c + i];
+            plo = dot4_f(a[m].x4(64 * c + 4 * i), w & 0x0F0F0F0Fu, plo);
+            phi = dot4_f(a[m].x4(64 * c + 32 + 4 * i), w & 0xF0F0F0F0u, phi);
+          }
+          const float4 sx = a[m].s4(c);  // sums of elements 64c .. 64c + 63, 16 at a time
+          const float d1 = d * (float)k4_pick(s.sc_lo, s.sc_hi, 2 * c);
+          const float m1 = dmin * (float)k4_pick(s.mn_lo, s.mn_hi, 2 * c);
+          const float d2 = (d * (float)k4_pick(s.sc_lo, s.sc_hi, 2 * c + 1)) * 0.0625f;
+          const float m2 = dmin * (float)k4_pick(s.mn_lo, s.mn_hi, 2 * c + 1);
+          t[2 * c] = fmaf(d1, plo, -(m1 * (sx.x + sx.y)));
+          t[2 * c + 1] = fmaf(d2, phi, -(m2 * (sx.z + sx.w)));
+        }
+        V[m] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+      }
+    }
+    D = 0.0f;
+  }
+  __device__ static float fold(float acc, float, float v, float) { return acc + v; }
+};
+
+template <>
+struct Lpb<T_Q6_K_F> {
+  static constexpr int kBytes = 210;
+  static constexpr bool kHasD = false;
+  // sub-block sb of 16: (d * sc_sb) * (sum(x * u) - 32 sum(x)), u = q + 32 the stored code
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
+    uint32_t w[53];  // bytes 0..211: ql 0..127, qh 128..191, scales 192..207, d 208..209
+    lds_words<53>(wb, off, w);
+    const float d = half_to_float(w[52]);
+    float r[MAXM][8];  // sums of sub-block pairs 2i, 2i + 1
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint32_t U[8];  // codes of elements 128h + 32g + 4i .. +3
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t l = w[16 * h + ((g & 1) ? 8 : 0) + i], qh = w[32 + 8 * h + i];
+          U[i] = g == 0 ? q6_codes<0>(l, qh) : g == 1 ? q6_codes<1>(l, qh)
+               : g == 2 ? q6_codes<2>(l, qh) : q6_codes<3>(l, qh);
+        }
+        const int sb = 8 * h + 2 * g;  // sub-blocks sb, sb + 1
+        const float dsc0 = d * (float)(int)(int8_t)(uint8_t)(w[48 + (sb >> 2)] >> (8 * (sb & 3)));
+        const float dsc1 = d * (float)(int)(int8_t)(uint8_t)(w[48 + (sb >> 2)] >> (8 * (sb & 3) + 8));
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m) {
+          if (m < M) {
+            float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              p0 = dot4_f(a[m].x4(128 * h + 32 * g + 4 * i), U[i], p0);
+              p1 = dot4_f(a[m].x4(128 * h + 32 * g + 16 + 4 * i), U[4 + i], p1);
+            }
+            r[m][4 * h + g] = dsc0 * fmaf(-32.0f, a[m].s1(sb), p0) + dsc1 * fmaf(-32.0f, a[m].s1(sb + 1), p1);
+          }
+        }
+      }
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m)
+      if (m < M) V[m] = ((r[m][0] + r[m][1]) + (r[m][2] + r[m][3])) + ((r[m][4] + r[m][5]) + (r[m][6] + r[m][7]));
+    D = 0.0f;
+  }
+  __device__ static float fold(float acc, float, float v, float) { return acc + v; }
+};
+
+template <>
+struct Lpb<T_Q8_0_F> {
+  static constexpr int kBytes = 272;  // eight 34-byte blocks
+  static constexpr bool kHasD = false;
+  // block k of 32: d_k * (sum(x * (q + 128)) - 128 sum(x)), the signed codes taken as unsigned
+  // bytes q + 128 (one bit operation)
+  template <int MAXM, class A>
+  __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
+    const uint8_t* blk = wb + off;  // 4-byte aligned
+    float t[MAXM][8];
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {  // pairs of 34-byte blocks: 68 bytes, 17 words
+      uint32_t w[17];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4a4 v = *(const u32x4a4*)(blk + 68 * pr + 16 * i);
+        w[4 * i] = v.x, w[4 * i + 1] = v.y, w[4 * i + 2] = v.z, w[4 * i + 3] = v.w;
+      }
+      w[16] = *(const uint32_t*)(blk + 68 * pr + 64);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int k = 2 * pr + e;
+        const float dk = e == 0 ? half_to_float(w[0]) : half_to_float(w[8] >> 16);
+        uint32_t qs[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          qs[i] = (e == 0 ? __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2) : w[9 + i]) ^ 0x80808080u;
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m) {
+          if (m < M) {
+            float p = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) p = dot4_f(a[m].x4(32 * k + 4 * i), qs[i], p);
+            t[m][k] = dk * fmaf(-128.0f, a[m].s1(2 * k) + a[m].s1(2 * k + 1), p);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m)
+      if (m < M) V[m] = ((t[m][0] + t[m][1]) + (t[m][2] + t[m][3])) + ((t[m][4] + t[m][5]) + (t[m][6] + t[m][7]));
     D = 0.0f;
   }
   __device__ static float fold(float acc, float, float v, float) { return acc + v; }

@@ -18,8 +18,16 @@ with its Q8_K blocks; `DevicePackedLinear` then runs the matmul alone on them.
 
 Only Q8_0, Q4_K, Q6_K and IQ4_XS (with in_features % 256 == 0) are computed here; a loader
 asks `HipDequantizer.supports` / `HipGemm.supports` and keeps the reference module for the rest.
+
+`MATRICXON_GEMV_BACKEND` (app/config.py:123, "native" by default) picks the activation numerics of
+`DevicePackedLinear`: "native" quantizes x to Q8_K as the reference's C kernels do; "numba" keeps x
+in float32 for decode-sized calls (`mxa_gemv_f32`, the Numba GEMVs' numerics,
+app/gguf/dequant/quantized_gemv.py:51-180) and, like the reference's QuantizedLinear prefill
+(app/architectures/quantized_linear.py:101-106), dequantizes the weight transiently to the layer
+dtype for larger calls.
 """
 
+import os
 import warnings
 
 import numpy as np
@@ -31,6 +39,17 @@ from matricxon_amd.gemm import HipGemm
 from matricxon_amd.quant_types import GEOMETRY
 
 _IQ4_XS = 23
+GEMV_BACKENDS = ("native", "numba")
+F32_GEMV_MAX_ROWS = 4  # "numba" backend: rows per call that take the fp32-activation GEMV
+
+
+def gemv_backend() -> str:
+    """`MATRICXON_GEMV_BACKEND`, "native" when unset; ValueError for another value (the
+    reference's settings accept only these two, app/config.py:123)."""
+    value = os.environ.get("MATRICXON_GEMV_BACKEND", "native").strip().lower()
+    if value not in GEMV_BACKENDS:
+        raise ValueError(f"MATRICXON_GEMV_BACKEND must be one of {GEMV_BACKENDS}, got {value!r}")
+    return value
 
 
 _UPLOADERS: dict[torch.device, "PackedUploader"] = {}
@@ -99,6 +118,8 @@ class DevicePackedLinear(nn.Module):
         ggml_type: int,
         bias: torch.Tensor | None = None,
         dtype: torch.dtype = torch.bfloat16,
+        *,
+        backend: str | None = None,
     ) -> None:
         super().__init__()
         gemm = HipGemm.get()
@@ -106,6 +127,10 @@ class DevicePackedLinear(nn.Module):
             raise ValueError(
                 f"no HIP kernel for GGML type {int(ggml_type)} with in_features={in_features}"
             )
+        backend = gemv_backend() if backend is None else backend
+        if backend not in GEMV_BACKENDS:
+            raise ValueError(f"backend must be one of {GEMV_BACKENDS}, got {backend!r}")
+        self.backend = backend
         self.out_features = packed.shape[0]
         self.in_features = in_features
         self._ggml_type = int(ggml_type)
@@ -128,6 +153,8 @@ class DevicePackedLinear(nn.Module):
         x = x.to(self._dtype)
         lead = x.shape[:-1]
         k = self.in_features
+        if self.backend == "numba":
+            return self.finish(self._forward_f32(x.reshape(-1, k)), lead)
         ws = HANDOFF.claim(x) if self._ggml_type != _IQ4_XS else None
         if ws is not None:  # x came from a fused producer that also wrote its Q8_K blocks
             n = x.numel() // k
@@ -137,6 +164,18 @@ class DevicePackedLinear(nn.Module):
             y = self._gemm.matmul(self._ggml_type, self.packed, x.reshape(-1, k),
                                   self.out_features, k)
         return self.finish(y, lead)
+
+    def _forward_f32(self, x2: torch.Tensor) -> torch.Tensor:
+        """The "numba" backend: float32 activations against the dequantized weight values, through
+        the fp32-activation GEMV for decode-sized calls, else a transient dequantization to the
+        layer dtype and a matmul (quantized_linear.py:101-106). (M, N) float32."""
+        k, n = self.in_features, self.out_features
+        if x2.shape[0] <= F32_GEMV_MAX_ROWS:
+            return self._gemm.gemv_f32(self._ggml_type, self.packed, x2, n, k)
+        weight = self._gemm.dequantize(self.packed, self._ggml_type).reshape(n, k).to(self._dtype)
+        y = (x2.to(self._dtype) @ weight.T).to(torch.float32)
+        del weight
+        return y
 
     def finish(self, y: torch.Tensor, lead: tuple[int, ...]) -> torch.Tensor:
         """Float32 result rows (M, N) -> the layer's output (..., N) in its dtype, plus bias."""

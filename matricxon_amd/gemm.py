@@ -52,6 +52,12 @@ def _require_device_tensor(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be a tensor on a HIP device, got {getattr(t, 'device', t)}")
 
 
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """`t`, or a copy of it when its data does not start on a 16-byte boundary (the kernels read
+    activations as 16-byte vectors; a view into the middle of a tensor may start anywhere)."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 class HipGemm:
     _active: "HipGemm | None" = None
 
@@ -154,8 +160,8 @@ class HipGemm:
         if not self.supports(ggml_type, in_features):
             raise RuntimeError(f"mxa_gemm failed with status -1 for type {ggml_type}")
         self._check_packed(ggml_type, packed, out_features, in_features)
-        x32 = x.detach().reshape(-1, in_features).to(device=packed.device,
-                                                     dtype=torch.float32).contiguous()
+        x32 = _aligned16(x.detach().reshape(-1, in_features).to(device=packed.device,
+                                                                dtype=torch.float32).contiguous())
         n_tokens = x32.shape[0]
         if out is None:
             out = torch.empty((n_tokens, out_features), dtype=torch.float32, device=packed.device)
@@ -170,6 +176,33 @@ class HipGemm:
                                     n_tokens, out_features, in_features, ws.data_ptr(), ws_bytes,
                                     _stream(packed.device))
         self._check(status, "mxa_gemm", ggml_type)
+        self._calls += 1
+        return out
+
+    def gemv_f32(self, ggml_type: int, packed: torch.Tensor, x: torch.Tensor, out_features: int,
+                 in_features: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """`matmul` with x kept in float32 (never quantized to Q8_K), the numerics of the
+        reference's fp32-activation GEMVs (app/gguf/dequant/quantized_gemv.py:51-180). Meant for
+        decode-sized calls: the kernel takes four activation rows per pass over the weight.
+        `x`: (n_tokens, in_features); returns (n_tokens, out_features) float32."""
+        ggml_type = int(ggml_type)
+        if not self.supports(ggml_type, in_features):
+            raise RuntimeError(f"mxa_gemv_f32 failed with status -1 for type {ggml_type}")
+        self._check_packed(ggml_type, packed, out_features, in_features)
+        x32 = _aligned16(x.detach().reshape(-1, in_features).to(device=packed.device,
+                                                                dtype=torch.float32).contiguous())
+        n_tokens = x32.shape[0]
+        if out is None:
+            out = torch.empty((n_tokens, out_features), dtype=torch.float32, device=packed.device)
+        elif out.shape != (n_tokens, out_features) or out.dtype != torch.float32 or \
+                not out.is_contiguous() or out.device != packed.device:
+            raise ValueError("out must be a contiguous float32 (n_tokens, out_features) tensor")
+        if n_tokens == 0:
+            return out
+        status = self._lib.mxa_gemv_f32(ggml_type, packed.data_ptr(), x32.data_ptr(),
+                                        out.data_ptr(), n_tokens, out_features, in_features,
+                                        _stream(packed.device))
+        self._check(status, "mxa_gemv_f32", ggml_type)
         self._calls += 1
         return out
 

@@ -84,6 +84,13 @@ def test_argument_errors_return_status_without_launching(lib) -> None:
     assert lib.mxa_quantize_q8_k(a, 2, 512, a, 10, None) == -2
     assert lib.mxa_dequantize(11, a, 4, a, None) == -1
     assert lib.mxa_dequant_rows(12, a, 10, a, 2, 300, a, None) == -1
+    # fp32-activation GEMV: unsupported type / shape, null or misaligned operands -> -1
+    assert lib.mxa_gemv_f32(10, a, a, a, 1, 4, 4096, None) == -1
+    assert lib.mxa_gemv_f32(12, a, a, a, 1, 4, 4000, None) == -1
+    assert lib.mxa_gemv_f32(14, a, None, a, 1, 4, 4096, None) == -1
+    assert lib.mxa_gemv_f32(8, a, a, a, 0, 4, 4096, None) == -1
+    assert lib.mxa_gemv_f32(23, a, vp(0x10008), a, 1, 4, 4096, None) == -1
+    assert lib.mxa_gemv_f32(12, vp(0x10002), a, a, 1, 4, 4096, None) == -1
     n = 5
     types = (ctypes.c_int * n)(*([12] * n))
     assert lib.mxa_gemm_multi(n, types, a, a, a, a, 1, 4096, a, 1 << 20, None) == -1
@@ -132,3 +139,26 @@ def test_fused_max_tokens_moves_the_workspace_crossover(lib) -> None:
         assert lib.mxa_fused_max_tokens() == 0
     finally:
         lib.mxa_set_fused_max_tokens(3)
+
+
+def test_fp32_gemv_registry_and_backend_setting(monkeypatch) -> None:
+    """The Numba-registry mirror (quantized_gemv_registry.py:63-93) and MATRICXON_GEMV_BACKEND."""
+    import torch
+
+    from matricxon_amd import device_packed as DP
+    from matricxon_amd.quantized_gemv import GEMV_KERNELS, has_gemv_kernel, qgemv_q6_k
+
+    assert {t: size for t, (_, size) in GEMV_KERNELS.items()} == {8: 34, 12: 144, 14: 210, 23: 136}
+    assert has_gemv_kernel(12) and not has_gemv_kernel(2) and not has_gemv_kernel(10)
+    with pytest.raises(ValueError, match="multiple of block_size"):
+        qgemv_q6_k(torch.zeros(300), torch.zeros(210, dtype=torch.uint8), 1, 300)
+    monkeypatch.delenv("MATRICXON_GEMV_BACKEND", raising=False)
+    assert DP.gemv_backend() == "native"
+    monkeypatch.setenv("MATRICXON_GEMV_BACKEND", "Numba")
+    assert DP.gemv_backend() == "numba"
+    monkeypatch.setenv("MATRICXON_GEMV_BACKEND", "triton")
+    with pytest.raises(ValueError, match="MATRICXON_GEMV_BACKEND"):
+        DP.gemv_backend()
+    g = DP.HipGemm.get()
+    with pytest.raises(ValueError, match="HIP device"):
+        g.gemv_f32(14, torch.zeros((1, 210), dtype=torch.uint8), torch.zeros(1, 256), 1, 256)
