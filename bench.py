@@ -221,9 +221,23 @@ def bench_configs(gemm, dev, steps: int, warmup: int) -> None:
             report(f"{name} M={m}", us, n * row_bytes(t, k), 2.0 * m * n * k)
         del ws
 
+    def gemv_f32(name, t, n, k, ms, seed):
+        ws = weights(t, n, k, seed)
+        for m in ms:
+            x = torch.from_numpy(S.activations(m, k, seed=seed + m)).to(dev)
+            y = torch.empty((m, n), dtype=torch.float32, device=dev)
+            us = _graph_us(lambda i: gemm.gemv_f32(t, ws[i % len(ws)], x, n, k, out=y), steps, warmup)
+            report(f"{name} M={m} fp32 activations", us, n * row_bytes(t, k), 2.0 * m * n * k)
+        del ws
+
     gemv("cfg1 Q8_0 4096x4096", 8, 4096, 4096, [1], 11)
     gemv("cfg2 Q4_K 14336x4096", 12, 14336, 4096, [1, 2, 3, 4, 8, 16], 12)
     gemv("cfg3 Q6_K 128256x4096", 14, 128256, 4096, [1, 16], 13)
+    # the fp32-activation GEMV (x not quantized), decode sizes
+    gemv_f32("cfg1 Q8_0 4096x4096", 8, 4096, 4096, [1], 11)
+    gemv_f32("cfg2 Q4_K 14336x4096", 12, 14336, 4096, [1, 4], 12)
+    gemv_f32("cfg3 Q6_K 128256x4096", 14, 128256, 4096, [1], 13)
+    gemv_f32("IQ4_XS 4096x4096", 23, 4096, 4096, [1], 14)
     # q, k (Q4_K), v (Q6_K), o, gate, up (Q4_K), down (Q6_K)
     layer = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096), (12, 4096, 4096),
              (12, 14336, 4096), (12, 14336, 4096), (14, 4096, 14336)]

@@ -6,11 +6,11 @@ dequantizing with torch ops and calling `F.linear`.
   constructor, attributes (`out_features`, `in_features`, non-persistent `packed` buffer,
   `bias`) and `forward(x: (..., K)) -> (..., N)` in `dtype`, as the reference's
   (device_packed.py:22-63). The weight is never dequantized: one fused quantized matmul per call.
-* `DevicePackedEmbedding(packed, embedding_dim, ggml_type, dtype)`: a lookup dequantizes only
-  the rows it needs (device_packed.py:66-84); `as_linear` is the tied lm_head over the same
-  bytes (device_packed.py:86-89).
-* `upload_packed(raw, n_rows, device)`: (n_rows, row_bytes) uint8 device copy of packed bytes
-  (device_packed.py:14-19).
+* `DevicePackedEmbedding(packed, embedding_dim, ggml_type, dtype)`: lookups expand only the
+  requested rows (device_packed.py:66-84); `as_linear` shares the bytes with the tied output
+  projection (device_packed.py:86-89).
+* `upload_packed(raw, n_rows, device)`: packed bytes copied into a new device tensor of
+  n_rows rows (device_packed.py:14-19).
 * `HipDequantizer`: the `TorchDequantizer` interface (torch_dequant.py:221-236) on the kernels.
 
 A float32 input that a fused producer (`matricxon_amd.fused_ops.HipFusedOps`) just wrote comes
@@ -64,7 +64,8 @@ def _host_nbytes(raw) -> int | None:
 
 
 def upload_packed(raw, n_rows: int, device: torch.device) -> torch.Tensor:
-    """`(n_rows, row_bytes)` uint8 copy of packed bytes on `device` (never aliases `raw`).
+    """A fresh device tensor of shape (n_rows, row_bytes), dtype uint8, holding the packed bytes of
+    `raw`; `raw` itself is never referenced afterwards.
     Host sources of 16 MiB or more go to a GPU through the pinned, overlapped staging of
     `matricxon_amd.loading.PackedUploader`."""
     device = torch.device(device)
@@ -184,8 +185,9 @@ class DevicePackedLinear(nn.Module):
 
 
 class DevicePackedEmbedding(nn.Module):
-    """Packed token-embedding table on the device: a lookup dequantizes only the rows it needs.
-    `as_linear` is the tied lm_head over the same bytes (no second copy)."""
+    """Token embeddings kept as packed GGUF rows in device memory. `forward` expands just the
+    looked-up ids (one `mxa_dequant_rows` launch); `as_linear` reuses the same bytes as the tied
+    output projection."""
 
     def __init__(
         self, packed: torch.Tensor, embedding_dim: int, ggml_type: int, dtype: torch.dtype

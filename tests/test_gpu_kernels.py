@@ -173,6 +173,25 @@ def test_decode_rows_equal_prefill_rows(gpu, ggml_type) -> None:
         assert np.array_equal(bits(alone[0]), bits(batch[t]))
 
 
+@pytest.mark.parametrize("m", [17, 64, 512])
+def test_iq4_xs_prefill_rows_near_decode_rows(gpu, m) -> None:
+    """The one relaxation of tests/unit/test_native_gemm.py:177-189: IQ4_XS batches of 17 rows or
+    more run on bf16 matrix cores with x split into hi + lo parts, which sums in another order
+    than the decode kernels (and drops x's bits below hi + lo, under 2^-16 of |x|). Each such row
+    must stay within the north-star bound of the same token decoded alone: rel-L2 <= 1e-4 and
+    max|diff| <= 2e-3 * max|decode row|. Up to 16 rows the equality is bit for bit (above)."""
+    n, k = 96, 4096
+    w = dev(S.packed_weight(D.IQ4_XS, n, k, seed=78))
+    x = S.activations(m, k, seed=500 + m)
+    batch = host(gpu.matmul(D.IQ4_XS, w, dev(x), n, k))
+    worst = 0.0
+    for t in range(m):
+        alone = host(gpu.matmul(D.IQ4_XS, w, dev(x[t : t + 1]), n, k))[0]
+        assert_within_tolerance(batch[t], alone)
+        worst = max(worst, float(np.linalg.norm(batch[t] - alone) / np.linalg.norm(alone)))
+    print(f"IQ4_XS M={m}: worst row rel-L2 prefill vs decode {worst:.2e}")
+
+
 def test_gemm_multi_equals_separate_calls(gpu) -> None:
     k = 1024
     items = [(D.Q4_K, 64), (D.Q4_K, 16), (D.Q6_K, 16)]
