@@ -260,6 +260,25 @@ int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, float* y, 
 // only as fast as the queue drains, so a wave that tried to issue everything up front would sit
 // in the issue queue instead of computing. After its last stage one lane per (row, activation
 // row) folds the row's nb block values in order.
+//
+// LONG: a wave whose range has more blocks than the value ring (kVRing) folds, after each stage,
+// every row that stage completed, keeps its outputs in LDS until the end, and may run with a
+// single stage buffer (P == 0: the next stage is requested as soon as this one is computed).
+// Its LDS then no longer grows with the rows per wave, so 8 weight waves fit where the block
+// values of all rows did not (the Q6_K vocabulary head: 3 waves per CU before, each SIMD with a
+// single wave issuing ~470 VALU per 64-block stage at a fraction of its rate). The short form
+// keeps its own instantiation: folding inside its loop measured slower (10.3 vs 9.1 us).
+
+// Block values of a LONG weight wave wait in a ring of this many slots per activation row until
+// their row is complete (a row has at most 64 blocks, so 64 + nb - 1 slots are enough).
+constexpr int kVRing = 128;
+// LDS of a weight wave beside its stage buffers: its block values and D (all of them, or the ring
+// and the folded outputs of its R rows when LONG); a multiple of 16 so that every wave's buffers
+// stay 16-byte aligned.
+template <int MAXM>
+__host__ __device__ constexpr int wave_value_bytes(bool long_form, int R, int nb) {
+  return long_form ? (kVRing * 4 * (MAXM + 1) + R * MAXM * 4 + 15) & ~15 : R * nb * 4 * (MAXM + 1);
+}
 
 struct PipeGeo {
   int rows_per_wave;  // R
@@ -376,7 +395,7 @@ __device__ __forceinline__ void stage_activations(const Act& act, int M, int aw,
 // so the lane keeps that block's Q8_K values in registers instead of reading LDS per stage.
 // One workgroup's share of a pipelined decode: rows of workgroup tile `tile` (R rows per weight
 // wave) of one packed weight.
-template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG>
+template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG, bool LONG = false>
 __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
                                           const Act& act, float* __restrict__ y, long long ldy,
                                           int M, int N, const PipeGeo& geo, int tile) {
@@ -400,13 +419,15 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
   }
 
   const int R = geo.rows_per_wave, P = geo.ahead, ww = wave - na;
-  const int vslots = R * nb;
+  // block values: all R * nb of them, or (LONG) block j at ring slot j % kVRing
+  const int vslots = LONG ? kVRing : R * nb;
   const int buf_bytes = geo.buf_kb * 1024;
-  const int nbuf = min(P + 1, (vslots + 63) >> 6);  // P >= the stage count: no buffer is reused
-  const int wave_bytes = nbuf * buf_bytes + vslots * 4 * (MAXM + 1);
+  const int nbuf = max(1, min(P + 1, (R * nb + 63) >> 6));  // P >= the stage count: no reuse
+  const int wave_bytes = nbuf * buf_bytes + wave_value_bytes<MAXM>(LONG, R, nb);
   uint8_t* wreg = region + ww * wave_bytes;
   float* Vbuf = (float*)(wreg + nbuf * buf_bytes);  // [MAXM][vslots]
   float* Dbuf = Vbuf + MAXM * vslots;                   // [vslots]
+  float* Ybuf = Dbuf + vslots;                          // LONG: [MAXM][R] folded outputs
 
   const int n0 = (tile * geo.weight_waves + ww) * R;
   const int nrows = max(0, min(R, N - n0));
@@ -430,7 +451,7 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
   };
 
   __builtin_amdgcn_s_barrier();  // first barrier: the activation loads are queued
-  for (int s = 0; s < min(P, stages); ++s) issue(s);
+  for (int s = 0; s < min(max(P, 1), stages); ++s) issue(s);
   __builtin_amdgcn_s_barrier();  // second barrier: the activations are in LDS
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
@@ -447,12 +468,45 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
     areg.bs[0] = *(const u32x4a4*)(act_bs + 16 * b);
     areg.bs[1] = *(const u32x4a4*)(act_bs + 16 * b + 8);
   }
+  // LONG fold: rows folded .. upto - 1, whose blocks are all computed; pair f -> activation row
+  // f / cnt, row folded + f % cnt; blocks in order; outputs to Ybuf (a store here would count on
+  // vmcnt and hold up the next stage's wait)
+  int folded = 0;
+  auto fold_rows = [&](int upto) {
+    const int cnt = upto - folded;
+    for (int f = lane; f < cnt * M; f += 64) {
+      const int fm = f / cnt, fr = folded + (f - fm * cnt);
+      const float* v = Vbuf + fm * kVRing;
+      const float* xd = act_d + fm * nb;
+      const int base = fr * nb;  // the row's first block in the range
+      float acc = 0.0f;
+      int bb = 0;
+      for (; bb + 16 <= nb; bb += 16) {
+        float vv[16], xx[16], ww[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int slot = (base + bb + i) & (kVRing - 1);
+          vv[i] = v[slot];
+          xx[i] = kFloatAct ? 0.0f : xd[bb + i];
+          ww[i] = L::kHasD ? Dbuf[slot] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = L::fold(acc, xx[i], vv[i], ww[i]);
+      }
+      for (; bb < nb; ++bb) {
+        const int slot = (base + bb) & (kVRing - 1);
+        acc = L::fold(acc, kFloatAct ? 0.0f : xd[bb], v[slot], L::kHasD ? Dbuf[slot] : 0.0f);
+      }
+      Ybuf[fm * R + fr] = acc;
+    }
+    folded = upto;
+  };
   for (int s = 0; s < stages; ++s) {
     // copies issued after stage s: stages s + 1 .. min(s + P - 1, stages - 1)
     int after = 0;
     for (int k = s + 1; k <= min(s + P - 1, stages - 1); ++k) after += stage_copies<L::kBytes>(k, nblk, mis);
     wait_vmcnt(after);
-    if (s + P < stages) issue(s + P);
+    if (P > 0 && s + P < stages) issue(s + P);
     int jl = lane, boff = lane_off, bb = b;
     if (64 * s + 64 > nblk) {  // partial last stage
       jl = min(lane, nblk - 1 - 64 * s);
@@ -476,15 +530,33 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
       L::template compute<MAXM, ActBlock>(wreg + (s % nbuf) * buf_bytes, boff, ablk, M, V, D);
     b += step;
     b = b >= nb ? b - nb : b;
-    const int j = 64 * s + jl;
+    if constexpr (LONG) {
+      // one buffer: its bytes have all been read (the compute used them), so the next stage can
+      // be requested into it before this stage's rows are folded
+      if (P == 0 && s + 1 < stages) issue(s + 1);
+    }
+    const int j = LONG ? (64 * s + jl) & (kVRing - 1) : 64 * s + jl;
     if (jl == lane) {
 #pragma unroll
       for (int m = 0; m < MAXM; ++m)
         if (m < M) Vbuf[m * vslots + j] = V[m];
       if (L::kHasD) Dbuf[j] = D;
     }
+    if constexpr (LONG) {
+      // rows complete after this stage are folded now, while the next stage is in flight: a row
+      // still open spans at most nb - 1 earlier slots, and the next stage writes 64 later ones
+      __builtin_amdgcn_wave_barrier();
+      fold_rows(min(64 * (s + 1), nblk) / nb);
+    }
   }
   __builtin_amdgcn_wave_barrier();
+  if constexpr (LONG) {
+    for (int f = lane; f < nrows * M; f += 64) {  // consecutive lanes, consecutive rows
+      const int fm = f / nrows, fr = f - fm * nrows;
+      y[(size_t)fm * ldy + n0 + fr] = Ybuf[fm * R + fr];
+    }
+    return;
+  }
   // fold: pair f -> row f % nrows, activation row f / nrows; blocks in order
   for (int f = lane; f < nrows * M; f += 64) {
     const int fm = f / nrows, fr = f - fm * nrows;
@@ -529,7 +601,7 @@ inline bool pipe_pack(const PipeGeo& g, int nb, int grid, PipePack& p) {
   return true;
 }
 
-template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG>
+template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG, bool LONG>
 __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, const float* x,
                                                          float* __restrict__ y, int row_bytes,
                                                          int N, int M, int ldy, uint32_t pack_a,
@@ -546,8 +618,8 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, const 
   Act act;
   act.q = q, act.d = d, act.bsums = bsums, act.x = x;
   act.k = nb * QK, act.nb = nb, act.xsplit = nullptr;
-  pipe_rows<TYPE, MAXM, FUSEQ, ACTREG>(smem, w, row_bytes, act, y, ldy, M, N, geo,
-                                       xcd_tile(blockIdx.x, grid));
+  pipe_rows<TYPE, MAXM, FUSEQ, ACTREG, LONG>(smem, w, row_bytes, act, y, ldy, M, N, geo,
+                                             xcd_tile(blockIdx.x, grid));
 }
 
 // Several packed weights that share the activations (e.g. q, k and v) in one launch: workgroups
@@ -608,8 +680,9 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   PipeGeo geo;
   geo.act_waves = na;
   geo.buf_kb = kBufKb;
-  auto wave_bytes = [&](int P, int R) {
-    return min(P + 1, (R * nb + 63) / 64) * kBufKb * 1024 + R * nb * 4 * (MAXM + 1);
+  auto wave_bytes = [&](int P, int R, bool long_form) {
+    return max(1, min(P + 1, (R * nb + 63) / 64)) * kBufKb * 1024 +
+           wave_value_bytes<MAXM>(long_form, R, nb);
   };
   // First choice: one workgroup per CU whose waves stream all their rows (every row requested in
   // one round). When the rows' block values do not fit beside the buffers: two workgroups per CU
@@ -617,29 +690,41 @@ int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y,
   // in flight per wave and as many waves as fit (up to 8, two per SIMD) measured fastest on
   // MI355X: more copies in flight only lengthen the queue at HBM.
   int P = 0, nw = 0, R = 0;
-  bool ok = false;
+  bool ok = false, persistent = false, long_form = false;
   for (int mode = 0; mode < 4 && !ok; ++mode) {
-    const bool persistent = mode < 2;
+    persistent = mode < 2;
     P = mode % 2 == 0 ? 1 : 2;
     const int budget = (persistent ? kLdsMax : kLdsMax / 2) - act_lds;
     for (nw = 8; nw >= 2 && !ok; --nw) {  // nw + na <= 12 waves: the kernel's launch bound
       R = persistent ? (int)((N + (long long)ncu * nw - 1) / ((long long)ncu * nw)) : max(1, 512 / nb);
-      ok = nw * wave_bytes(P, R) <= budget;
+      ok = nw * wave_bytes(P, R, false) <= budget;
       if (ok) break;
+    }
+  }
+  // Fewer than 8 persistent weight waves: the LONG form with one stage buffer per wave fits 8
+  // (two per SIMD) when each wave's range outgrows the value ring.
+  if (ok && persistent && nw < 8) {
+    const int R8 = (int)((N + (long long)ncu * 8 - 1) / ((long long)ncu * 8));
+    if (R8 * nb > kVRing && 8 * wave_bytes(0, R8, true) <= kLdsMax - act_lds) {
+      P = 0;
+      nw = 8;
+      R = R8;
+      long_form = true;
     }
   }
   if (!ok || kBufKb * P > kMaxCopies) return -1;
   geo.ahead = P;
   geo.weight_waves = nw;
   geo.rows_per_wave = R;
-  const int lds = act_lds + nw * wave_bytes(P, R);
+  const int lds = act_lds + nw * wave_bytes(P, R, long_form);
   if (lds > kLdsMax) return -1;
   const int grid = (int)((N + (long long)nw * R - 1) / ((long long)nw * R));
   constexpr bool kRegOk = MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0);
   const bool actreg = kRegOk && 64 % nb == 0;
-  auto kern = actreg ? gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk> : gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>;
-  allow_lds((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk>, kLdsMax);
-  allow_lds((const void*)gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false>, kLdsMax);
+  auto kern = long_form ? gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false, true>
+              : actreg  ? gemv_pipe_kernel<TYPE, MAXM, FUSEQ, kRegOk, false>
+                        : gemv_pipe_kernel<TYPE, MAXM, FUSEQ, false, false>;
+  allow_lds((const void*)kern, kLdsMax);
   PipePack pk;
   if (!pipe_pack(geo, nb, grid, pk) || ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF) return -1;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (nw + na)), lds, stream, w, act.x, y,

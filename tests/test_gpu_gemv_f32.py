@@ -62,6 +62,19 @@ def test_gemv_f32_matches_float64_product(gpu, t, n, k, m) -> None:
 
 
 @pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("m", [1, 3])
+def test_gemv_f32_long_ranges(gpu, t, m) -> None:
+    # 30000 rows of 9 blocks: each weight wave's range wraps the block-value ring (rows folded as
+    # stages complete); checked on a spread of rows
+    n, k = 30000, 2304
+    w = S.packed_weight(t, n, k, seed=7600 + t)
+    x = S.activations(m, k, seed=7601 + m)
+    y = host(gpu.gemv_f32(t, dev(w), dev(x), n, k))
+    rows = np.unique(np.concatenate([np.arange(300), np.arange(n - 300, n), np.arange(0, n, 61)]))
+    assert_f32_accurate(y[:, rows], product64(t, w[rows], x, len(rows), k))
+
+
+@pytest.mark.parametrize("t", TYPES)
 def test_gemv_f32_one_hot_picks_dequantized_columns(gpu, t) -> None:
     # one-hot rows pick out single weight columns: a wrong element, nibble or sub-block mapping
     # lands on another column's value. The kernel takes d * sc * q - dmin * m with one rounding

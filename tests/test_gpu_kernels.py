@@ -331,6 +331,21 @@ def test_batched_decode_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m)
     check_gemm(gpu, oracle, ggml_type, w, x, n, k)
 
 
+# Decode ranges longer than the block-value ring (over 128 blocks per weight wave at 8 waves per
+# CU): the form that folds rows as stages complete, with one stage buffer per wave. Block counts
+# that do not divide 64 (K = 2304: 9 blocks, 768: 3) put rows across stage and ring boundaries.
+LONG_SHAPES = [(30000, 2304, 1), (30000, 2304, 3), (20000, 4096, 2), (90000, 768, 1),
+               (17000, 4096, 4)]
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("n,k,m", LONG_SHAPES)
+def test_long_range_decode_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> None:
+    w = S.packed_weight(ggml_type, n, k, seed=n + k * 7 + m)
+    x = S.activations(m, k, seed=m * 17 + k)
+    check_gemm(gpu, oracle, ggml_type, w, x, n, k)
+
+
 # Prefill: 64-row activation tiles of 128 weight rows: N below, at and past whole 128-row tiles, M
 # at and past whole 64-row tiles (rows past M repeat row M - 1), odd and long block counts
 # (K = 2304: 9 blocks, 14336: 56).
