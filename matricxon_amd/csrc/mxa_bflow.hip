@@ -147,9 +147,9 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
         if (i < cp.mine) {
           const uint32_t dst = lds0 + (uint32_t)(tb * t + 1024 * (cw + NC * i));
           if (whole) {
-            if (cp.row[i] < 16) copy16_to_lds_s(base, cp.off[i], dst);
+            if (cp.row[i] < 16) copy16_to_lds_s_nt(base, cp.off[i], dst);
           } else if (cp.row[i] < min(live, 16)) {
-            copy16_to_lds((const void*)min((uintptr_t)(base + cp.off[i]), (uintptr_t)last), dst);
+            copy16_to_lds_nt((const void*)min((uintptr_t)(base + cp.off[i]), (uintptr_t)last), dst);
           }
         }
       }
@@ -261,11 +261,25 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
   }
 }
 
+// The arguments in the order the waves first need them, the geometry packed into two dwords, so
+// that what the first requests need arrives preloaded in SGPRs (structures never do):
+// pack_a = rows_per_wg | ncw << 12 | M << 16 | nb << 21, pack_b = rs | ctrl_off << 12.
 template <int TYPE, int C>
-__global__ __launch_bounds__(1024) void bflow_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                     float* __restrict__ y, long long ldy, int M,
-                                                     int N, BfGeo geo) {
+__global__ __launch_bounds__(1024) void bflow_kernel(const uint8_t* w, uint32_t pack_a,
+                                                     uint32_t pack_b, int N, int row_bytes,
+                                                     const int8_t* q, const int16_t* bsums,
+                                                     const float* d, float* __restrict__ y,
+                                                     int ldy) {
   extern __shared__ __align__(16) uint8_t smem[];
+  BfGeo geo;
+  geo.rows_per_wg = pack_a & 0xFFF;
+  geo.ncw = (pack_a >> 12) & 0xF;
+  geo.rs = pack_b & 0xFFF;
+  geo.ctrl_off = pack_b >> 12;
+  const int M = (pack_a >> 16) & 0x1F, nb = pack_a >> 21;
+  Act act;
+  act.q = q, act.d = d, act.bsums = bsums, act.x = nullptr;
+  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr;
   bflow_rows<TYPE, C>(smem, w, row_bytes, act, y, ldy, M, N, geo, blockIdx.x);
 }
 
@@ -291,10 +305,15 @@ int launch_bf(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
   geo.ctrl_off = T * 16 * geo.rs * 16;
   const int lds = geo.ctrl_off + nb * 16 * 4 + (kBfCopyWaves + kBfMaxTiles) * 4;
   if (lds > kBfLds) return -1;
+  if (R > 0xFFF || geo.rs > 0xFFF || geo.ctrl_off > 0xFFFFF || nb > 0x7FF || row_bytes > 0x7FFFFFFF ||
+      ldy > 0x7FFFFFFF)
+    return -1;
+  const uint32_t pack_a = (uint32_t)R | (uint32_t)geo.ncw << 12 | (uint32_t)M << 16 | (uint32_t)nb << 21;
+  const uint32_t pack_b = (uint32_t)geo.rs | (uint32_t)geo.ctrl_off << 12;
   allow_lds((const void*)bflow_kernel<TYPE, C>, kBfLds);
   const int grid = (int)((N + (long long)R - 1) / R);
   hipLaunchKernelGGL((bflow_kernel<TYPE, C>), dim3(grid), dim3(64 * (geo.ncw + kBfCopyWaves)), lds,
-                     stream, w, row_bytes, act, y, ldy, M, N, geo);
+                     stream, w, pack_a, pack_b, N, (int)row_bytes, act.q, act.bsums, act.d, y, (int)ldy);
   return 0;
 }
 

@@ -191,6 +191,9 @@ __device__ __forceinline__ void copy16_to_lds_nt(const void* g, uint32_t lds_add
 __device__ __forceinline__ void copy16_to_lds_s(const void* base, uint32_t off, uint32_t lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
+__device__ __forceinline__ void copy16_to_lds_s_nt(const void* base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
+}
 
 // Grid-order tile index for workgroup `wg` of `n_wg` such that consecutive tiles land on the same
 // XCD: workgroups are dealt to the 8 XCDs round-robin, so XCD x gets a contiguous tile range.
