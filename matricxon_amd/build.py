@@ -48,18 +48,45 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+def _jobs() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("MAX_JOBS", "16")), 16))
+
+
 def build(verbose: bool = False) -> Path:
-    """Compiles every csrc/*.hip into LIB_PATH; raises RuntimeError with the compiler output on
-    failure."""
+    """Compiles every csrc/*.hip into LIB_PATH: one object per source, compiled in parallel into
+    _build/, then one link. Raises RuntimeError with the compiler output on failure."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    obj_dir = PKG_DIR.parent / "_build" / "csrc"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src: Path) -> tuple[Path, subprocess.CompletedProcess]:
+        obj = obj_dir / (src.stem + ".o")
+        cmd = [hipcc(), *compile_flags, "-c", "-o", str(obj), str(src)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        return obj, subprocess.run(cmd, capture_output=True, text=True)
+
+    with ThreadPoolExecutor(_jobs()) as pool:
+        results = list(pool.map(compile_one, sources()))
+    errors = [r.stderr for _, r in results if r.returncode != 0]
+    if errors:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(e[-8000:] for e in errors))
     fd, tmp = tempfile.mkstemp(dir=PKG_DIR, suffix=".so.tmp")
     os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *map(str, sources())]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
+           *(str(o) for o, _ in results)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         Path(tmp).unlink(missing_ok=True)
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
+        raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{res.stderr[-8000:]}")
     os.chmod(tmp, 0o755)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH

@@ -833,7 +833,13 @@ int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long lo
 int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (m_rows < 1 || m_rows > 4) return -1;
-  if (m_rows == 1 && launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
+  if (m_rows == 1) {
+    // one activation row: the floor-shaped kernel wherever it applies (measured faster at every
+    // size on MI355X: Q4_K 4096 x 4096 3.8 vs 5.3 us, 14336 x 4096 7.4 vs 8.6 us), else the
+    // workgroup-resident kernel for weights up to 12 MB
+    if (launch_gemv_wave(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
+    if (launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
+  }
   switch (type) {
     case T_Q4_K: return launch_lpb_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q6_K: return launch_lpb_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);

@@ -1,0 +1,302 @@
+// Decode GEMV for one activation row in the shape of the read floor: one workgroup per CU whose
+// waves request every byte of their rows at their first instructions, then compute each row set
+// as it lands. y[n] = sum_k x[k] * W[n, k] for K-quant / Q8_0 weights with nb = K / 256 in
+// {4, 8, 16, 32, 64}.
+//
+// Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, one byte range,
+// 16-byte aligned because row_bytes is) and issues all of its range's 1 KB copies
+// (global_load_lds_dwordx4, fully coalesced) into its own LDS stage before anything waits. The CU
+// takes them in as its memory pipeline drains (it accepts ~64 KB in flight, so half the waves sit
+// in their issue loop for microseconds); the whole matrix is in flight from the start and lands
+// in the order HBM returns it. A wave waits only for its own copies (vmcnt), never for another
+// wave's.
+//
+// Activations. The first waves (stagers) also bring the activations into LDS with LDS-DMA copies
+// issued before their weight copies: fp32 x, which they then quantize to Q8_K (16 lanes per
+// 256-value block, the arithmetic of quantize_q8k_kernel), or the caller's Q8_K blocks, gathered
+// per lane straight into place. Being copies, not loads, these are waited for with the stager's
+// own vmcnt (a compiler-tracked load would make it wait for every weight copy issued after it).
+// The stagers publish through an LDS counter, not a barrier, so a wave still issuing copies holds
+// up no other. The q8 values sit in LDS as [16-byte piece i][block b]: the 64 lanes of a wave
+// reading piece i of blocks lane % nb touch consecutive 16-byte words.
+//
+// Compute. Lane l computes block l of its wave's range whole (row l / nb, block l % nb), with the
+// lane-per-block arithmetic of the pipelined decode kernel (mxa_lpb.hpp), Q4_K and Q8_0 with the
+// lane's activation block in registers; one lane per row folds the row's block values in order
+// with the CPU oracle's fused steps, so results equal it bit for bit
+// (app/native/src/mx_dot_k_ssse3.c:115-209, mx_dot_q8_0.c:5-22). nb is a template parameter: as
+// a run-time value it costs the compute section ~1.7x the instructions (measured 8.0 vs 7.3 us).
+#include "mxa_kernels.hpp"
+#include "mxa_lpb.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mxa {
+namespace {
+
+constexpr int kWaveMaxWaves = 16;
+constexpr int kWaveLds = 160 * 1024;
+
+template <int TYPE>
+constexpr int wave_stage_bytes() {  // a wave's 64 blocks, in whole 1 KB copies
+  return (64 * Lpb<TYPE>::kBytes + 1023) / 1024 * 1024;
+}
+// LDS of one wave: stage, block values V and (Q6_K) block scales D
+template <int TYPE>
+constexpr int wave_region_bytes() {
+  return wave_stage_bytes<TYPE>() + 64 * 4 * (Lpb<TYPE>::kHasD ? 2 : 1);
+}
+// Activation area: q8 pieces (nb * 256 bytes), bsums and d each in whole 1 KB copy windows (a
+// gathering copy writes 1 KB), the counter, then (fp32 x) nb KB of staged x.
+__host__ __device__ constexpr int wave_bs_off(int nb) { return nb * QK; }
+__host__ __device__ constexpr int wave_d_off(int nb) { return nb * QK + (nb * 32 + 1023) / 1024 * 1024; }
+__host__ __device__ constexpr int wave_flag_off(int nb) { return wave_d_off(nb) + 1024; }
+__host__ __device__ constexpr int wave_x_off(int nb) { return wave_flag_off(nb) + 16; }
+__host__ __device__ constexpr int wave_act_bytes(int nb, bool fuseq) {
+  return wave_x_off(nb) + (fuseq ? nb * 1024 : 0);
+}
+
+// Q8_K activations staged as [piece i][block b][16 bytes]: the accessor of block b.
+struct ActPieces {
+  const int8_t* q;  // piece 0 of the block
+  int stride;       // bytes between pieces (16 nb)
+  const int16_t* bsums;
+  __device__ i32x4a4 q16(int off) const { return *(const i32x4a4*)(q + (off >> 4) * stride); }
+  __device__ u32x4a4 bs8(int h) const { return *(const u32x4a4*)(bsums + 8 * h); }
+  __device__ uint32_t bs2(int j) const { return *(const uint32_t*)(bsums + 2 * j); }
+  __device__ float4 x4(int) const { return float4{0.0f, 0.0f, 0.0f, 0.0f}; }
+};
+
+typedef __attribute__((address_space(3))) int lds_int;
+
+// A wait that gives up after this many polls (the counter always reaches its target: each stager
+// counts once after a bounded amount of work); a wave that gives up writes NaN.
+constexpr int kWaveSpinLimit = 1 << 22;
+
+// pack: waves | stagers << 8: the first `waves` waves of the workgroup own rows, the first
+// `stagers` also stage the activations (the workgroup has max(waves, stagers) waves; one that
+// owns no rows only stages)
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG>
+__global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int N,
+    int row_bytes, uint32_t pack, const int8_t* __restrict__ aq, const float* __restrict__ ad,
+    const int16_t* __restrict__ abs_) {
+  using L = Lpb<TYPE>;
+  constexpr int kStage = wave_stage_bytes<TYPE>(), kCopies = kStage / 1024;
+  constexpr int R = 64 / NB, kRounds = NB / 4;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int waves = pack & 0xFF, nq = pack >> 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint8_t* act_q = smem;                                 // [16][NB][16]
+  int16_t* act_bs = (int16_t*)(smem + wave_bs_off(NB));  // [NB][16]
+  float* act_d = (float*)(smem + wave_d_off(NB));        // [NB]
+  lds_int* flag = (lds_int*)(lds_u8*)(smem + wave_flag_off(NB));
+  float* xs = (float*)(smem + wave_x_off(NB));           // fp32 x: [NB][256]
+  uint8_t* wreg = smem + wave_act_bytes(NB, FUSEQ) + wave * wave_region_bytes<TYPE>();
+  float* Vbuf = (float*)(wreg + kStage);
+  float* Dbuf = Vbuf + 64;
+
+  if (tid == 0) *flag = 0;
+  __syncthreads();  // nothing is outstanding yet: the barrier waits for no memory
+
+  // stager copies, ahead of this wave's weight copies: fp32 x one 1 KB block per copy (rounds of
+  // four blocks: wave, wave + nq, ..), or the Q8_K parts gathered into place (copy j by stager
+  // j % nq)
+  const bool stager = wave < nq;
+  if (stager) {
+    if constexpr (FUSEQ) {
+      for (int r = wave; r < kRounds; r += nq)
+        for (int g = 4 * r; g < 4 * r + 4; ++g)
+          copy16_to_lds((const void*)(x + g * QK + 4 * lane), lds_addr(xs + g * QK));
+    } else {
+      constexpr int kQ = NB / 4, kBs = (NB * 2 + 63) / 64;  // copies of q8 pieces and of bsums
+      for (int j = wave; j < kQ + kBs + 1; j += nq) {
+        const void* src;
+        uint32_t dst;
+        if (j < kQ) {  // slot s = 64 j + lane: piece s / NB of block s % NB
+          const int s = 64 * j + lane;
+          src = aq + (s % NB) * QK + 16 * (s / NB);
+          dst = lds_addr(act_q + 1024 * j);
+        } else if (j < kQ + kBs) {  // eight bsums per slot; slots past the last repeat it
+          const int s = min(64 * (j - kQ) + lane, 2 * NB - 1);
+          src = abs_ + 8 * s;
+          dst = lds_addr((uint8_t*)act_bs + 1024 * (j - kQ));
+        } else {  // four scales per slot; slots past the last repeat it
+          src = ad + 4 * min(lane, NB / 4 - 1);
+          dst = lds_addr(act_d);
+        }
+        copy16_to_lds(src, dst);
+      }
+    }
+  }
+
+  // every copy of the wave's range (the last ones may pass it: they read the next wave's rows,
+  // or stop at the matrix's last 16-byte word, and land in this wave's stage)
+  const bool has_rows = wave < waves;
+  const int n0 = (xcd_tile(blockIdx.x, gridDim.x) * waves + wave) * R;
+  const int nrows = has_rows ? max(0, min(R, N - n0)) : 0;
+  const uint8_t* src = w + (size_t)min(n0, N - 1) * row_bytes;
+  const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
+  const uint32_t lds_w = lds_addr(wreg);
+  if (has_rows) {
+#pragma unroll
+    for (int c = 0; c < kCopies; ++c)
+      copy16_to_lds_nt((const void*)min((uintptr_t)src + (uintptr_t)c * 1024 + (uintptr_t)lane * 16, last),
+                       lds_w + c * 1024);
+  }
+
+  if (stager) {
+    wait_vmcnt(has_rows ? kCopies : 0);  // the activation copies, issued first, have landed
+    if constexpr (FUSEQ) {
+      const int p = lane & 15;
+      for (int r = wave; r < kRounds; r += nq) {
+        const int g = 4 * r + (lane >> 4);
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 f = *(const float4*)(xs + g * QK + 16 * p + 4 * q);
+          v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+        }
+        // the steps of q8k_part16, piece p of block g going to 16 (p NB + g)
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = max16(amax);
+        int qv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qv[i] = 0;
+        if (amax != 0.0f) {
+          const float iscale = 127.0f / amax;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) qv[i] = (int)fminf(fmaxf(rintf(v[i] * iscale), -127.0f), 127.0f);
+        }
+        uint32_t packed[4];
+        int bsum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          packed[i] = (uint32_t)(qv[4 * i] & 0xFF) | ((uint32_t)(qv[4 * i + 1] & 0xFF) << 8) |
+                      ((uint32_t)(qv[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * i + 3] & 0xFF) << 24);
+          bsum += qv[4 * i] + qv[4 * i + 1] + qv[4 * i + 2] + qv[4 * i + 3];
+        }
+        *(uint4*)(act_q + (p * NB + g) * 16) = uint4{packed[0], packed[1], packed[2], packed[3]};
+        act_bs[g * 16 + p] = (int16_t)bsum;
+        if (p == 0) act_d[g] = amax / 127.0f;
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) __hip_atomic_fetch_add(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+
+  if (!has_rows) return;
+  int spin = 0;
+  while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nq &&
+         ++spin < kWaveSpinLimit)
+    __builtin_amdgcn_s_sleep(1);
+  const bool gave_up = spin >= kWaveSpinLimit;
+
+  const int b = lane % NB;
+  const int jl = min(lane, max(nrows, 1) * NB - 1);  // lanes past the range redo its last block
+  ActPieces ap;
+  ap.q = (const int8_t*)(act_q + b * 16);
+  ap.stride = NB * 16;
+  ap.bsums = act_bs + b * 16;
+  ActRegs areg;
+  if constexpr (ACTREG) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) areg.q[i] = ap.q16(16 * i);
+    areg.bs[0] = ap.bs8(0);
+    areg.bs[1] = ap.bs8(1);
+  }
+  wait_vmcnt(0);
+  float V[1], D;
+  if constexpr (ACTREG)
+    L::template compute<1, ActRegs>(wreg, jl * L::kBytes, &areg, 1, V, D);
+  else
+    L::template compute<1, ActPieces>(wreg, jl * L::kBytes, &ap, 1, V, D);
+  Vbuf[lane] = V[0];
+  if (L::kHasD) Dbuf[lane] = D;
+  __builtin_amdgcn_wave_barrier();
+  if (lane < nrows) {
+    constexpr int kC = NB < 16 ? NB : 16;  // blocks whose operands are read before they are folded
+    float acc = 0.0f;
+#pragma unroll
+    for (int bb = 0; bb < NB; bb += kC) {
+      float vv[kC], xx[kC], dd[kC];
+#pragma unroll
+      for (int i = 0; i < kC; ++i) {
+        vv[i] = Vbuf[lane * NB + bb + i];
+        xx[i] = act_d[bb + i];
+        dd[i] = L::kHasD ? Dbuf[lane * NB + bb + i] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kC; ++i) acc = L::fold(acc, xx[i], vv[i], dd[i]);
+    }
+    y[n0 + lane] = gave_up ? __builtin_nanf("") : acc;
+  }
+}
+
+template <int TYPE, int NB, bool FUSEQ>
+int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
+                  hipStream_t stream) {
+  constexpr bool kReg = TYPE != T_Q6_K;  // Q6_K's compute leaves no room for them
+  constexpr int R = 64 / NB;
+  const int ncu = cu_count();
+  const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
+  const int fit = (kWaveLds - wave_act_bytes(NB, FUSEQ)) / wave_region_bytes<TYPE>();
+  const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
+  if (waves < 1 || (long long)waves * R * ncu < N) return -1;  // more rows than one round holds
+  const int grid = (N + waves * R - 1) / (waves * R);
+  // stagers: a round of four blocks each, in waves of their own when the workgroup has fewer
+  // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)
+  const int nq = min(kWaveMaxWaves, NB / 4);
+  const int nw = max(waves, nq);
+  const int lds = wave_act_bytes(NB, FUSEQ) + waves * wave_region_bytes<TYPE>();  // row waves only
+  auto kern = gemv_wave_kernel<TYPE, NB, FUSEQ, kReg>;
+  allow_lds((const void*)kern, kWaveLds);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N,
+                     (int)row_bytes, (uint32_t)waves | (uint32_t)nq << 8, act.q, act.d, act.bsums);
+  return 0;
+}
+
+template <int TYPE, int NB>
+int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
+                   hipStream_t stream) {
+  return act.q == nullptr ? launch_wave_t<TYPE, NB, true>(w, row_bytes, act, y, N, stream)
+                          : launch_wave_t<TYPE, NB, false>(w, row_bytes, act, y, N, stream);
+}
+
+template <int TYPE>
+int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
+                     hipStream_t stream) {
+  switch (act.nb) {
+    case 4: return launch_wave_nb<TYPE, 4>(w, row_bytes, act, y, N, stream);
+    case 8: return launch_wave_nb<TYPE, 8>(w, row_bytes, act, y, N, stream);
+    case 16: return launch_wave_nb<TYPE, 16>(w, row_bytes, act, y, N, stream);
+    case 32: return launch_wave_nb<TYPE, 32>(w, row_bytes, act, y, N, stream);
+    case 64: return launch_wave_nb<TYPE, 64>(w, row_bytes, act, y, N, stream);
+    default: return -1;
+  }
+}
+
+}  // namespace
+
+int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                     int n_rows, hipStream_t stream) {
+  if (n_rows < 1) return -1;
+  if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF) return -1;
+  // activations move in 16-byte pieces: fp32 x, or the Q8_K parts (q rows and bsums are 16-byte
+  // multiples, d is 256-byte aligned in the workspace layout)
+  if (act.q == nullptr ? ((uintptr_t)act.x & 15) != 0
+                       : (((uintptr_t)act.q | (uintptr_t)act.bsums | (uintptr_t)act.d) & 15) != 0)
+    return -1;
+  switch (type) {
+    case T_Q4_K: return launch_wave_type<T_Q4_K>(w, row_bytes, act, y, n_rows, stream);
+    case T_Q8_0: return launch_wave_type<T_Q8_0>(w, row_bytes, act, y, n_rows, stream);
+    case T_Q6_K: return launch_wave_type<T_Q6_K>(w, row_bytes, act, y, n_rows, stream);
+    default: return -1;
+  }
+}
+
+}  // namespace mxa

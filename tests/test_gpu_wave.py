@@ -1,0 +1,82 @@
+"""GPU parity of the one-row decode kernel in the read floor's shape (mxa_gemv_wave.hip) against
+the CPU oracle, through the C ABI: bit-exact for Q8_0 / Q4_K / Q6_K.
+
+The kernel takes every one-token K-quant / Q8_0 call whose blocks per row nb = K / 256 divide 64
+and whose rows fit one round of its workgroups (one per CU). A wave owns 64 / nb rows; the shapes
+cover each nb it is built for (4, 8, 16, 32, 64), N that leaves the last wave or workgroup
+partial, N so small that some workgroups' waves only stage the activations, N at the largest one
+round holds on a 256-CU MI355X (14 Q4_K waves of 4 rows, 8 Q8_0, 9 Q6_K per CU) and one row past
+it (another kernel then), with x quantized in the kernel and with Q8_K blocks from the workspace.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from matricxon_amd import synthetic as S
+from matricxon_amd.gemm import q8k_bytes
+from oracle import dequant as D
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [D.Q8_0, D.Q4_K, D.Q6_K]
+SHAPES = [(1000, 1024), (1500, 2048), (37, 4096), (1, 4096), (4100, 4096), (2000, 8192),
+          (700, 16384), (3, 16384)]
+# the largest N one round holds per type at K = 4096 on 256 CUs, and one more row
+ROUND_EDGE = {D.Q4_K: 14336, D.Q8_0: 8192, D.Q6_K: 9216}
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bit_exact(got: np.ndarray, want: np.ndarray) -> None:
+    assert got.shape == want.shape
+    diff = np.nonzero(bits(got) != bits(want))
+    assert diff[0].size == 0, (f"{diff[0].size} outputs differ from the oracle, first at "
+                               f"{diff[0][0]},{diff[1][0]}: {got[diff][0]} vs {want[diff][0]}")
+
+
+def run_both(gpu, oracle, t, n, k, seed):
+    w = S.packed_weight(t, n, k, seed=seed)
+    x = S.activations(1, k, seed=seed + 1)
+    want = oracle.gemm(t, w, x, n, k)
+    wd, xd = dev(w), dev(x)
+    assert_bit_exact(host(gpu.matmul(t, wd, xd, n, k)), want)  # x quantized in the kernel
+    ws = torch.empty(q8k_bytes(1, k), dtype=torch.uint8, device="cuda")
+    gpu.quantize_into(xd, ws)
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    assert_bit_exact(host(gpu.matmul_q8k(t, wd, ws, None, out, 1, n, k)), want)  # Q8_K given
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_one_row_wave_kernel_matches_oracle(gpu, oracle, ggml_type, n, k) -> None:
+    run_both(gpu, oracle, ggml_type, n, k, seed=n + k + ggml_type)
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("extra", [0, 1])
+def test_one_row_wave_kernel_round_edge(gpu, oracle, ggml_type, extra) -> None:
+    run_both(gpu, oracle, ggml_type, ROUND_EDGE[ggml_type] + extra, 4096, seed=7 + extra)
+
+
+def test_one_row_wave_kernel_repeated_calls_share_nothing(gpu, oracle) -> None:
+    """Back-to-back calls on different activations in one stream: nothing of one call's
+    activations or counter survives into the next (the counter is reset by every workgroup)."""
+    n, k = 4100, 4096
+    w = S.packed_weight(D.Q4_K, n, k, seed=3)
+    wd = dev(w)
+    xs = [S.activations(1, k, seed=s) for s in (10, 11, 12)]
+    outs = [gpu.matmul(D.Q4_K, wd, dev(x), n, k) for x in xs]
+    for x, y in zip(xs, outs):
+        assert_bit_exact(host(y), oracle.gemm(D.Q4_K, w, x, n, k))
