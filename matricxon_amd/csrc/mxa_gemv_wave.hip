@@ -246,7 +246,12 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
   const int fit = (kWaveLds - wave_act_bytes(NB, FUSEQ)) / wave_region_bytes<TYPE>();
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
-  if (waves < 1 || (long long)waves * R * ncu < N) return -1;  // more rows than one round holds
+  // More rows than one round of workgroups holds: later workgroups start as earlier ones finish.
+  // Measured on MI355X against the pipelined kernel: faster for Q4_K / Q8_0 up to four rounds
+  // (Q4_K 28672 x 4096: 13.5 vs 17.1 us; 57344 x 4096: 25.2 vs 27.2 us), slower for Q6_K (fewer
+  // waves fit: the 128256 x 4096 head 93.9 vs 80.5 us) and for 64-block rows (one row per wave).
+  constexpr int kWgRounds = (TYPE == T_Q6_K || NB > 32) ? 1 : 4;
+  if (waves < 1 || (long long)waves * R * ncu * kWgRounds < N) return -1;
   const int grid = (N + waves * R - 1) / (waves * R);
   // stagers: a round of four blocks each, in waves of their own when the workgroup has fewer
   // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)

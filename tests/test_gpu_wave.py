@@ -2,11 +2,12 @@
 the CPU oracle, through the C ABI: bit-exact for Q8_0 / Q4_K / Q6_K.
 
 The kernel takes every one-token K-quant / Q8_0 call whose blocks per row nb = K / 256 divide 64
-and whose rows fit one round of its workgroups (one per CU). A wave owns 64 / nb rows; the shapes
+and whose rows fit one round of its workgroups (one per CU), or up to four rounds for Q4_K and
+Q8_0 with nb <= 32. A wave owns 64 / nb rows; the shapes
 cover each nb it is built for (4, 8, 16, 32, 64), N that leaves the last wave or workgroup
 partial, N so small that some workgroups' waves only stage the activations, N at the largest one
 round holds on a 256-CU MI355X (14 Q4_K waves of 4 rows, 8 Q8_0, 9 Q6_K per CU) and one row past
-it (another kernel then), with x quantized in the kernel and with Q8_K blocks from the workspace.
+it, several rounds, with x quantized in the kernel and with Q8_K blocks from the workspace.
 """
 
 import numpy as np
@@ -68,6 +69,17 @@ def test_one_row_wave_kernel_matches_oracle(gpu, oracle, ggml_type, n, k) -> Non
 @pytest.mark.parametrize("extra", [0, 1])
 def test_one_row_wave_kernel_round_edge(gpu, oracle, ggml_type, extra) -> None:
     run_both(gpu, oracle, ggml_type, ROUND_EDGE[ggml_type] + extra, 4096, seed=7 + extra)
+
+
+# More rows than one round of workgroups holds (Q4_K / Q8_0, up to four rounds, later
+# workgroups starting as earlier ones finish), and one row past four rounds (another kernel).
+ROUNDS_CASES = [(D.Q4_K, 28672, 4096), (D.Q8_0, 14336, 4096), (D.Q4_K, 14336, 8192),
+                (D.Q4_K, 57344, 4096), (D.Q4_K, 57345, 4096)]
+
+
+@pytest.mark.parametrize("ggml_type,n,k", ROUNDS_CASES)
+def test_one_row_wave_kernel_several_rounds(gpu, oracle, ggml_type, n, k) -> None:
+    run_both(gpu, oracle, ggml_type, n, k, seed=n + k)
 
 
 def test_one_row_wave_kernel_repeated_calls_share_nothing(gpu, oracle) -> None:
