@@ -419,9 +419,9 @@ HEAD_N = 128256
 # Workloads of `--kernel-only [--head]` whose HBM traffic `--traffic-summary` reports:
 # (profile name, kernel-name pattern, algorithmic bytes per launch, workload, kernel source files)
 TRAFFIC_KERNELS = [
-    ("gemv_pipe_q4k_14336x4096_m1", r"gemv_pipe_kernel<12, 1, ", algorithmic_bytes(1),
+    ("gemv_wave_q4k_14336x4096_m1", r"gemv_wave_kernel<12, 16, true, ", algorithmic_bytes(1),
      "Q4_K 14336x4096, M=1, x quantized in the kernel (weight + fp32 x + fp32 y)",
-     ("mxa_gemv_lpb.hip",)),
+     ("mxa_gemv_wave.hip",)),
     ("bflow_q4k_14336x4096_m16", r"bflow_kernel<12, ",
      weight_bytes() + q8k_act_bytes(16, K) + 16 * N * 4,
      "Q4_K 14336x4096, M=16, on Q8_K activations (weight + Q8_K x + fp32 y)",
@@ -686,7 +686,7 @@ def main() -> int:
     if not args.no_cpu:
         cpu = cpu_baseline(w_np, args.cpu_seconds)
 
-    traffic1 = traffic_of("gemv_pipe_q4k_14336x4096_m1")
+    traffic1 = traffic_of("gemv_wave_q4k_14336x4096_m1")
     traffic16 = traffic_of("bflow_q4k_14336x4096_m16")
 
     r1, r16 = results[1], results[16]
@@ -725,7 +725,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(r1["kernel_alg_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic1,
-            "kernel": "gemv_pipe_kernel<Q4_K, M=1, fused Q8_K>",
+            "kernel": "gemv_wave_kernel<Q4_K, nb=16, fused Q8_K>",
             "kernel_us": round(r1["kernel_us"], 3),
             "bytes_per_launch": algorithmic_bytes(1),
             "m16_traffic": traffic16,
