@@ -45,7 +45,7 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 N, K = 14336, 4096
-Q4_K = 12
+Q4_K, Q6_K = 12, 14
 SEED_W, SEED_X = 2, 1002
 
 
@@ -379,6 +379,81 @@ def bench_load(dev) -> None:
           file=sys.stderr, flush=True)
 
 
+MOE_CASES = [
+    # (name, n_experts, top_k, n_embd, ffn_len, types gate/up/down)
+    ("mixtral-8x7b-like", 8, 2, 4096, 14336, (Q4_K, Q4_K, Q6_K)),
+    ("granite-moe-3b-like", 40, 8, 1536, 512, (Q4_K, Q4_K, Q6_K)),
+]
+
+
+def bench_moe(dev, steps: int) -> None:
+    """One MoE expert FFN (moe_experts.py:81-88) on random-init packed experts, per token count:
+    the grouped module (three launches for all experts, routing sorted on the device) against the
+    reference's loop over per-expert DevicePackedLinear calls (one host sync on the routed ids,
+    three calls per active expert). Both give the same bits (tests/test_gpu_moe.py). Eager wall
+    time per forward; one JSON line per case on stderr."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from matricxon_amd import synthetic as S
+    from matricxon_amd.device_packed import DevicePackedLinear
+    from matricxon_amd.moe import HipPackedMoEExperts
+
+    for name, n_exp, top_k, n_embd, ffn, types in MOE_CASES:
+        raws = [np.concatenate([S.packed_weight(t, n_out, k_in, seed=100 * j + e)
+                                for e in range(n_exp)])
+                for j, (t, n_out, k_in) in enumerate(((types[0], ffn, n_embd),
+                                                      (types[1], ffn, n_embd),
+                                                      (types[2], n_embd, ffn)))]
+        mod = HipPackedMoEExperts.from_packed_bytes(*(r.tobytes() for r in raws), types, n_exp,
+                                                    n_embd, ffn, F.silu, torch.bfloat16, dev)
+        per = [tuple(DevicePackedLinear(w[e], k_in, t, None, torch.bfloat16)
+                     for w, k_in, t in ((mod.gate_packed, n_embd, types[0]),
+                                        (mod.up_packed, n_embd, types[1]),
+                                        (mod.down_packed, ffn, types[2])))
+               for e in range(n_exp)]
+
+        def loop(x, tw, tidx):
+            out = torch.zeros(x.shape[0], n_embd, dtype=torch.float32, device=dev)
+            for e in tidx.unique().tolist():
+                g_m, u_m, d_m = per[e]
+                tok, kk = (tidx == e).nonzero(as_tuple=True)
+                x_e = x.index_select(0, tok).unsqueeze(0)
+                h = F.silu(g_m(x_e)) * u_m(x_e)
+                out.index_add_(0, tok, (d_m(h).squeeze(0) * tw[tok, kk].unsqueeze(-1)).float())
+            return out.to(x.dtype)
+
+        expert_bytes = sum(r.nbytes for r in raws) // n_exp
+        for n_tok in (1, 16, 128):
+            g = torch.Generator().manual_seed(n_tok)
+            w, idx = torch.topk(torch.softmax(torch.randn(n_tok, n_exp, generator=g), -1), top_k)
+            tw, tidx = (w / w.sum(-1, keepdim=True)).to(dev), idx.to(dev)
+            x = torch.from_numpy(S.activations(n_tok, n_embd, seed=n_tok)).to(dev, torch.bfloat16)
+            same = bool(torch.equal(mod(x, tw, tidx), loop(x, tw, tidx)))
+            times = {}
+            for label, fn in (("grouped", mod), ("per_expert_loop", loop)):
+                for _ in range(3):
+                    fn(x, tw, tidx)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    fn(x, tw, tidx)
+                torch.cuda.synchronize()
+                times[label] = (time.perf_counter() - t0) / steps * 1e6
+            active = int(tidx.unique().numel())
+            print(json.dumps({"config": f"moe {name} tokens={n_tok}", "experts": n_exp,
+                              "top_k": top_k, "active_experts": active,
+                              "grouped_us": round(times["grouped"], 1),
+                              "per_expert_loop_us": round(times["per_expert_loop"], 1),
+                              "speedup": round(times["per_expert_loop"] / times["grouped"], 2),
+                              "grouped_weight_gbs": round(active * expert_bytes
+                                                          / times["grouped"] / 1e3, 1),
+                              "bit_identical": same}), file=sys.stderr, flush=True)
+        del mod, per, raws
+        torch.cuda.empty_cache()
+
+
 def sources_sha16(files: tuple[str, ...]) -> str:
     """Hash of the kernel sources a measurement depends on: the named files of
     matricxon_amd/csrc and every shared header there (*.hpp). The stamp ties a counter measurement
@@ -546,6 +621,9 @@ def main() -> int:
                          "into HBM, the reference's pageable copy vs the staged uploader")
     ap.add_argument("--configs", action="store_true",
                     help="also time the benchmark configs 1-5 (one JSON line each on stderr)")
+    ap.add_argument("--moe", action="store_true",
+                    help="only the MoE expert FFN: grouped launches vs the per-expert loop "
+                         "(one JSON line per case on stderr)")
     ap.add_argument("--head", action="store_true",
                     help="with --kernel-only: also the config 3 Q6_K 128256x4096 head at M=1 "
                          "and M=16 (for rocprofv3 --pmc runs)")
@@ -576,6 +654,9 @@ def main() -> int:
 
     if args.prefill_only:
         prefill_eager(gemm, dev, args.steps)
+        return 0
+    if args.moe:
+        bench_moe(dev, min(args.steps, 50))
         return 0
 
     w_np = S.packed_weight(Q4_K, N, K, seed=SEED_W)

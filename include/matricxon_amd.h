@@ -118,6 +118,24 @@ int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_t
                  int out_features, int in_features, const void *workspace,
                  size_t workspace_bytes, void *stream);
 
+/* Grouped projection of packed MoE experts, one launch for all of them: expert e of n_experts
+ * (packed weight w + e * expert_stride bytes, out_features x row bytes; w 4-byte aligned,
+ * expert_stride a multiple of 4) multiplies
+ * rows [offsets[e], offsets[e + 1]) of x (n_rows, in_features) fp32, writing the same rows of
+ * y (n_rows, out_features). `offsets` is a DEVICE int32 array of n_experts + 1 ascending values
+ * from 0 to n_rows (the rows grouped by expert), so routing needs no host sync;
+ * max_rows_per_expert is a host bound on any expert's rows (n_rows always is one). x == NULL:
+ * `workspace` already holds the Q8_K activations of the n_rows rows (mxa_quantize_q8_k,
+ * mxa_silu_mul_q8_k). workspace: mxa_quantize_q8_k's layout for n_rows rows. Each row equals
+ * mxa_gemm of that row alone bit for bit. Q4_K, Q6_K, Q8_0 (IQ4_XS: -1).
+ * Replaces the per-expert loop of `QuantizedMoEExperts.forward`
+ * (app/architectures/moe_experts.py:81-88: one `DevicePackedLinear` call per active expert and
+ * projection, after a host sync on the routed expert ids). */
+int mxa_gemm_moe(int ggml_type, const void *w, long long expert_stride, int n_experts,
+                 const float *x, const int32_t *offsets, int n_rows, int max_rows_per_expert,
+                 float *y, int out_features, int in_features, void *workspace,
+                 size_t workspace_bytes, void *stream);
+
 /* Up to 4 packed weights sharing one input (q/k/v, gate/up): one activation quantization, then
  * each weight's output columns written after the previous weight's, y (n_tokens, sum outs).
  * `types`, `ws` (device pointers) and `outs` are HOST arrays of n entries.

@@ -166,6 +166,15 @@ bool mtile_supported(int type);
 int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Grouped MoE projection (mxa_mtile.hip): expert e of n_experts multiplies rows
+// [offsets[e], offsets[e + 1]) of the total_rows Q8_K activation rows in `act` (a device array of
+// n_experts + 1 ascending offsets; at most max_rows rows per expert) by its packed weight
+// w + e * expert_stride (n_rows x row_bytes), writing the same rows of y. Q4_K, Q6_K, Q8_0; -1
+// otherwise.
+int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                   int n_experts, const Act& act, const int32_t* offsets, int total_rows,
+                   int max_rows, float* y, long long ldy, int n_rows, hipStream_t stream);
+
 // Batched decode (m_rows <= 16) on the matrix cores with the weight rows streamed into LDS by
 // coalesced copies, one persistent workgroup per CU: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
 // workspace. -1 when the shape does not suit it (the caller uses launch_mtile).

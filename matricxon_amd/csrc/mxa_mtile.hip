@@ -199,9 +199,12 @@ constexpr int kDecBStride = kDecCh * 16 + 8;
 
 // kDecRT 16-row weight tiles per workgroup: 2, or 1 for Q6_K (its per-lane block bytes need twice
 // the registers; one tile keeps two waves per SIMD).
+// The body of one workgroup: weight tile `wg` of n_wg (16 kDecRT rows) against M <= 16 activation
+// rows.
 template <int TYPE, int kDecRT>
-__global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                   float* __restrict__ y, long long ldy, int M, int N) {
+__device__ __forceinline__ void mdec_rows(const uint8_t* w, long long row_bytes, const Act& act,
+                                          float* __restrict__ y, long long ldy, int M, int N, int wg,
+                                          int n_wg) {
   using Tile = typename TileOf<TYPE>::T;
   using W = typename Tile::W;
   __shared__ __align__(16) int8_t Aq[16 * kDecQStride];
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ln = lane & 15, g = lane >> 4;
-  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * 16 * kDecRT;
+  const int n0 = xcd_tile(wg, n_wg) * 16 * kDecRT;
   const uint8_t* rows[kDecRT];
 #pragma unroll
   for (int t = 0; t < kDecRT; ++t) rows[t] = w + (size_t)min(n0 + 16 * t + ln, N - 1) * row_bytes;
@@ -304,6 +307,37 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
   }
 }
 
+template <int TYPE, int kDecRT>
+__global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long row_bytes, Act act,
+                                                   float* __restrict__ y, long long ldy, int M, int N) {
+  mdec_rows<TYPE, kDecRT>(w, row_bytes, act, y, ldy, M, N, blockIdx.x, gridDim.x);
+}
+
+// Grouped MoE projection: expert e = blockIdx.y multiplies its rows [offsets[e], offsets[e + 1])
+// of the Q8_K activations (16 per blockIdx.z) by its packed weight (w + e * expert_stride); the
+// outputs go to the same rows of y. A workgroup whose expert has no row in its chunk exits. The
+// offsets come from the device (no host sync), so they are clamped to [0, total_rows): a bad
+// table gives wrong rows, never an access outside the activations or y.
+template <int TYPE, int kDecRT>
+__global__ __launch_bounds__(256) void moe_dec_kernel(const uint8_t* w, long long row_bytes,
+                                                      long long expert_stride, Act act,
+                                                      const int32_t* __restrict__ offsets,
+                                                      int total_rows, float* __restrict__ y,
+                                                      long long ldy, int N) {
+  const int e = blockIdx.y;
+  const int begin = min(max(offsets[e], 0), total_rows);
+  const int end = min(max(offsets[e + 1], begin), total_rows);
+  const int p0 = begin + 16 * (int)blockIdx.z;
+  const int M = min(16, end - p0);
+  if (M <= 0) return;  // uniform over the workgroup
+  Act a = act;
+  a.q = act.q + (size_t)p0 * act.k;
+  a.d = act.d + (size_t)p0 * act.nb;
+  a.bsums = act.bsums + (size_t)p0 * act.nb * 16;
+  mdec_rows<TYPE, kDecRT>(w + (size_t)e * expert_stride, row_bytes, a, y + (size_t)p0 * ldy, ldy, M,
+                          N, blockIdx.x, gridDim.x);
+}
+
 template <int TYPE, int MT, int NT, int WAVES>
 int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
               int N, hipStream_t stream) {
@@ -342,6 +376,28 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float*
 }  // namespace
 
 bool mtile_supported(int type) { return type == T_Q4_K || type == T_Q6_K || type == T_Q8_0; }
+
+int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                   int n_experts, const Act& act, const int32_t* offsets, int total_rows,
+                   int max_rows, float* y, long long ldy, int n_rows, hipStream_t stream) {
+  if (act.q == nullptr || n_experts < 1 || n_experts > 65535 || max_rows < 1 || n_rows < 1 ||
+      total_rows < 1)
+    return -1;
+  const int chunks = (max_rows + 15) / 16;
+  if (chunks > 65535) return -1;
+  auto go = [&](auto kern, int rt) {
+    const int tiles = (n_rows + 16 * rt - 1) / (16 * rt);
+    hipLaunchKernelGGL(kern, dim3(tiles, n_experts, chunks), dim3(256), 0, stream, w, row_bytes,
+                       expert_stride, act, offsets, total_rows, y, ldy, n_rows);
+    return 0;
+  };
+  switch (type) {
+    case T_Q4_K: return go(moe_dec_kernel<T_Q4_K, 2>, 2);
+    case T_Q8_0: return go(moe_dec_kernel<T_Q8_0, 2>, 2);
+    case T_Q6_K: return go(moe_dec_kernel<T_Q6_K, 1>, 1);
+    default: return -1;
+  }
+}
 
 int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream) {

@@ -323,6 +323,59 @@ class HipGemm:
         self._check(status, "mxa_silu_mul_q8_k", 15)
         return out, ws
 
+    def matmul_moe(self, ggml_type: int, experts: torch.Tensor, x: torch.Tensor | None,
+                   offsets: torch.Tensor, max_rows_per_expert: int, out_features: int,
+                   in_features: int, workspace: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+        """Grouped projection of packed MoE experts (`mxa_gemm_moe`), one launch for all of
+        them: `experts` (n_experts, out_features, row_bytes) uint8 on the device; rows
+        [offsets[e], offsets[e + 1]) of `x` (n_rows, in_features) go through expert e
+        (`offsets`: int32 on the device, n_experts + 1 ascending values from 0 to n_rows, so no
+        host sync). x None: `workspace` already holds the Q8_K activations of the n_rows rows.
+        Returns (n_rows, out_features) float32; each row equals `matmul` of that row alone bit
+        for bit. Replaces the per-expert calls of QuantizedMoEExperts.forward
+        (app/architectures/moe_experts.py:81-88)."""
+        ggml_type = int(ggml_type)
+        _require_device_tensor("experts", experts)
+        device = experts.device
+        rb = self.row_bytes(ggml_type, in_features)
+        if experts.dtype != torch.uint8 or experts.dim() != 3 or \
+                tuple(experts.shape[1:]) != (out_features, rb) or not experts.is_contiguous():
+            raise ValueError(f"experts must be contiguous uint8 (n_experts, {out_features}, {rb})")
+        n_experts = experts.shape[0]
+        if offsets.dtype != torch.int32 or offsets.shape != (n_experts + 1,) or \
+                offsets.device != device:
+            raise ValueError(f"offsets must be int32 ({n_experts + 1},) on {device}")
+        x32 = None
+        if x is not None:
+            x32 = _aligned16(x.detach().reshape(-1, in_features).to(device=device,
+                                                                    dtype=torch.float32).contiguous())
+            n_rows = x32.shape[0]
+        elif workspace is None:
+            raise ValueError("matmul_moe needs x or a workspace holding its Q8_K activations")
+        else:
+            n_rows = out.shape[0] if out is not None else -1
+            if n_rows < 0:
+                raise ValueError("matmul_moe on a prequantized workspace needs `out` (n_rows rows)")
+        if out is None:
+            out = torch.empty((n_rows, out_features), dtype=torch.float32, device=device)
+        elif out.shape != (n_rows, out_features) or out.dtype != torch.float32 or \
+                not out.is_contiguous() or out.device != device:
+            raise ValueError("out must be a contiguous float32 (n_rows, out_features) tensor")
+        if n_rows == 0:
+            return out
+        ws_bytes = q8k_bytes(n_rows, in_features)
+        if workspace is None:
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        status = self._lib.mxa_gemm_moe(
+            ggml_type, experts.data_ptr(), rb * out_features, n_experts,
+            None if x32 is None else x32.data_ptr(), offsets.data_ptr(), n_rows,
+            max(1, min(int(max_rows_per_expert), n_rows)), out.data_ptr(), out_features,
+            in_features, workspace.data_ptr(), workspace.numel(), _stream(device))
+        self._check(status, "mxa_gemm_moe", ggml_type)
+        self._calls += 1
+        return out
+
     def matmul_multi_q8k(self, items: list[tuple[int, torch.Tensor, int]], workspace: torch.Tensor,
                          n_tokens: int, in_features: int,
                          out: torch.Tensor | None = None) -> list[torch.Tensor]:

@@ -1,0 +1,116 @@
+"""Packed MoE experts on the device with one grouped launch per projection: the drop-in for the
+reference's `QuantizedMoEExperts` in packed-GPU mode (app/architectures/moe_experts.py:29-89).
+
+The reference loops over the routed experts on the host (`top_k_idx.unique().tolist()`, a host
+sync), gathers each expert's tokens and calls that expert's `DevicePackedLinear` three times, then
+adds each expert's weighted output into the result in ascending expert order (moe_experts.py:81-88).
+Here the routing is sorted on the device into (token, expert) pairs grouped by expert, and each
+projection is one `mxa_gemm_moe` launch over all experts. Every pair row equals the reference's
+per-expert row bit for bit (the same packed matmul per row), the projections' outputs take the
+module's dtype as the reference's modules return it, and the weighted outputs are added per token
+in ascending expert order, so the result is the reference's bit for bit.
+"""
+
+from collections.abc import Callable
+
+import torch
+from torch import nn
+
+from .gemm import HipGemm
+
+
+def route_pairs(top_k_idx: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, torch.Tensor,
+                                                                    torch.Tensor]:
+    """(order, offsets, pair_tok) of the routing (n_tokens, top_k), all on its device and without
+    a host sync: `order` sorts the flattened (token, slot) pairs by expert (stable: tokens
+    ascending within an expert), `offsets` (num_experts + 1, int32) delimits each expert's pairs,
+    and `pair_tok` is the token of each sorted pair. Expert ids outside [0, num_experts) are
+    clamped into it (a router never produces them; clamping keeps a bad id from indexing past
+    the counts)."""
+    flat = top_k_idx.reshape(-1).to(torch.int64).clamp(0, num_experts - 1)
+    order = torch.argsort(flat, stable=True)
+    counts = torch.zeros(num_experts, dtype=torch.int64, device=flat.device)
+    counts.scatter_add_(0, flat, torch.ones_like(flat))
+    offsets = torch.zeros(num_experts + 1, dtype=torch.int32, device=flat.device)
+    offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
+    pair_tok = order // top_k_idx.shape[1]
+    return order, offsets, pair_tok
+
+
+def combine_in_expert_order(contrib: torch.Tensor, order: torch.Tensor, top_k_idx: torch.Tensor
+                            ) -> torch.Tensor:
+    """out[t] = the float32 contributions of token t's pairs added in ascending expert order, as
+    the reference's loop of `index_add_` over the sorted expert ids adds them
+    (app/architectures/moe_experts.py:81-88). `contrib` (n_pairs, n_embd) float32 is in the
+    expert-sorted pair order `order`."""
+    n_tokens, top_k = top_k_idx.shape
+    by_pair = torch.empty_like(contrib)
+    by_pair.index_copy_(0, order, contrib)  # back to (token, slot) order
+    slot_order = torch.argsort(top_k_idx, dim=1, stable=True)
+    rows = torch.arange(n_tokens, device=contrib.device).unsqueeze(1) * top_k + slot_order
+    out = torch.zeros(n_tokens, contrib.shape[1], dtype=torch.float32, device=contrib.device)
+    for r in range(top_k):
+        out += by_pair.index_select(0, rows[:, r])
+    return out
+
+
+class HipPackedMoEExperts(nn.Module):
+    """Packed expert FFN: gate/up/down as (num_experts, out_features, row_bytes) packed bytes on
+    the device (`matricxon_amd.loading.PackedUploader.upload_experts`), all of one GGUF type each.
+    `forward(x, top_k_weights, top_k_idx)` has the reference's signature and result."""
+
+    def __init__(self, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor,
+                 gate_type: int, up_type: int, down_type: int, n_embd: int, ffn_len: int,
+                 activation: Callable[[torch.Tensor], torch.Tensor],
+                 dtype: torch.dtype = torch.float32) -> None:
+        super().__init__()
+        self.num_experts = gate.shape[0]
+        self.n_embd, self.ffn_len = n_embd, ffn_len
+        self.activation = activation
+        self.dtype = dtype
+        self.types = (int(gate_type), int(up_type), int(down_type))
+        self._gemm = HipGemm.get()
+        for t, k in ((gate_type, n_embd), (up_type, n_embd), (down_type, ffn_len)):
+            if not self._gemm.supports(int(t), k) or int(t) == 23:
+                raise ValueError(f"no grouped HIP projection for GGUF type {int(t)}")
+        for name, w in (("gate", gate), ("up", up), ("down", down)):
+            if w.dim() != 3 or w.shape[0] != self.num_experts or (w.shape[1] * w.shape[2]) % 4:
+                raise ValueError(f"{name} experts must be (num_experts, out, row_bytes) with each "
+                                 "expert's bytes a multiple of 4")
+        self.register_buffer("gate_packed", gate, persistent=False)
+        self.register_buffer("up_packed", up, persistent=False)
+        self.register_buffer("down_packed", down, persistent=False)
+
+    def forward(self, x: torch.Tensor, top_k_weights: torch.Tensor,
+                top_k_idx: torch.Tensor) -> torch.Tensor:
+        n_tokens, n_embd = x.shape
+        top_k = top_k_idx.shape[1]
+        order, offsets, pair_tok = route_pairs(top_k_idx, self.num_experts)
+        g = self._gemm
+        # the reference casts x to the layer dtype before each matmul (device_packed.py:54)
+        xs = x.to(self.dtype).index_select(0, pair_tok)  # each pair's token, by expert
+        bound = n_tokens  # an expert takes each token at most once
+        gt, ut, dt = self.types
+        gate = g.matmul_moe(gt, self.gate_packed, xs, offsets, bound, self.ffn_len, n_embd)
+        up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd)
+        act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
+        down = g.matmul_moe(dt, self.down_packed, act, offsets, bound, n_embd, self.ffn_len)
+        w = top_k_weights.reshape(-1).index_select(0, order).unsqueeze(-1)
+        contrib = (down.to(self.dtype) * w).to(torch.float32)  # sorted pair order
+        return combine_in_expert_order(contrib, order, top_k_idx).to(x.dtype)
+
+    @classmethod
+    def from_packed_bytes(cls, gate_raw, up_raw, down_raw, types: tuple[int, int, int],
+                          num_experts: int, n_embd: int, ffn_len: int,
+                          activation: Callable[[torch.Tensor], torch.Tensor],
+                          dtype: torch.dtype, device: torch.device) -> "HipPackedMoEExperts":
+        """From the GGUF bytes of the three expert tensors ((num_experts, out, in) each, as
+        `loader.raw_tensor_bytes_and_type` returns them for moe_experts.py:108-121), uploaded
+        still packed, one allocation per tensor."""
+        from .loading import PackedUploader
+
+        with PackedUploader(device) as up:
+            gate, _ = up.upload_experts(gate_raw, num_experts, ffn_len)
+            upw, _ = up.upload_experts(up_raw, num_experts, ffn_len)
+            down, _ = up.upload_experts(down_raw, num_experts, n_embd)
+        return cls(gate, upw, down, *types, n_embd, ffn_len, activation, dtype)

@@ -1,0 +1,178 @@
+"""GPU parity of the grouped MoE projection (`mxa_gemm_moe`, one launch over all experts) and of
+`HipPackedMoEExperts`, the packed-GPU `QuantizedMoEExperts` (app/architectures/moe_experts.py:29-89).
+
+Each row of the grouped launch must equal the CPU oracle's matmul of that row by its expert's
+weight bit for bit. The module must equal, bit for bit, the reference's own forward loop
+(moe_experts.py:81-88) run over per-expert `DevicePackedLinear`s: one call per active expert and
+projection, `index_add_` in ascending expert order. Routings cover experts with no rows, an
+expert with more than one 16-row chunk, a single token, all tokens on one expert, and output
+widths that leave the last row tile partial.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from matricxon_amd import synthetic as S
+from matricxon_amd.device_packed import DevicePackedLinear
+from matricxon_amd.gemm import q8k_bytes
+from matricxon_amd.moe import HipPackedMoEExperts, route_pairs
+from oracle import dequant as D
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [D.Q4_K, D.Q6_K, D.Q8_0]
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bit_exact(got: np.ndarray, want: np.ndarray, what: str) -> None:
+    assert got.shape == want.shape, what
+    diff = np.nonzero(bits(got) != bits(want))
+    assert diff[0].size == 0, (f"{what}: {diff[0].size} outputs differ, first at "
+                               f"{diff[0][0]},{diff[1][0]}: {got[diff][0]} vs {want[diff][0]}")
+
+
+def expert_weights(t: int, n_experts: int, n: int, k: int, seed: int) -> np.ndarray:
+    """(n_experts, n, row_bytes) packed bytes, each expert its own random weight."""
+    return np.stack([S.packed_weight(t, n, k, seed=seed + e) for e in range(n_experts)])
+
+
+def offsets_of(counts: list[int]) -> np.ndarray:
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+
+
+# rows per expert: an empty expert first, in the middle and last; one expert past 16 rows
+COUNTS = [[0, 3, 0, 37, 1, 0], [5], [1, 1, 1, 1], [0, 0, 17, 0]]
+
+
+@pytest.mark.parametrize("ggml_type", TYPES)
+@pytest.mark.parametrize("n,k", [(512, 1024), (300, 2048), (96, 256)])
+@pytest.mark.parametrize("ci", range(len(COUNTS)))
+def test_grouped_rows_match_oracle(gpu, oracle, ggml_type, n, k, ci) -> None:
+    counts = COUNTS[ci]
+    n_experts, n_rows = len(counts), sum(counts)
+    w = expert_weights(ggml_type, n_experts, n, k, seed=n + k + ci)
+    x = S.activations(n_rows, k, seed=ci + 1)
+    off = offsets_of(counts)
+    want = np.zeros((n_rows, n), dtype=np.float32)
+    for e in range(n_experts):
+        if counts[e]:
+            want[off[e]:off[e + 1]] = oracle.gemm(ggml_type, w[e], x[off[e]:off[e + 1]], n, k)
+    wd = torch.from_numpy(w).cuda()
+    offd = torch.from_numpy(off).cuda()
+    xd = torch.from_numpy(x).cuda()
+    got = gpu.matmul_moe(ggml_type, wd, xd, offd, max(counts), n, k)
+    assert_bit_exact(got.cpu().numpy(), want, "x quantized by the call")
+    # the Q8_K activations already in the workspace (x None)
+    ws = torch.empty(q8k_bytes(n_rows, k), dtype=torch.uint8, device="cuda")
+    gpu.quantize_into(xd, ws)
+    out = torch.full((n_rows, n), float("nan"), dtype=torch.float32, device="cuda")
+    got = gpu.matmul_moe(ggml_type, wd, None, offd, max(counts), n, k, workspace=ws, out=out)
+    assert_bit_exact(got.cpu().numpy(), want, "Q8_K given")
+
+
+def test_grouped_rows_with_loose_bound(gpu, oracle) -> None:
+    """max_rows_per_expert above every expert's count (the module passes n_tokens): the extra
+    16-row chunks find no rows and exit."""
+    counts = [2, 0, 9]
+    n, k, t = 256, 1024, D.Q4_K
+    w = expert_weights(t, len(counts), n, k, seed=5)
+    x = S.activations(sum(counts), k, seed=6)
+    off = offsets_of(counts)
+    got = gpu.matmul_moe(t, torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(),
+                         torch.from_numpy(off).cuda(), 200, n, k).cpu().numpy()
+    for e in range(len(counts)):
+        if counts[e]:
+            assert_bit_exact(got[off[e]:off[e + 1]],
+                             oracle.gemm(t, w[e], x[off[e]:off[e + 1]], n, k), f"expert {e}")
+
+
+def test_route_pairs_on_device_matches_host() -> None:
+    idx = torch.tensor([[3, 0], [1, 3], [0, 2], [3, 1]], device="cuda")
+    order, offsets, pair_tok = route_pairs(idx, 5)
+    assert offsets.cpu().tolist() == [0, 2, 4, 5, 8, 8]
+    assert order.cpu().tolist() == [1, 4, 2, 7, 5, 0, 3, 6]
+    assert pair_tok.cpu().tolist() == [0, 2, 1, 3, 2, 0, 1, 3]
+
+
+def reference_forward(x, top_k_weights, top_k_idx, per_expert, activation):
+    """The reference's QuantizedMoEExperts.forward (moe_experts.py:81-88) over per-expert
+    DevicePackedLinear modules: gate, up, down per active expert in ascending id order."""
+    n_tokens, n_embd = x.shape
+    out = torch.zeros(n_tokens, n_embd, dtype=torch.float32, device=x.device)
+    for expert_id in top_k_idx.unique().tolist():
+        gate_m, up_m, down_m = per_expert[expert_id]
+        token_idx, k_idx = (top_k_idx == expert_id).nonzero(as_tuple=True)
+        x_e = x.index_select(0, token_idx)
+        gate = activation(gate_m(x_e.unsqueeze(0)).squeeze(0))
+        up = up_m(x_e.unsqueeze(0)).squeeze(0)
+        down = down_m((gate * up).unsqueeze(0)).squeeze(0)
+        weight = top_k_weights[token_idx, k_idx].unsqueeze(-1)
+        out.index_add_(0, token_idx, (down * weight).to(torch.float32))
+    return out.to(x.dtype)
+
+
+def build_experts(types, n_experts, n_embd, ffn_len, dtype, seed):
+    gt, ut, dt = types
+    gate = expert_weights(gt, n_experts, ffn_len, n_embd, seed)
+    up = expert_weights(ut, n_experts, ffn_len, n_embd, seed + 100)
+    down = expert_weights(dt, n_experts, n_embd, ffn_len, seed + 200)
+    mod = HipPackedMoEExperts.from_packed_bytes(gate.tobytes(), up.tobytes(), down.tobytes(),
+                                                types, n_experts, n_embd, ffn_len, F.silu, dtype,
+                                                torch.device("cuda"))
+    per_expert = [tuple(DevicePackedLinear(torch.from_numpy(np.ascontiguousarray(w[e])).cuda(),
+                                           k, t, None, dtype)
+                        for w, k, t in ((gate, n_embd, gt), (up, n_embd, ut), (down, ffn_len, dt)))
+                  for e in range(n_experts)]
+    return mod, per_expert
+
+
+def routing(n_tokens, n_experts, top_k, seed, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(n_tokens, n_experts, generator=g)
+    w, idx = torch.topk(torch.softmax(logits, dim=-1), top_k, dim=-1)
+    return (w / w.sum(-1, keepdim=True)).to(device), idx.to(device)
+
+
+MODULE_CASES = [
+    # (types gate/up/down, n_experts, n_embd, ffn_len, n_tokens, top_k, dtype)
+    ((D.Q4_K, D.Q4_K, D.Q6_K), 8, 1024, 512, 24, 2, torch.float32),
+    ((D.Q8_0, D.Q8_0, D.Q8_0), 4, 512, 768, 7, 2, torch.float32),
+    ((D.Q4_K, D.Q4_K, D.Q4_K), 16, 512, 256, 40, 4, torch.bfloat16),
+    ((D.Q6_K, D.Q6_K, D.Q4_K), 8, 256, 512, 1, 2, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", range(len(MODULE_CASES)))
+def test_module_matches_reference_loop(case) -> None:
+    types, n_experts, n_embd, ffn_len, n_tokens, top_k, dtype = MODULE_CASES[case]
+    mod, per_expert = build_experts(types, n_experts, n_embd, ffn_len, dtype, seed=case * 7)
+    x = torch.from_numpy(S.activations(n_tokens, n_embd, seed=case + 3)).cuda().to(dtype)
+    tw, tidx = routing(n_tokens, n_experts, top_k, seed=case)
+    got = mod(x, tw, tidx)
+    want = reference_forward(x, tw, tidx, per_expert, F.silu)
+    assert got.dtype == want.dtype == dtype
+    assert torch.equal(got.float().view(torch.int32), want.float().view(torch.int32)), \
+        f"max |diff| {(got.float() - want.float()).abs().max().item()}"
+
+
+def test_module_all_tokens_on_one_expert() -> None:
+    types = (D.Q4_K, D.Q4_K, D.Q4_K)
+    mod, per_expert = build_experts(types, 4, 256, 256, torch.float32, seed=11)
+    n_tokens = 33  # three 16-row chunks for the one expert
+    x = torch.from_numpy(S.activations(n_tokens, 256, seed=12)).cuda()
+    tidx = torch.full((n_tokens, 1), 2, dtype=torch.int64, device="cuda")
+    tw = torch.rand(n_tokens, 1, generator=torch.Generator().manual_seed(1)).cuda()
+    got = mod(x, tw, tidx)
+    want = reference_forward(x, tw, tidx, per_expert, F.silu)
+    assert torch.equal(got, want)
+
+
+def test_module_rejects_types_without_grouped_launch() -> None:
+    z = torch.zeros((2, 256, 136), dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        HipPackedMoEExperts(z, z, z, D.IQ4_XS, D.IQ4_XS, D.IQ4_XS, 256, 256, F.silu)
