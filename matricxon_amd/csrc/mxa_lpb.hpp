@@ -331,43 +331,46 @@ struct Lpb<T_Q4_K_F> {
   static constexpr int kBytes = 144;
   static constexpr bool kHasD = false;
   // sub-block sb: (d * sc_sb) * sum(x * q) - (dmin * m_sb) * sum(x); high nibbles are taken as
-  // 16 q (one bit operation), whose exact factor 1/16 goes into their scale
+  // 16 q (one bit operation), whose exact factor 1/16 goes into their scale. The block's codes
+  // are read 32 bytes (two sub-blocks) at a time and met by every row before the next 32: with
+  // the whole block held across rows, two or more rows spill at the pipelined kernel's budget.
   template <int MAXM, class A>
   __device__ static void compute(const uint8_t* wb, int off, const A* a, int M, float* V, float& D) {
     const uint8_t* blk = wb + off;  // 4-byte aligned
     const u32x4a4 h = *(const u32x4a4*)blk;
-    uint32_t q[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const u32x4a4 v = *(const u32x4a4*)(blk + 16 + 16 * i);
-      q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
-    }
     const float d = half_to_float(h.x), dmin = half_to_float(h.x >> 16);
     const K4Scales s = k4_scales(h.y, h.z, h.w);
+    float t[MAXM][8];
 #pragma unroll
-    for (int m = 0; m < MAXM; ++m) {
-      if (m < M) {
-        float t[8];
+    for (int c = 0; c < 4; ++c) {
+      uint32_t q[8];
+      const u32x4a4 v0 = *(const u32x4a4*)(blk + 16 + 32 * c);
+      const u32x4a4 v1 = *(const u32x4a4*)(blk + 32 + 32 * c);
+      q[0] = v0.x, q[1] = v0.y, q[2] = v0.z, q[3] = v0.w;
+      q[4] = v1.x, q[5] = v1.y, q[6] = v1.z, q[7] = v1.w;
+      const float d1 = d * (float)k4_pick(s.sc_lo, s.sc_hi, 2 * c);
+      const float m1 = dmin * (float)k4_pick(s.mn_lo, s.mn_hi, 2 * c);
+      const float d2 = (d * (float)k4_pick(s.sc_lo, s.sc_hi, 2 * c + 1)) * 0.0625f;
+      const float m2 = dmin * (float)k4_pick(s.mn_lo, s.mn_hi, 2 * c + 1);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+      for (int m = 0; m < MAXM; ++m) {
+        if (m < M) {
           float plo = 0.0f, phi = 0.0f;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const uint32_t w = q[8 * c + i];
-            plo = dot4_f(a[m].x4(64 * c + 4 * i), w & 0x0F0F0F0Fu, plo);
-            phi = dot4_f(a[m].x4(64 * c + 32 + 4 * i), w & 0xF0F0F0F0u, phi);
+            plo = dot4_f(a[m].x4(64 * c + 4 * i), q[i] & 0x0F0F0F0Fu, plo);
+            phi = dot4_f(a[m].x4(64 * c + 32 + 4 * i), q[i] & 0xF0F0F0F0u, phi);
           }
           const float4 sx = a[m].s4(c);  // sums of elements 64c .. 64c + 63, 16 at a time
-          const float d1 = d * (float)k4_pick(s.sc_lo, s.sc_hi, 2 * c);
-          const float m1 = dmin * (float)k4_pick(s.mn_lo, s.mn_hi, 2 * c);
-          const float d2 = (d * (float)k4_pick(s.sc_lo, s.sc_hi, 2 * c + 1)) * 0.0625f;
-          const float m2 = dmin * (float)k4_pick(s.mn_lo, s.mn_hi, 2 * c + 1);
-          t[2 * c] = fmaf(d1, plo, -(m1 * (sx.x + sx.y)));
-          t[2 * c + 1] = fmaf(d2, phi, -(m2 * (sx.z + sx.w)));
+          t[m][2 * c] = fmaf(d1, plo, -(m1 * (sx.x + sx.y)));
+          t[m][2 * c + 1] = fmaf(d2, phi, -(m2 * (sx.z + sx.w)));
         }
-        V[m] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
       }
     }
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m)
+      if (m < M)
+        V[m] = ((t[m][0] + t[m][1]) + (t[m][2] + t[m][3])) + ((t[m][4] + t[m][5]) + (t[m][6] + t[m][7]));
     D = 0.0f;
   }
   __device__ static float fold(float acc, float, float v, float) { return acc + v; }
