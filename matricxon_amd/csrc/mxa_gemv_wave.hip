@@ -1,10 +1,11 @@
 // Decode GEMV for one activation row in the shape of the read floor: one workgroup per CU whose
 // waves request every byte of their rows at their first instructions, then compute each row set
 // as it lands. y[n] = sum_k x[k] * W[n, k] for K-quant / Q8_0 weights with nb = K / 256 in
-// {4, 8, 16, 32, 64}.
+// {4, 8, 16, 32, 64}, and 56 on Q8_K activations from the workspace.
 //
-// Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, one byte range,
-// 16-byte aligned because row_bytes is) and issues all of its range's 1 KB copies
+// Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, or one row of 56
+// with eight lanes idle; one byte range, 16-byte aligned because row_bytes is) and issues all of
+// its range's 1 KB copies
 // (global_load_lds_dwordx4, fully coalesced) into its own LDS stage before anything waits. The CU
 // takes them in as its memory pipeline drains (it accepts ~64 KB in flight, so half the waves sit
 // in their issue loop for microseconds); the whole matrix is in flight from the start and lands
@@ -37,14 +38,14 @@ namespace {
 constexpr int kWaveMaxWaves = 16;
 constexpr int kWaveLds = 160 * 1024;
 
-template <int TYPE>
-constexpr int wave_stage_bytes() {  // a wave's 64 blocks, in whole 1 KB copies
-  return (64 * Lpb<TYPE>::kBytes + 1023) / 1024 * 1024;
+template <int TYPE, int NB>
+constexpr int wave_stage_bytes() {  // a wave's R = 64 / NB rows of NB blocks, in whole 1 KB copies
+  return ((64 / NB) * NB * Lpb<TYPE>::kBytes + 1023) / 1024 * 1024;
 }
 // LDS of one wave: stage, block values V and (Q6_K) block scales D
-template <int TYPE>
+template <int TYPE, int NB>
 constexpr int wave_region_bytes() {
-  return wave_stage_bytes<TYPE>() + 64 * 4 * (Lpb<TYPE>::kHasD ? 2 : 1);
+  return wave_stage_bytes<TYPE, NB>() + 64 * 4 * (Lpb<TYPE>::kHasD ? 2 : 1);
 }
 // Activation area: q8 pieces (nb * 256 bytes), bsums and d each in whole 1 KB copy windows (a
 // gathering copy writes 1 KB), the counter, then (fp32 x) nb KB of staged x.
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
     int row_bytes, uint32_t pack, const int8_t* __restrict__ aq, const float* __restrict__ ad,
     const int16_t* __restrict__ abs_) {
   using L = Lpb<TYPE>;
-  constexpr int kStage = wave_stage_bytes<TYPE>(), kCopies = kStage / 1024;
+  constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
   constexpr int R = 64 / NB, kRounds = NB / 4;
   extern __shared__ __align__(16) uint8_t smem[];
   const int waves = pack & 0xFF, nq = pack >> 8;
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
   float* act_d = (float*)(smem + wave_d_off(NB));        // [NB]
   lds_int* flag = (lds_int*)(lds_u8*)(smem + wave_flag_off(NB));
   float* xs = (float*)(smem + wave_x_off(NB));           // fp32 x: [NB][256]
-  uint8_t* wreg = smem + wave_act_bytes(NB, FUSEQ) + wave * wave_region_bytes<TYPE>();
+  uint8_t* wreg = smem + wave_act_bytes(NB, FUSEQ) + wave * wave_region_bytes<TYPE, NB>();
   float* Vbuf = (float*)(wreg + kStage);
   float* Dbuf = Vbuf + 64;
 
@@ -219,7 +220,9 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
   if (L::kHasD) Dbuf[lane] = D;
   __builtin_amdgcn_wave_barrier();
   if (lane < nrows) {
-    constexpr int kC = NB < 16 ? NB : 16;  // blocks whose operands are read before they are folded
+    // blocks whose operands are read before they are folded (a divisor of NB)
+    constexpr int kC = NB < 16 ? NB : NB % 16 == 0 ? 16 : 8;
+    static_assert(NB % kC == 0, "fold chunks cover the row exactly");
     float acc = 0.0f;
 #pragma unroll
     for (int bb = 0; bb < NB; bb += kC) {
@@ -244,20 +247,25 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   constexpr int R = 64 / NB;
   const int ncu = cu_count();
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
-  const int fit = (kWaveLds - wave_act_bytes(NB, FUSEQ)) / wave_region_bytes<TYPE>();
+  const int fit = (kWaveLds - wave_act_bytes(NB, FUSEQ)) / wave_region_bytes<TYPE, NB>();
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
   // More rows than one round of workgroups holds: later workgroups start as earlier ones finish.
   // Measured on MI355X against the pipelined kernel: faster for Q4_K / Q8_0 up to four rounds
   // (Q4_K 28672 x 4096: 13.5 vs 17.1 us; 57344 x 4096: 25.2 vs 27.2 us), slower for Q6_K (fewer
   // waves fit: the 128256 x 4096 head 93.9 vs 80.5 us) and for 64-block rows (one row per wave).
-  constexpr int kWgRounds = (TYPE == T_Q6_K || NB > 32) ? 1 : 4;
+  // 56-block rows (K = 14336) take the Q8_K blocks from the workspace only (the 56 KB of staged
+  // fp32 x leave room for too few weight waves: Q4_K 4096 x 14336 13.3 vs 11.2 us on the pipelined
+  // kernel), up to four rounds except Q6_K (Q4_K 4096 x 14336 8.86 vs 11.9 us, Q6_K 2048 x 14336
+  // 8.2 vs 10.9 us; Q6_K 4096 x 14336 in two rounds 16.5 vs 15.8 us).
+  if constexpr (NB == 56 && FUSEQ) return -1;
+  constexpr int kWgRounds = (TYPE == T_Q6_K || (NB > 32 && NB != 56)) ? 1 : 4;
   if (waves < 1 || (long long)waves * R * ncu * kWgRounds < N) return -1;
   const int grid = (N + waves * R - 1) / (waves * R);
   // stagers: a round of four blocks each, in waves of their own when the workgroup has fewer
   // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)
   const int nq = min(kWaveMaxWaves, NB / 4);
   const int nw = max(waves, nq);
-  const int lds = wave_act_bytes(NB, FUSEQ) + waves * wave_region_bytes<TYPE>();  // row waves only
+  const int lds = wave_act_bytes(NB, FUSEQ) + waves * wave_region_bytes<TYPE, NB>();  // row waves only
   auto kern = gemv_wave_kernel<TYPE, NB, FUSEQ, kReg>;
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N,
@@ -280,6 +288,7 @@ int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, floa
     case 8: return launch_wave_nb<TYPE, 8>(w, row_bytes, act, y, N, stream);
     case 16: return launch_wave_nb<TYPE, 16>(w, row_bytes, act, y, N, stream);
     case 32: return launch_wave_nb<TYPE, 32>(w, row_bytes, act, y, N, stream);
+    case 56: return launch_wave_nb<TYPE, 56>(w, row_bytes, act, y, N, stream);
     case 64: return launch_wave_nb<TYPE, 64>(w, row_bytes, act, y, N, stream);
     default: return -1;
   }

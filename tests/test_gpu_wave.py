@@ -2,12 +2,13 @@
 the CPU oracle, through the C ABI: bit-exact for Q8_0 / Q4_K / Q6_K.
 
 The kernel takes every one-token K-quant / Q8_0 call whose blocks per row nb = K / 256 divide 64
-and whose rows fit one round of its workgroups (one per CU), or up to four rounds for Q4_K and
-Q8_0 with nb <= 32. A wave owns 64 / nb rows; the shapes
-cover each nb it is built for (4, 8, 16, 32, 64), N that leaves the last wave or workgroup
-partial, N so small that some workgroups' waves only stage the activations, N at the largest one
-round holds on a 256-CU MI355X (14 Q4_K waves of 4 rows, 8 Q8_0, 9 Q6_K per CU) and one row past
-it, several rounds, with x quantized in the kernel and with Q8_K blocks from the workspace.
+(or nb = 56 on Q8_K blocks from the workspace) and whose rows fit one round of its workgroups
+(one per CU), or up to four rounds for Q4_K and Q8_0 with nb <= 32 or nb = 56. A wave owns
+64 / nb rows (one row of 56 blocks at nb = 56, eight lanes idle); the shapes cover each nb it is
+built for (4, 8, 16, 32, 56, 64), N that leaves the last wave or workgroup partial, N so small
+that some workgroups' waves only stage the activations, N at the largest one round holds on a
+256-CU MI355X (14 Q4_K waves of 4 rows, 8 Q8_0, 9 Q6_K per CU) and one row past it, several
+rounds, with x quantized in the kernel and with Q8_K blocks from the workspace.
 """
 
 import numpy as np
@@ -22,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 TYPES = [D.Q8_0, D.Q4_K, D.Q6_K]
 SHAPES = [(1000, 1024), (1500, 2048), (37, 4096), (1, 4096), (4100, 4096), (2000, 8192),
-          (700, 16384), (3, 16384)]
+          (700, 16384), (3, 16384), (4096, 14336), (1500, 14336), (5, 14336)]
 # the largest N one round holds per type at K = 4096 on 256 CUs, and one more row
 ROUND_EDGE = {D.Q4_K: 14336, D.Q8_0: 8192, D.Q6_K: 9216}
 
@@ -74,7 +75,8 @@ def test_one_row_wave_kernel_round_edge(gpu, oracle, ggml_type, extra) -> None:
 # More rows than one round of workgroups holds (Q4_K / Q8_0, up to four rounds, later
 # workgroups starting as earlier ones finish), and one row past four rounds (another kernel).
 ROUNDS_CASES = [(D.Q4_K, 28672, 4096), (D.Q8_0, 14336, 4096), (D.Q4_K, 14336, 8192),
-                (D.Q4_K, 57344, 4096), (D.Q4_K, 57345, 4096)]
+                (D.Q4_K, 57344, 4096), (D.Q4_K, 57345, 4096), (D.Q4_K, 14336, 14336),
+                (D.Q8_0, 4097, 14336)]
 
 
 @pytest.mark.parametrize("ggml_type,n,k", ROUNDS_CASES)
