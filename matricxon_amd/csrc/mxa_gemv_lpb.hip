@@ -822,6 +822,7 @@ int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long lo
                         int m_rows, hipStream_t stream) {
   if (m_rows < 1 || m_rows > kFusedQuantMaxRows) return -1;
   const bool fuse = act.q == nullptr;
+  if (m_rows == 1 && launch_gemv_wave_multi(seg, count, act, stream) == 0) return 0;
   if (m_rows == 1) return fuse ? launch_pipe_multi<1, true>(seg, count, act, ldy, m_rows, stream)
                                : launch_pipe_multi<1, false>(seg, count, act, ldy, m_rows, stream);
   if (m_rows == 2) return fuse ? launch_pipe_multi<2, true>(seg, count, act, ldy, m_rows, stream)

@@ -77,16 +77,17 @@ constexpr int kWaveSpinLimit = 1 << 22;
 // pack: waves | stagers << 8: the first `waves` waves of the workgroup own rows, the first
 // `stagers` also stage the activations (the workgroup has max(waves, stagers) waves; one that
 // owns no rows only stages)
+// The workgroup's work: workgroup wg of n_wg over the N rows of one weight.
 template <int TYPE, int NB, bool FUSEQ, bool ACTREG>
-__global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
-    const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int N,
-    int row_bytes, uint32_t pack, const int8_t* __restrict__ aq, const float* __restrict__ ad,
-    const int16_t* __restrict__ abs_) {
+__device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                          float* __restrict__ y, int N, int row_bytes, int waves,
+                                          int nq, const int8_t* __restrict__ aq,
+                                          const float* __restrict__ ad,
+                                          const int16_t* __restrict__ abs_, int wg, int n_wg) {
   using L = Lpb<TYPE>;
   constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
   constexpr int R = 64 / NB, kRounds = NB / 4;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int waves = pack & 0xFF, nq = pack >> 8;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint8_t* act_q = smem;                                 // [16][NB][16]
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
   // every copy of the wave's range (the last ones may pass it: they read the next wave's rows,
   // or stop at the matrix's last 16-byte word, and land in this wave's stage)
   const bool has_rows = wave < waves;
-  const int n0 = (xcd_tile(blockIdx.x, gridDim.x) * waves + wave) * R;
+  const int n0 = (xcd_tile(wg, n_wg) * waves + wave) * R;
   const int nrows = has_rows ? max(0, min(R, N - n0)) : 0;
   const uint8_t* src = w + (size_t)min(n0, N - 1) * row_bytes;
   const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
@@ -240,6 +241,47 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
   }
 }
 
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG>
+__global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int N,
+    int row_bytes, uint32_t pack, const int8_t* __restrict__ aq, const float* __restrict__ ad,
+    const int16_t* __restrict__ abs_) {
+  wave_rows<TYPE, NB, FUSEQ, ACTREG>(w, x, y, N, row_bytes, pack & 0xFF, pack >> 8, aq, ad, abs_,
+                                     blockIdx.x, gridDim.x);
+}
+
+// Several weights that share the activation row (q|k|v, gate|up), one launch: each weight's
+// workgroups follow the previous weight's, and a workgroup runs the single-weight form of its
+// weight's block type.
+constexpr int kWaveMaxSegs = 4;
+struct WaveSeg {
+  const uint8_t* w;
+  float* y;
+  int n, row_bytes, type, wg0, waves, n_wg;
+};
+struct WaveSegs {
+  WaveSeg s[kWaveMaxSegs];
+  int count;
+};
+
+template <int NB, bool FUSEQ>
+__global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
+    WaveSegs segs, const float* __restrict__ x, int nq, const int8_t* __restrict__ aq,
+    const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < kWaveMaxSegs; ++i)
+    if (i < segs.count && (int)blockIdx.x >= segs.s[i].wg0) si = i;
+  const WaveSeg& g = segs.s[si];
+  const int wg = (int)blockIdx.x - g.wg0;
+  if (g.type == T_Q4_K)
+    wave_rows<T_Q4_K, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, aq, ad, abs_, wg, g.n_wg);
+  else if (g.type == T_Q8_0)
+    wave_rows<T_Q8_0, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, aq, ad, abs_, wg, g.n_wg);
+  else
+    wave_rows<T_Q6_K, NB, FUSEQ, false>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, aq, ad, abs_, wg, g.n_wg);
+}
+
 template <int TYPE, int NB, bool FUSEQ>
 int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
                   hipStream_t stream) {
@@ -294,6 +336,58 @@ int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, floa
   }
 }
 
+template <int NB>
+int region_of(int type) {
+  return type == T_Q4_K ? wave_region_bytes<T_Q4_K, NB>()
+       : type == T_Q8_0 ? wave_region_bytes<T_Q8_0, NB>()
+                        : wave_region_bytes<T_Q6_K, NB>();
+}
+
+// Each weight gets workgroups in proportion to its bytes (at least one), and its workgroups as
+// many row waves as spread its rows over them; the grid must fit the rounds the single-weight form
+// allows its types.
+template <int NB, bool FUSEQ>
+int launch_wave_multi_t(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream) {
+  constexpr int R = 64 / NB;
+  const int ncu = cu_count();
+  const int act_lds = wave_act_bytes(NB, FUSEQ);
+  double total = 0.0;
+  bool heavy = NB > 32;
+  for (int i = 0; i < count; ++i) {
+    total += (double)seg[i].n * (double)seg[i].row_bytes;
+    heavy = heavy || seg[i].type == T_Q6_K;
+  }
+  WaveSegs segs{};
+  segs.count = count;
+  int grid = 0, nw = min(kWaveMaxWaves, NB / 4), lds = act_lds;
+  for (int i = 0; i < count; ++i) {
+    const int region = region_of<NB>(seg[i].type);
+    const int fit = (kWaveLds - act_lds) / region;
+    const int share = max(1, (int)((double)ncu * seg[i].n * seg[i].row_bytes / total + 0.5));
+    const int per_wg = (seg[i].n + share - 1) / share;
+    const int waves = min(min(kWaveMaxWaves, fit), (per_wg + R - 1) / R);
+    if (waves < 1) return -1;
+    const int wgs = (seg[i].n + waves * R - 1) / (waves * R);
+    segs.s[i] = WaveSeg{seg[i].w, seg[i].y, seg[i].n, (int)seg[i].row_bytes, seg[i].type, grid,
+                        waves, wgs};
+    grid += wgs;
+    nw = max(nw, waves);
+    lds = max(lds, act_lds + waves * region);
+  }
+  if (grid > ncu * (heavy ? 1 : 4)) return -1;
+  auto kern = gemv_wave_multi_kernel<NB, FUSEQ>;
+  allow_lds((const void*)kern, kWaveLds);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, segs, act.x,
+                     min(kWaveMaxWaves, NB / 4), act.q, act.d, act.bsums);
+  return 0;
+}
+
+template <int NB>
+int launch_wave_multi_nb(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream) {
+  return act.q == nullptr ? launch_wave_multi_t<NB, true>(seg, count, act, stream)
+                          : launch_wave_multi_t<NB, false>(seg, count, act, stream);
+}
+
 }  // namespace
 
 int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
@@ -309,6 +403,27 @@ int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act&
     case T_Q4_K: return launch_wave_type<T_Q4_K>(w, row_bytes, act, y, n_rows, stream);
     case T_Q8_0: return launch_wave_type<T_Q8_0>(w, row_bytes, act, y, n_rows, stream);
     case T_Q6_K: return launch_wave_type<T_Q6_K>(w, row_bytes, act, y, n_rows, stream);
+    default: return -1;
+  }
+}
+
+int launch_gemv_wave_multi(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream) {
+  if (count < 1 || count > kWaveMaxSegs) return -1;
+  for (int i = 0; i < count; ++i) {
+    const int t = seg[i].type;
+    if ((t != T_Q4_K && t != T_Q6_K && t != T_Q8_0) || seg[i].n < 1 ||
+        ((uintptr_t)seg[i].w & 15) != 0 || seg[i].row_bytes % 16 != 0 ||
+        seg[i].row_bytes > 0x7FFFFFFF)
+      return -1;
+  }
+  if (act.q == nullptr ? ((uintptr_t)act.x & 15) != 0
+                       : (((uintptr_t)act.q | (uintptr_t)act.bsums | (uintptr_t)act.d) & 15) != 0)
+    return -1;
+  switch (act.nb) {
+    case 4: return launch_wave_multi_nb<4>(seg, count, act, stream);
+    case 8: return launch_wave_multi_nb<8>(seg, count, act, stream);
+    case 16: return launch_wave_multi_nb<16>(seg, count, act, stream);
+    case 32: return launch_wave_multi_nb<32>(seg, count, act, stream);
     default: return -1;
   }
 }

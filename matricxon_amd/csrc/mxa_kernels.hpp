@@ -154,6 +154,10 @@ struct DecodeSeg {
   int n;     // output rows of the weight
 };
 
+// One-row decode over up to 4 Q4_K / Q6_K / Q8_0 weights sharing the activations, in the
+// floor-shaped kernel (mxa_gemv_wave.hip); -1 when the weights do not suit it.
+int launch_gemv_wave_multi(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream);
+
 // Decode for 1 <= m_rows <= 4 over up to 4 K-quant / Q8_0 weights in one launch (shared-input
 // projections such as q/k/v or gate/up); quantizes act.x itself when act.q == nullptr. -1 when
 // the weights do not suit it (the caller launches them one by one).

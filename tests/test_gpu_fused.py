@@ -95,6 +95,8 @@ def test_fused_ops_match_reference_fixtures(gpu) -> None:
 # token counts on each kernel path (decode, batched decode, matrix-core prefill)
 Q8K_GROUPS = [
     ([(D.Q4_K, 512), (D.Q4_K, 128), (D.Q6_K, 128)], 4096, 1),
+    ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 1),
+    ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 1),
     ([(D.Q4_K, 700), (D.Q4_K, 700)], 4096, 3),
     ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65)], 2048, 4),
     ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 9),

@@ -217,6 +217,14 @@ MULTI_CASES = [
     ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 16),
     # q|k|v shape: segments of different types and tile counts
     ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 9),
+    # one token (the floor-shaped multi-weight kernel): q|k|v and gate|up at full size (gate|up
+    # in two rounds of workgroups), four segments of 8-block rows, 4-block rows, and a Q6_K group
+    # past one round (taken by the pipelined kernel instead)
+    ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 1),
+    ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 1),
+    ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65), (D.Q4_K, 1)], 2048, 1),
+    ([(D.Q8_0, 3000), (D.Q4_K, 5000)], 1024, 1),
+    ([(D.Q6_K, 9000), (D.Q4_K, 100)], 4096, 1),
 ]
 
 
