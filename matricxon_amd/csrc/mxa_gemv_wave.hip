@@ -10,7 +10,9 @@
 // takes them in as its memory pipeline drains (it accepts ~64 KB in flight, so half the waves sit
 // in their issue loop for microseconds); the whole matrix is in flight from the start and lands
 // in the order HBM returns it. A wave waits only for its own copies (vmcnt), never for another
-// wave's.
+// wave's. With more rows than the CUs' waves hold, a Q4_K wave takes further row sets, each
+// requested as soon as the previous one's bytes are in registers; other types run later rounds
+// of workgroups.
 //
 // Activations. The first waves (stagers) also bring the activations into LDS with LDS-DMA copies
 // issued before their weight copies: fp32 x, which they then quantize to Q8_K (16 lanes per
@@ -135,18 +137,22 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
 
   // every copy of the wave's range (the last ones may pass it: they read the next wave's rows,
   // or stop at the matrix's last 16-byte word, and land in this wave's stage)
+  // Row set s (rows R s .. R s + R - 1): the workgroup's waves take sets (tile * waves + wave),
+  // then every n_wg * waves further, each set's copies issued as soon as the previous set's bytes
+  // are in registers.
   const bool has_rows = wave < waves;
-  const int n0 = (xcd_tile(wg, n_wg) * waves + wave) * R;
-  const int nrows = has_rows ? max(0, min(R, N - n0)) : 0;
-  const uint8_t* src = w + (size_t)min(n0, N - 1) * row_bytes;
+  const int n_sets = (N + R - 1) / R, set_stride = n_wg * waves;
+  int set = xcd_tile(wg, n_wg) * waves + wave;
   const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
   const uint32_t lds_w = lds_addr(wreg);
-  if (has_rows) {
+  const auto issue = [&](int s) {
+    const uint8_t* src = w + (size_t)min(s * R, N - 1) * row_bytes;
 #pragma unroll
     for (int c = 0; c < kCopies; ++c)
       copy16_to_lds_nt((const void*)min((uintptr_t)src + (uintptr_t)c * 1024 + (uintptr_t)lane * 16, last),
                        lds_w + c * 1024);
-  }
+  };
+  if (has_rows) issue(set);
 
   if (stager) {
     wait_vmcnt(has_rows ? kCopies : 0);  // the activation copies, issued first, have landed
@@ -199,7 +205,6 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   const bool gave_up = spin >= kWaveSpinLimit;
 
   const int b = lane % NB;
-  const int jl = min(lane, max(nrows, 1) * NB - 1);  // lanes past the range redo its last block
   ActPieces ap;
   ap.q = (const int8_t*)(act_q + b * 16);
   ap.stride = NB * 16;
@@ -211,33 +216,46 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
     areg.bs[0] = ap.bs8(0);
     areg.bs[1] = ap.bs8(1);
   }
-  wait_vmcnt(0);
-  float V[1], D;
-  if constexpr (ACTREG)
-    L::template compute<1, ActRegs>(wreg, jl * L::kBytes, &areg, 1, V, D);
-  else
-    L::template compute<1, ActPieces>(wreg, jl * L::kBytes, &ap, 1, V, D);
-  Vbuf[lane] = V[0];
-  if (L::kHasD) Dbuf[lane] = D;
-  __builtin_amdgcn_wave_barrier();
-  if (lane < nrows) {
-    // blocks whose operands are read before they are folded (a divisor of NB)
-    constexpr int kC = NB < 16 ? NB : NB % 16 == 0 ? 16 : 8;
-    static_assert(NB % kC == 0, "fold chunks cover the row exactly");
-    float acc = 0.0f;
-#pragma unroll
-    for (int bb = 0; bb < NB; bb += kC) {
-      float vv[kC], xx[kC], dd[kC];
-#pragma unroll
-      for (int i = 0; i < kC; ++i) {
-        vv[i] = Vbuf[lane * NB + bb + i];
-        xx[i] = act_d[bb + i];
-        dd[i] = L::kHasD ? Dbuf[lane * NB + bb + i] : 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < kC; ++i) acc = L::fold(acc, xx[i], vv[i], dd[i]);
+  for (;;) {
+    const int n0 = set * R;
+    const int nrows = max(0, min(R, N - n0));
+    const int jl = min(lane, max(nrows, 1) * NB - 1);  // lanes past the range redo its last block
+    wait_vmcnt(0);
+    float V[1], D;
+    if constexpr (ACTREG)
+      L::template compute<1, ActRegs>(wreg, jl * L::kBytes, &areg, 1, V, D);
+    else
+      L::template compute<1, ActPieces>(wreg, jl * L::kBytes, &ap, 1, V, D);
+    const int next = set + set_stride;
+    if (next < n_sets) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage's reads have returned
+      issue(next);
     }
-    y[n0 + lane] = gave_up ? __builtin_nanf("") : acc;
+    Vbuf[lane] = V[0];
+    if (L::kHasD) Dbuf[lane] = D;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < nrows) {
+      // blocks whose operands are read before they are folded (a divisor of NB)
+      constexpr int kC = NB < 16 ? NB : NB % 16 == 0 ? 16 : 8;
+      static_assert(NB % kC == 0, "fold chunks cover the row exactly");
+      float acc = 0.0f;
+#pragma unroll
+      for (int bb = 0; bb < NB; bb += kC) {
+        float vv[kC], xx[kC], dd[kC];
+#pragma unroll
+        for (int i = 0; i < kC; ++i) {
+          vv[i] = Vbuf[lane * NB + bb + i];
+          xx[i] = act_d[bb + i];
+          dd[i] = L::kHasD ? Dbuf[lane * NB + bb + i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kC; ++i) acc = L::fold(acc, xx[i], vv[i], dd[i]);
+      }
+      y[n0 + lane] = gave_up ? __builtin_nanf("") : acc;
+    }
+    if (next >= n_sets) break;
+    set = next;
+    __builtin_amdgcn_wave_barrier();  // every lane's fold has read Vbuf before it is rewritten
   }
 }
 
@@ -291,18 +309,27 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
   const int fit = (kWaveLds - wave_act_bytes(NB, FUSEQ)) / wave_region_bytes<TYPE, NB>();
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
-  // More rows than one round of workgroups holds: later workgroups start as earlier ones finish.
-  // Measured on MI355X against the pipelined kernel: faster for Q4_K / Q8_0 up to four rounds
-  // (Q4_K 28672 x 4096: 13.5 vs 17.1 us; 57344 x 4096: 25.2 vs 27.2 us), slower for Q6_K (fewer
-  // waves fit: the 128256 x 4096 head 93.9 vs 80.5 us) and for 64-block rows (one row per wave).
-  // 56-block rows (K = 14336) take the Q8_K blocks from the workspace only (the 56 KB of staged
-  // fp32 x leave room for too few weight waves: Q4_K 4096 x 14336 13.3 vs 11.2 us on the pipelined
-  // kernel), up to four rounds except Q6_K (Q4_K 4096 x 14336 8.86 vs 11.9 us, Q6_K 2048 x 14336
-  // 8.2 vs 10.9 us; Q6_K 4096 x 14336 in two rounds 16.5 vs 15.8 us).
+  // More rows than one round of workgroups holds (measured on MI355X against the pipelined
+  // kernel and each other). Q4_K: one workgroup per CU whose waves take further row sets as their
+  // previous set's bytes reach registers (28672 x 4096: 14.9 us, vs 15.7 in rounds of workgroups
+  // and 17.1 pipelined; 57344 x 4096: 25.6 vs 29.2 and 27.2). Q8_0: rounds of workgroups, later
+  // ones starting as earlier ones finish (row sets per wave measured 6% slower). Q6_K: one round
+  // only (fewer waves fit; the 128256 x 4096 head in rounds 93.9 vs 80.5 us, in row sets 168 us),
+  // and for 64-block rows (one row per wave). 56-block rows (K = 14336) take the Q8_K blocks
+  // from the workspace only (the 56 KB of staged fp32 x leave room for too few weight waves: Q4_K
+  // 4096 x 14336 13.3 vs 11.2 us pipelined), Q6_K in one round (Q4_K 4096 x 14336 8.86 vs 11.9
+  // us, Q6_K 2048 x 14336 8.2 vs 10.9 us; Q6_K 4096 x 14336 in two rounds 16.5 vs 15.8 us).
   if constexpr (NB == 56 && FUSEQ) return -1;
-  constexpr int kWgRounds = (TYPE == T_Q6_K || (NB > 32 && NB != 56)) ? 1 : 4;
-  if (waves < 1 || (long long)waves * R * ncu * kWgRounds < N) return -1;
-  const int grid = (N + waves * R - 1) / (waves * R);
+  if (waves < 1) return -1;
+  int grid = (N + waves * R - 1) / (waves * R);
+  if constexpr (TYPE == T_Q4_K && NB != 64) {
+    constexpr int kSets = 4;  // row sets per wave at most
+    grid = min(grid, ncu);
+    if ((long long)waves * R * grid * kSets < N) return -1;
+  } else {
+    constexpr int kWgRounds = (TYPE == T_Q6_K || (NB > 32 && NB != 56)) ? 1 : 4;
+    if ((long long)waves * R * ncu * kWgRounds < N) return -1;
+  }
   // stagers: a round of four blocks each, in waves of their own when the workgroup has fewer
   // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)
   const int nq = min(kWaveMaxWaves, NB / 4);
