@@ -45,18 +45,21 @@ constexpr int wave_stage_bytes() {  // a wave's R = 64 / NB rows of NB blocks, i
   return ((64 / NB) * NB * Lpb<TYPE>::kBytes + 1023) / 1024 * 1024;
 }
 // LDS of one wave: stage, block values V and (Q6_K) block scales D
-template <int TYPE, int NB>
+// LDS of one wave: stage, block values V (one set per activation row) and (Q6_K) block scales D
+template <int TYPE, int NB, int MAXM = 1>
 constexpr int wave_region_bytes() {
-  return wave_stage_bytes<TYPE, NB>() + 64 * 4 * (Lpb<TYPE>::kHasD ? 2 : 1);
+  return wave_stage_bytes<TYPE, NB>() + 64 * 4 * (MAXM + (Lpb<TYPE>::kHasD ? 1 : 0));
 }
-// Activation area: q8 pieces (nb * 256 bytes), bsums and d each in whole 1 KB copy windows (a
-// gathering copy writes 1 KB), the counter, then (fp32 x) nb KB of staged x.
+// Activation area: per activation row, q8 pieces (nb * 256 bytes), bsums and d each in whole 1 KB
+// copy windows (a gathering copy writes 1 KB); then the counter, then (fp32 x) nb KB of staged x
+// per row.
 __host__ __device__ constexpr int wave_bs_off(int nb) { return nb * QK; }
 __host__ __device__ constexpr int wave_d_off(int nb) { return nb * QK + (nb * 32 + 1023) / 1024 * 1024; }
-__host__ __device__ constexpr int wave_flag_off(int nb) { return wave_d_off(nb) + 1024; }
-__host__ __device__ constexpr int wave_x_off(int nb) { return wave_flag_off(nb) + 16; }
-__host__ __device__ constexpr int wave_act_bytes(int nb, bool fuseq) {
-  return wave_x_off(nb) + (fuseq ? nb * 1024 : 0);
+__host__ __device__ constexpr int wave_row_act(int nb) { return wave_d_off(nb) + 1024; }
+__host__ __device__ constexpr int wave_flag_off(int nb, int m) { return m * wave_row_act(nb); }
+__host__ __device__ constexpr int wave_x_off(int nb, int m) { return wave_flag_off(nb, m) + 16; }
+__host__ __device__ constexpr int wave_act_bytes(int nb, bool fuseq, int m = 1) {
+  return wave_x_off(nb, m) + (fuseq ? m * nb * 1024 : 0);
 }
 
 // Q8_K activations staged as [piece i][block b][16 bytes]: the accessor of block b.
@@ -76,81 +79,88 @@ typedef __attribute__((address_space(3))) int lds_int;
 // counts once after a bounded amount of work); a wave that gives up writes NaN.
 constexpr int kWaveSpinLimit = 1 << 22;
 
-// pack: waves | stagers << 8: the first `waves` waves of the workgroup own rows, the first
-// `stagers` also stage the activations (the workgroup has max(waves, stagers) waves; one that
-// owns no rows only stages)
-// The workgroup's work: workgroup wg of n_wg over the N rows of one weight.
-template <int TYPE, int NB, bool FUSEQ, bool ACTREG>
+// pack: waves | stagers << 8 | activation rows << 16: the first `waves` waves of the workgroup
+// own rows, the first `stagers` also stage the activations (the workgroup has max(waves, stagers)
+// waves; one that owns no rows only stages).
+// The workgroup's work: workgroup wg of n_wg over the N rows of one weight, for M <= MAXM
+// activation rows (y row m at y + m ldy).
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM = 1>
 __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                           float* __restrict__ y, int N, int row_bytes, int waves,
-                                          int nq, const int8_t* __restrict__ aq,
+                                          int nq, int M, int ldy, const int8_t* __restrict__ aq,
                                           const float* __restrict__ ad,
                                           const int16_t* __restrict__ abs_, int wg, int n_wg) {
   using L = Lpb<TYPE>;
+  static_assert(!ACTREG || MAXM == 1, "activations in registers for one row only");
   constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
-  constexpr int R = 64 / NB, kRounds = NB / 4;
+  constexpr int R = 64 / NB, kRounds = NB / 4, kRowAct = wave_row_act(NB), K = NB * QK;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  uint8_t* act_q = smem;                                 // [16][NB][16]
-  int16_t* act_bs = (int16_t*)(smem + wave_bs_off(NB));  // [NB][16]
-  float* act_d = (float*)(smem + wave_d_off(NB));        // [NB]
-  lds_int* flag = (lds_int*)(lds_u8*)(smem + wave_flag_off(NB));
-  float* xs = (float*)(smem + wave_x_off(NB));           // fp32 x: [NB][256]
-  uint8_t* wreg = smem + wave_act_bytes(NB, FUSEQ) + wave * wave_region_bytes<TYPE, NB>();
-  float* Vbuf = (float*)(wreg + kStage);
-  float* Dbuf = Vbuf + 64;
+  // activation row m: q8 pieces [16][NB][16] at smem + kRowAct m, bsums [NB][16], d [NB]
+  const auto act_q = [&](int m) { return smem + kRowAct * m; };
+  const auto act_bs = [&](int m) { return (int16_t*)(smem + kRowAct * m + wave_bs_off(NB)); };
+  const auto act_d = [&](int m) { return (float*)(smem + kRowAct * m + wave_d_off(NB)); };
+  lds_int* flag = (lds_int*)(lds_u8*)(smem + wave_flag_off(NB, M));
+  float* xs = (float*)(smem + wave_x_off(NB, M));  // fp32 x: row m at xs + m K
+  uint8_t* wreg = smem + wave_act_bytes(NB, FUSEQ, M) + wave * wave_region_bytes<TYPE, NB, MAXM>();
+  float* Vbuf = (float*)(wreg + kStage);  // row m's block values at Vbuf + 64 m
+  float* Dbuf = Vbuf + 64 * MAXM;
 
   if (tid == 0) *flag = 0;
   __syncthreads();  // nothing is outstanding yet: the barrier waits for no memory
 
   // stager copies, ahead of this wave's weight copies: fp32 x one 1 KB block per copy (rounds of
-  // four blocks: wave, wave + nq, ..), or the Q8_K parts gathered into place (copy j by stager
-  // j % nq)
+  // four blocks of one row: wave, wave + nq, ..), or the Q8_K parts gathered into place (copy j
+  // by stager j % nq)
   const bool stager = wave < nq;
+  constexpr int kQ = NB / 4, kBs = (NB * 2 + 63) / 64, kPer = kQ + kBs + 1;  // gather copies per row
   if (stager) {
     if constexpr (FUSEQ) {
-      for (int r = wave; r < kRounds; r += nq)
-        for (int g = 4 * r; g < 4 * r + 4; ++g)
-          copy16_to_lds((const void*)(x + g * QK + 4 * lane), lds_addr(xs + g * QK));
+      for (int r = wave; r < kRounds * M; r += nq) {
+        const int m = r / kRounds, g0 = 4 * (r % kRounds);
+        for (int g = g0; g < g0 + 4; ++g)
+          copy16_to_lds((const void*)(x + (size_t)m * K + g * QK + 4 * lane),
+                        lds_addr(xs + m * K + g * QK));
+      }
     } else {
-      constexpr int kQ = NB / 4, kBs = (NB * 2 + 63) / 64;  // copies of q8 pieces and of bsums
-      for (int j = wave; j < kQ + kBs + 1; j += nq) {
-        const void* src;
-        uint32_t dst;
-        if (j < kQ) {  // slot s = 64 j + lane: piece s / NB of block s % NB
-          const int s = 64 * j + lane;
-          src = aq + (s % NB) * QK + 16 * (s / NB);
-          dst = lds_addr(act_q + 1024 * j);
-        } else if (j < kQ + kBs) {  // eight bsums per slot; slots past the last repeat it
-          const int s = min(64 * (j - kQ) + lane, 2 * NB - 1);
-          src = abs_ + 8 * s;
-          dst = lds_addr((uint8_t*)act_bs + 1024 * (j - kQ));
-        } else {  // four scales per slot; slots past the last repeat it
-          src = ad + 4 * min(lane, NB / 4 - 1);
-          dst = lds_addr(act_d);
-        }
-        copy16_to_lds(src, dst);
+      // Copy j of row m: q8 pieces (j < kQ; slot s = 64 j + lane: piece s / NB of block s % NB),
+      // bsums (eight per slot), or the scales (four per slot); slots past the last repeat it.
+      // Selected without branches: as a three-way branch on j this loop was compiled with the
+      // scales' LDS destination left unset (the copy landed on the bsums).
+      for (int jm = wave; jm < kPer * M; jm += nq) {
+        const int m = jm / kPer, j = jm % kPer;
+        const int sq = 64 * min(j, kQ - 1) + lane;
+        const int sb = min(64 * max(j - kQ, 0) + lane, 2 * NB - 1);
+        const int8_t* const pq = aq + (size_t)m * K + (sq % NB) * QK + 16 * (sq / NB);
+        const int16_t* const pb = abs_ + (size_t)m * NB * 16 + 8 * sb;
+        const float* const pd = ad + (size_t)m * NB + 4 * min(lane, NB / 4 - 1);
+        const void* src = j < kQ ? (const void*)pq : j < kQ + kBs ? (const void*)pb : (const void*)pd;
+        const int off = j < kQ ? 1024 * j
+                      : j < kQ + kBs ? wave_bs_off(NB) + 1024 * (j - kQ) : wave_d_off(NB);
+        copy16_to_lds(src, lds_addr(act_q(m)) + (uint32_t)off);
       }
     }
   }
 
-  // every copy of the wave's range (the last ones may pass it: they read the next wave's rows,
-  // or stop at the matrix's last 16-byte word, and land in this wave's stage)
   // Row set s (rows R s .. R s + R - 1): the workgroup's waves take sets (tile * waves + wave),
-  // then every n_wg * waves further, each set's copies issued as soon as the previous set's bytes
-  // are in registers.
+  // then every n_wg * waves further, each set's copies issued once the previous set is computed.
+  // Every copy of a set's range is issued (the last ones may pass it: they read the next set's
+  // rows, or stop at the matrix's last 16-byte word, and land in this wave's stage).
   const bool has_rows = wave < waves;
   const int n_sets = (N + R - 1) / R, set_stride = n_wg * waves;
   int set = xcd_tile(wg, n_wg) * waves + wave;
   const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
-  const uint32_t lds_w = lds_addr(wreg);
+  const uint32_t lds_w = lds_addr(wreg), lane16 = 16u * (uint32_t)lane;
+  // a wave-uniform base and 32-bit lane offsets clamped to the matrix's last 16-byte word (one
+  // VGPR for every copy's address)
   const auto issue = [&](int s) {
-    const uint8_t* src = w + (size_t)min(s * R, N - 1) * row_bytes;
+    const uintptr_t src = (uintptr_t)w + (uintptr_t)min(s * R, N - 1) * (uintptr_t)row_bytes;
+    const uint64_t span = (uint64_t)(last - src);
+    const uint32_t lim = span > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)span;
 #pragma unroll
     for (int c = 0; c < kCopies; ++c)
-      copy16_to_lds_nt((const void*)min((uintptr_t)src + (uintptr_t)c * 1024 + (uintptr_t)lane * 16, last),
-                       lds_w + c * 1024);
+      copy16_to_lds_s_nt((const void*)src, min(lane16 + (uint32_t)(c * 1024), lim), lds_w + c * 1024);
   };
   if (has_rows) issue(set);
 
@@ -158,12 +168,12 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
     wait_vmcnt(has_rows ? kCopies : 0);  // the activation copies, issued first, have landed
     if constexpr (FUSEQ) {
       const int p = lane & 15;
-      for (int r = wave; r < kRounds; r += nq) {
-        const int g = 4 * r + (lane >> 4);
+      for (int r = wave; r < kRounds * M; r += nq) {
+        const int m = r / kRounds, g = 4 * (r % kRounds) + (lane >> 4);
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float4 f = *(const float4*)(xs + g * QK + 16 * p + 4 * q);
+          const float4 f = *(const float4*)(xs + m * K + g * QK + 16 * p + 4 * q);
           v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
         }
         // the steps of q8k_part16, piece p of block g going to 16 (p NB + g)
@@ -187,9 +197,9 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
                       ((uint32_t)(qv[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * i + 3] & 0xFF) << 24);
           bsum += qv[4 * i] + qv[4 * i + 1] + qv[4 * i + 2] + qv[4 * i + 3];
         }
-        *(uint4*)(act_q + (p * NB + g) * 16) = uint4{packed[0], packed[1], packed[2], packed[3]};
-        act_bs[g * 16 + p] = (int16_t)bsum;
-        if (p == 0) act_d[g] = amax / 127.0f;
+        *(uint4*)(act_q(m) + (p * NB + g) * 16) = uint4{packed[0], packed[1], packed[2], packed[3]};
+        act_bs(m)[g * 16 + p] = (int16_t)bsum;
+        if (p == 0) act_d(m)[g] = amax / 127.0f;
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
     }
@@ -205,67 +215,77 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   const bool gave_up = spin >= kWaveSpinLimit;
 
   const int b = lane % NB;
-  ActPieces ap;
-  ap.q = (const int8_t*)(act_q + b * 16);
-  ap.stride = NB * 16;
-  ap.bsums = act_bs + b * 16;
-  ActRegs areg;
-  if constexpr (ACTREG) {
+  ActPieces ap[MAXM];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) areg.q[i] = ap.q16(16 * i);
-    areg.bs[0] = ap.bs8(0);
-    areg.bs[1] = ap.bs8(1);
+  for (int m = 0; m < MAXM; ++m) {
+    ap[m].q = (const int8_t*)(act_q(m) + b * 16);
+    ap[m].stride = NB * 16;
+    ap[m].bsums = act_bs(m) + b * 16;
   }
+  // fold lanes: lane l folds row l % R of the set against activation row l / R
+  const int fr = lane % R, fm = lane / R;
   for (;;) {
     const int n0 = set * R;
     const int nrows = max(0, min(R, N - n0));
     const int jl = min(lane, max(nrows, 1) * NB - 1);  // lanes past the range redo its last block
+    // the lane's activation block into registers while the set's copies land (again for every
+    // set: held across sets, they crowd the compute into scratch)
+    ActRegs areg;
+    if constexpr (ACTREG) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) areg.q[i] = ap[0].q16(16 * i);
+      areg.bs[0] = ap[0].bs8(0);
+      areg.bs[1] = ap[0].bs8(1);
+    }
     wait_vmcnt(0);
-    float V[1], D;
+    float V[MAXM], D;
     if constexpr (ACTREG)
       L::template compute<1, ActRegs>(wreg, jl * L::kBytes, &areg, 1, V, D);
     else
-      L::template compute<1, ActPieces>(wreg, jl * L::kBytes, &ap, 1, V, D);
+      L::template compute<MAXM, ActPieces>(wreg, jl * L::kBytes, ap, M, V, D);
     const int next = set + set_stride;
-    if (next < n_sets) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage's reads have returned
-      issue(next);
-    }
-    Vbuf[lane] = V[0];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m)
+      if (m < M) Vbuf[64 * m + lane] = V[m];
     if (L::kHasD) Dbuf[lane] = D;
     __builtin_amdgcn_wave_barrier();
-    if (lane < nrows) {
+    if (fm < M && fr < nrows) {
       // blocks whose operands are read before they are folded (a divisor of NB)
       constexpr int kC = NB < 16 ? NB : NB % 16 == 0 ? 16 : 8;
       static_assert(NB % kC == 0, "fold chunks cover the row exactly");
+      const float* xd = act_d(fm);
       float acc = 0.0f;
 #pragma unroll
       for (int bb = 0; bb < NB; bb += kC) {
         float vv[kC], xx[kC], dd[kC];
 #pragma unroll
         for (int i = 0; i < kC; ++i) {
-          vv[i] = Vbuf[lane * NB + bb + i];
-          xx[i] = act_d[bb + i];
-          dd[i] = L::kHasD ? Dbuf[lane * NB + bb + i] : 0.0f;
+          vv[i] = Vbuf[64 * fm + fr * NB + bb + i];
+          xx[i] = xd[bb + i];
+          dd[i] = L::kHasD ? Dbuf[fr * NB + bb + i] : 0.0f;
         }
 #pragma unroll
         for (int i = 0; i < kC; ++i) acc = L::fold(acc, xx[i], vv[i], dd[i]);
       }
-      y[n0 + lane] = gave_up ? __builtin_nanf("") : acc;
+      y[(size_t)fm * ldy + n0 + fr] = gave_up ? __builtin_nanf("") : acc;
     }
     if (next >= n_sets) break;
-    set = next;
+    // the next set into the stage once this one's reads have returned (issued after the fold:
+    // issued between compute and fold, its addresses crowd the compute into scratch)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();  // every lane's fold has read Vbuf before it is rewritten
+    issue(next);
+    set = next;
   }
 }
 
-template <int TYPE, int NB, bool FUSEQ, bool ACTREG>
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM>
 __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int N,
-    int row_bytes, uint32_t pack, const int8_t* __restrict__ aq, const float* __restrict__ ad,
-    const int16_t* __restrict__ abs_) {
-  wave_rows<TYPE, NB, FUSEQ, ACTREG>(w, x, y, N, row_bytes, pack & 0xFF, pack >> 8, aq, ad, abs_,
-                                     blockIdx.x, gridDim.x);
+    int row_bytes, uint32_t pack, int ldy, const int8_t* __restrict__ aq,
+    const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
+  wave_rows<TYPE, NB, FUSEQ, ACTREG, MAXM>(w, x, y, N, row_bytes, pack & 0xFF, (pack >> 8) & 0xFF,
+                                           pack >> 16, ldy, aq, ad, abs_, blockIdx.x, gridDim.x);
 }
 
 // Several weights that share the activation row (q|k|v, gate|up), one launch: each weight's
@@ -293,21 +313,23 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
   const WaveSeg& g = segs.s[si];
   const int wg = (int)blockIdx.x - g.wg0;
   if (g.type == T_Q4_K)
-    wave_rows<T_Q4_K, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, aq, ad, abs_, wg, g.n_wg);
+    wave_rows<T_Q4_K, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
   else if (g.type == T_Q8_0)
-    wave_rows<T_Q8_0, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, aq, ad, abs_, wg, g.n_wg);
+    wave_rows<T_Q8_0, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
   else
-    wave_rows<T_Q6_K, NB, FUSEQ, false>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, aq, ad, abs_, wg, g.n_wg);
+    wave_rows<T_Q6_K, NB, FUSEQ, false>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
 }
 
-template <int TYPE, int NB, bool FUSEQ>
-int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
-                  hipStream_t stream) {
-  constexpr bool kReg = TYPE != T_Q6_K;  // Q6_K's compute leaves no room for them
+template <int TYPE, int NB, bool FUSEQ, int MAXM>
+int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+                  int M, int N, hipStream_t stream) {
+  constexpr bool kReg = TYPE != T_Q6_K && MAXM == 1;  // Q6_K's compute leaves no room for them
   constexpr int R = 64 / NB;
   const int ncu = cu_count();
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
-  const int fit = (kWaveLds - wave_act_bytes(NB, FUSEQ)) / wave_region_bytes<TYPE, NB>();
+  const int act_lds = wave_act_bytes(NB, FUSEQ, M);
+  const int region = wave_region_bytes<TYPE, NB, MAXM>();
+  const int fit = (kWaveLds - act_lds) / region;
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
   // More rows than one round of workgroups holds (measured on MI355X against the pipelined
   // kernel and each other). Q4_K: one workgroup per CU whose waves take further row sets as their
@@ -320,7 +342,7 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   // 4096 x 14336 13.3 vs 11.2 us pipelined), Q6_K in one round (Q4_K 4096 x 14336 8.86 vs 11.9
   // us, Q6_K 2048 x 14336 8.2 vs 10.9 us; Q6_K 4096 x 14336 in two rounds 16.5 vs 15.8 us).
   if constexpr (NB == 56 && FUSEQ) return -1;
-  if (waves < 1) return -1;
+  if (waves < 1 || ldy > 0x7FFFFFFF) return -1;
   int grid = (N + waves * R - 1) / (waves * R);
   if constexpr (TYPE == T_Q4_K && NB != 64) {
     constexpr int kSets = 4;  // row sets per wave at most
@@ -332,33 +354,49 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   }
   // stagers: a round of four blocks each, in waves of their own when the workgroup has fewer
   // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)
-  const int nq = min(kWaveMaxWaves, NB / 4);
+  const int nq = min(kWaveMaxWaves, M * NB / 4);
   const int nw = max(waves, nq);
-  const int lds = wave_act_bytes(NB, FUSEQ) + waves * wave_region_bytes<TYPE, NB>();  // row waves only
-  auto kern = gemv_wave_kernel<TYPE, NB, FUSEQ, kReg>;
+  const int lds = act_lds + waves * region;  // row waves only
+  auto kern = gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM>;
   allow_lds((const void*)kern, kWaveLds);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N,
-                     (int)row_bytes, (uint32_t)waves | (uint32_t)nq << 8, act.q, act.d, act.bsums);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N, (int)row_bytes,
+                     (uint32_t)waves | (uint32_t)nq << 8 | (uint32_t)M << 16, (int)ldy, act.q,
+                     act.d, act.bsums);
   return 0;
 }
 
+template <int TYPE, int NB, int MAXM>
+int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+                  int M, int N, hipStream_t stream) {
+  return act.q == nullptr
+             ? launch_wave_t<TYPE, NB, true, MAXM>(w, row_bytes, act, y, ldy, M, N, stream)
+             : launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream);
+}
+
+// One activation row: every nb the kernel is built for. Two rows: 8-, 16- and 32-block rows
+// (measured on MI355X against the pipelined kernel: Q4_K 4096 x 4096 4.8 vs 6.5 us, 28672 x 4096
+// 15.9 vs 19.3, 14336 x 4096 10.7 vs 10.7; Q6_K 4096 x 4096 6.3 vs 7.9; Q8_0 6.4 vs 7.4). Three
+// and four rows measured mixed (Q4_K 14336 x 4096 at three rows 12.9 vs 12.1 us, Q8_0 4096 x 4096
+// at four 14.3 vs 9.0) and stay on the pipelined kernel.
 template <int TYPE, int NB>
-int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
-                   hipStream_t stream) {
-  return act.q == nullptr ? launch_wave_t<TYPE, NB, true>(w, row_bytes, act, y, N, stream)
-                          : launch_wave_t<TYPE, NB, false>(w, row_bytes, act, y, N, stream);
+int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+                   int M, int N, hipStream_t stream) {
+  if (M == 1) return launch_wave_m<TYPE, NB, 1>(w, row_bytes, act, y, ldy, M, N, stream);
+  if constexpr (NB == 8 || NB == 16 || NB == 32)
+    if (M == 2) return launch_wave_m<TYPE, NB, 2>(w, row_bytes, act, y, ldy, M, N, stream);
+  return -1;
 }
 
 template <int TYPE>
-int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
-                     hipStream_t stream) {
+int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                     long long ldy, int M, int N, hipStream_t stream) {
   switch (act.nb) {
-    case 4: return launch_wave_nb<TYPE, 4>(w, row_bytes, act, y, N, stream);
-    case 8: return launch_wave_nb<TYPE, 8>(w, row_bytes, act, y, N, stream);
-    case 16: return launch_wave_nb<TYPE, 16>(w, row_bytes, act, y, N, stream);
-    case 32: return launch_wave_nb<TYPE, 32>(w, row_bytes, act, y, N, stream);
-    case 56: return launch_wave_nb<TYPE, 56>(w, row_bytes, act, y, N, stream);
-    case 64: return launch_wave_nb<TYPE, 64>(w, row_bytes, act, y, N, stream);
+    case 4: return launch_wave_nb<TYPE, 4>(w, row_bytes, act, y, ldy, M, N, stream);
+    case 8: return launch_wave_nb<TYPE, 8>(w, row_bytes, act, y, ldy, M, N, stream);
+    case 16: return launch_wave_nb<TYPE, 16>(w, row_bytes, act, y, ldy, M, N, stream);
+    case 32: return launch_wave_nb<TYPE, 32>(w, row_bytes, act, y, ldy, M, N, stream);
+    case 56: return launch_wave_nb<TYPE, 56>(w, row_bytes, act, y, ldy, M, N, stream);
+    case 64: return launch_wave_nb<TYPE, 64>(w, row_bytes, act, y, ldy, M, N, stream);
     default: return -1;
   }
 }
@@ -417,9 +455,9 @@ int launch_wave_multi_nb(const DecodeSeg* seg, int count, const Act& act, hipStr
 
 }  // namespace
 
-int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
-                     int n_rows, hipStream_t stream) {
-  if (n_rows < 1) return -1;
+int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                       long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+  if (n_rows < 1 || m_rows < 1 || m_rows > 4) return -1;
   if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF) return -1;
   // activations move in 16-byte pieces: fp32 x, or the Q8_K parts (q rows and bsums are 16-byte
   // multiples, d is 256-byte aligned in the workspace layout)
@@ -427,11 +465,16 @@ int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act&
                        : (((uintptr_t)act.q | (uintptr_t)act.bsums | (uintptr_t)act.d) & 15) != 0)
     return -1;
   switch (type) {
-    case T_Q4_K: return launch_wave_type<T_Q4_K>(w, row_bytes, act, y, n_rows, stream);
-    case T_Q8_0: return launch_wave_type<T_Q8_0>(w, row_bytes, act, y, n_rows, stream);
-    case T_Q6_K: return launch_wave_type<T_Q6_K>(w, row_bytes, act, y, n_rows, stream);
+    case T_Q4_K: return launch_wave_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q8_0: return launch_wave_type<T_Q8_0>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q6_K: return launch_wave_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }
+}
+
+int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                     int n_rows, hipStream_t stream) {
+  return launch_gemv_wave_m(type, w, row_bytes, act, y, n_rows, 1, n_rows, stream);
 }
 
 int launch_gemv_wave_multi(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream) {

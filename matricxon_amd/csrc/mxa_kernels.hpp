@@ -130,11 +130,14 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
 int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float* x, int k,
                     float* y, long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
-// Decode GEMV for one activation row in the read floor's shape (mxa_gemv_wave.hip): one
-// workgroup per CU, every weight byte requested at once, lane-per-block compute as each wave's
-// rows land. y[n] for n < n_rows; quantizes act.x to Q8_K in the kernel when act.q == nullptr.
-// Q4_K / Q8_0 / Q6_K with 64 % (K / 256) == 0, 16-byte aligned rows, and at most one round of
-// rows per CU; -1 otherwise.
+// Decode GEMV in the read floor's shape (mxa_gemv_wave.hip): one workgroup per CU, every weight
+// byte requested at once, lane-per-block compute as each wave's rows land. y[m * ldy + n] for
+// m < m_rows <= 2, n < n_rows; quantizes act.x to Q8_K in the kernel when act.q == nullptr.
+// Q4_K / Q8_0 / Q6_K with K / 256 in {4, 8, 16, 32, 64} (56 on workspace Q8_K; {8, 16, 32} for
+// two rows), 16-byte aligned rows, and the rows per CU the type allows; -1 otherwise.
+int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                       long long ldy, int m_rows, int n_rows, hipStream_t stream);
+// The same for one activation row.
 int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                      int n_rows, hipStream_t stream);
 

@@ -96,3 +96,28 @@ def test_one_row_wave_kernel_repeated_calls_share_nothing(gpu, oracle) -> None:
     outs = [gpu.matmul(D.Q4_K, wd, dev(x), n, k) for x in xs]
     for x, y in zip(xs, outs):
         assert_bit_exact(host(y), oracle.gemm(D.Q4_K, w, x, n, k))
+
+
+def run_rows(gpu, oracle, t, n, k, m, seed):
+    w = S.packed_weight(t, n, k, seed=seed)
+    x = S.activations(m, k, seed=seed + 1)
+    want = oracle.gemm(t, w, x, n, k)
+    wd, xd = dev(w), dev(x)
+    assert_bit_exact(host(gpu.matmul(t, wd, xd, n, k)), want)  # x quantized in the kernel
+    ws = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device="cuda")
+    gpu.quantize_into(xd, ws)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    assert_bit_exact(host(gpu.matmul_q8k(t, wd, ws, None, out, m, n, k)), want)  # Q8_K given
+
+
+# Two activation rows (8-, 16- and 32-block rows; three and four rows run the pipelined kernel
+# and are checked here too): every row's block values from one read of the weight, the last wave
+# partial, Q4_K past one pass (row sets), Q6_K and Q8_0 rows.
+ROWS_CASES = [(D.Q4_K, 14336, 4096), (D.Q4_K, 1001, 2048), (D.Q6_K, 4100, 4096),
+              (D.Q8_0, 3000, 8192), (D.Q4_K, 28672, 4096), (D.Q4_K, 5000, 8192)]
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("ggml_type,n,k", ROWS_CASES)
+def test_decode_two_to_four_rows(gpu, oracle, ggml_type, n, k, m) -> None:
+    run_rows(gpu, oracle, ggml_type, n, k, m, seed=n + k + m)
