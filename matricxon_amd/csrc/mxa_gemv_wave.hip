@@ -84,7 +84,7 @@ constexpr int kWaveSpinLimit = 1 << 22;
 // waves; one that owns no rows only stages).
 // The workgroup's work: workgroup wg of n_wg over the N rows of one weight, for M <= MAXM
 // activation rows (y row m at y + m ldy).
-template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM = 1>
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM = 1, bool LOOP = false>
 __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                           float* __restrict__ y, int N, int row_bytes, int waves,
                                           int nq, int M, int ldy, const int8_t* __restrict__ aq,
@@ -94,6 +94,7 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   static_assert(!ACTREG || MAXM == 1, "activations in registers for one row only");
   constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
   constexpr int R = 64 / NB, kRounds = NB / 4, kRowAct = wave_row_act(NB), K = NB * QK;
+  if constexpr (MAXM == 1) M = 1;  // constant LDS offsets for the one-row kernel
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -152,15 +153,23 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   int set = xcd_tile(wg, n_wg) * waves + wave;
   const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
   const uint32_t lds_w = lds_addr(wreg), lane16 = 16u * (uint32_t)lane;
-  // a wave-uniform base and 32-bit lane offsets clamped to the matrix's last 16-byte word (one
-  // VGPR for every copy's address)
+  // Copies clamped to the matrix's last 16-byte word. With the set loop: a wave-uniform base and
+  // 32-bit lane offsets (one VGPR for every copy's address, which keeps the loop out of scratch);
+  // in one pass, 64-bit lane addresses (measured 0.5-2% faster there).
   const auto issue = [&](int s) {
     const uintptr_t src = (uintptr_t)w + (uintptr_t)min(s * R, N - 1) * (uintptr_t)row_bytes;
-    const uint64_t span = (uint64_t)(last - src);
-    const uint32_t lim = span > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)span;
+    if constexpr (LOOP) {
+      const uint64_t span = (uint64_t)(last - src);
+      const uint32_t lim = span > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)span;
 #pragma unroll
-    for (int c = 0; c < kCopies; ++c)
-      copy16_to_lds_s_nt((const void*)src, min(lane16 + (uint32_t)(c * 1024), lim), lds_w + c * 1024);
+      for (int c = 0; c < kCopies; ++c)
+        copy16_to_lds_s_nt((const void*)src, min(lane16 + (uint32_t)(c * 1024), lim), lds_w + c * 1024);
+    } else {
+#pragma unroll
+      for (int c = 0; c < kCopies; ++c)
+        copy16_to_lds_nt((const void*)min(src + (uintptr_t)c * 1024 + (uintptr_t)lane16, last),
+                         lds_w + c * 1024);
+    }
   };
   if (has_rows) issue(set);
 
@@ -269,7 +278,7 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
       }
       y[(size_t)fm * ldy + n0 + fr] = gave_up ? __builtin_nanf("") : acc;
     }
-    if (next >= n_sets) break;
+    if (!LOOP || next >= n_sets) break;
     // the next set into the stage once this one's reads have returned (issued after the fold:
     // issued between compute and fold, its addresses crowd the compute into scratch)
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -279,12 +288,13 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   }
 }
 
-template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM>
+// LOOP: waves may take more than one row set (a single pass compiles without the set loop)
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM, bool LOOP>
 __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int N,
     int row_bytes, uint32_t pack, int ldy, const int8_t* __restrict__ aq,
     const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
-  wave_rows<TYPE, NB, FUSEQ, ACTREG, MAXM>(w, x, y, N, row_bytes, pack & 0xFF, (pack >> 8) & 0xFF,
+  wave_rows<TYPE, NB, FUSEQ, ACTREG, MAXM, LOOP>(w, x, y, N, row_bytes, pack & 0xFF, (pack >> 8) & 0xFF,
                                            pack >> 16, ldy, aq, ad, abs_, blockIdx.x, gridDim.x);
 }
 
@@ -357,7 +367,10 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   const int nq = min(kWaveMaxWaves, M * NB / 4);
   const int nw = max(waves, nq);
   const int lds = act_lds + waves * region;  // row waves only
-  auto kern = gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM>;
+  constexpr bool kLoopable = TYPE == T_Q4_K && NB != 64;
+  auto kern = kLoopable && (long long)grid * waves * R < N
+                  ? gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, kLoopable>
+                  : gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, false>;
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N, (int)row_bytes,
                      (uint32_t)waves | (uint32_t)nq << 8 | (uint32_t)M << 16, (int)ldy, act.q,
