@@ -1,7 +1,7 @@
 // Decode GEMV for one activation row in the shape of the read floor: one workgroup per CU whose
 // waves request every byte of their rows at their first instructions, then compute each row set
 // as it lands. y[n] = sum_k x[k] * W[n, k] for K-quant / Q8_0 weights with nb = K / 256 in
-// {4, 8, 16, 32, 64}, and 56 on Q8_K activations from the workspace.
+// {4, 8, 16, 32, 56, 64} (56 with x quantized in the kernel: Q4_K only).
 //
 // Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, or one row of 56
 // with eight lanes idle; one byte range, 16-byte aligned because row_bytes is) and issues all of
@@ -10,9 +10,8 @@
 // takes them in as its memory pipeline drains (it accepts ~64 KB in flight, so half the waves sit
 // in their issue loop for microseconds); the whole matrix is in flight from the start and lands
 // in the order HBM returns it. A wave waits only for its own copies (vmcnt), never for another
-// wave's. With more rows than the CUs' waves hold, a Q4_K wave takes further row sets, each
-// requested as soon as the previous one's bytes are in registers; other types run later rounds
-// of workgroups.
+// wave's. With more rows than the CUs' waves hold, a wave takes further row sets, each requested
+// once the previous one is computed.
 //
 // Activations. The first waves (stagers) also bring the activations into LDS with LDS-DMA copies
 // issued before their weight copies: fp32 x, which they then quantize to Q8_K (16 lanes per
@@ -341,36 +340,27 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   const int region = wave_region_bytes<TYPE, NB, MAXM>();
   const int fit = (kWaveLds - act_lds) / region;
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
-  // More rows than one round of workgroups holds (measured on MI355X against the pipelined
-  // kernel and each other). Q4_K: one workgroup per CU whose waves take further row sets as their
-  // previous set's bytes reach registers (28672 x 4096: 14.9 us, vs 15.7 in rounds of workgroups
-  // and 17.1 pipelined; 57344 x 4096: 25.6 vs 29.2 and 27.2). Q8_0: rounds of workgroups, later
-  // ones starting as earlier ones finish (row sets per wave measured 6% slower). Q6_K: one round
-  // only (fewer waves fit; the 128256 x 4096 head in rounds 93.9 vs 80.5 us, in row sets 168 us),
-  // and for 64-block rows (one row per wave). 56-block rows (K = 14336) take the Q8_K blocks
-  // from the workspace only (the 56 KB of staged fp32 x leave room for too few weight waves: Q4_K
-  // 4096 x 14336 13.3 vs 11.2 us pipelined), Q6_K in one round (Q4_K 4096 x 14336 8.86 vs 11.9
-  // us, Q6_K 2048 x 14336 8.2 vs 10.9 us; Q6_K 4096 x 14336 in two rounds 16.5 vs 15.8 us).
-  if constexpr (NB == 56 && FUSEQ) return -1;
+  // More rows than one round of workgroups holds: one workgroup per CU whose waves take further
+  // row sets, each requested once the previous set is computed (measured on MI355X against the
+  // pipelined kernel and against rounds of workgroups: Q4_K 28672 x 4096 14.8 vs 17.1 and 15.7
+  // us, 128256 x 4096 47.3 vs 52.9 us pipelined; Q6_K 14336 x 4096 12.2 vs 13.7, the 128256 x 4096
+  // head 74.4 vs 77.2, 8192 x 16384 27.9 vs 29.4; Q8_0 14336 x 4096 11.3 vs 13.1). 56-block rows
+  // (K = 14336) with fp32 x staged in the kernel leave room for few weight waves (56 KB of x):
+  // Q4_K only (4096 x 14336 10.4 vs 11.3 us; Q6_K 15.5 vs 15.6, Q8_0 16.1 vs 15.7 stay
+  // pipelined); on workspace Q8_K all three (Q4_K 8.9 vs 11.9, Q6_K 14.6 vs 15.8, Q8_0 14.2 vs
+  // 15.5 us).
+  if constexpr (NB == 56 && FUSEQ && TYPE != T_Q4_K) return -1;
   if (waves < 1 || ldy > 0x7FFFFFFF) return -1;
-  int grid = (N + waves * R - 1) / (waves * R);
-  if constexpr (TYPE == T_Q4_K && NB != 64) {
-    constexpr int kSets = 4;  // row sets per wave at most
-    grid = min(grid, ncu);
-    if ((long long)waves * R * grid * kSets < N) return -1;
-  } else {
-    constexpr int kWgRounds = (TYPE == T_Q6_K || (NB > 32 && NB != 56)) ? 1 : 4;
-    if ((long long)waves * R * ncu * kWgRounds < N) return -1;
-  }
+  constexpr int kSets = 64;  // row sets per wave at most
+  const int grid = min((N + waves * R - 1) / (waves * R), ncu);
+  if ((long long)waves * R * grid * kSets < N) return -1;
   // stagers: a round of four blocks each, in waves of their own when the workgroup has fewer
   // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)
   const int nq = min(kWaveMaxWaves, M * NB / 4);
   const int nw = max(waves, nq);
   const int lds = act_lds + waves * region;  // row waves only
-  constexpr bool kLoopable = TYPE == T_Q4_K && NB != 64;
-  auto kern = kLoopable && (long long)grid * waves * R < N
-                  ? gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, kLoopable>
-                  : gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, false>;
+  auto kern = (long long)grid * waves * R < N ? gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, true>
+                                              : gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, false>;
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N, (int)row_bytes,
                      (uint32_t)waves | (uint32_t)nq << 8 | (uint32_t)M << 16, (int)ldy, act.q,

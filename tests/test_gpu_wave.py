@@ -1,15 +1,14 @@
 """GPU parity of the one-row decode kernel in the read floor's shape (mxa_gemv_wave.hip) against
 the CPU oracle, through the C ABI: bit-exact for Q8_0 / Q4_K / Q6_K.
 
-The kernel takes every one-token K-quant / Q8_0 call whose blocks per row nb = K / 256 divide 64
-(or nb = 56 on Q8_K blocks from the workspace) and whose rows fit one round of its workgroups
-(one per CU); past that, Q4_K waves take up to four row sets each and Q8_0 runs up to four rounds
-of workgroups (nb <= 32 or nb = 56). A wave owns
-64 / nb rows (one row of 56 blocks at nb = 56, eight lanes idle); the shapes cover each nb it is
-built for (4, 8, 16, 32, 56, 64), N that leaves the last wave or workgroup partial, N so small
-that some workgroups' waves only stage the activations, N at the largest one round holds on a
-256-CU MI355X (14 Q4_K waves of 4 rows, 8 Q8_0, 9 Q6_K per CU) and one row past it, several
-rounds, with x quantized in the kernel and with Q8_K blocks from the workspace.
+The kernel takes every one-token K-quant / Q8_0 call whose blocks per row nb = K / 256 are in
+{4, 8, 16, 32, 56, 64} (56 with x quantized in the kernel: Q4_K only), one workgroup per CU;
+past one pass its waves take up to 64 row sets each. A wave owns 64 / nb rows (one row of 56
+blocks at nb = 56, eight lanes idle); the shapes cover each nb it is built for, N that leaves the
+last wave or workgroup partial, N so small that some workgroups' waves only stage the
+activations, N at the largest one pass holds on a 256-CU MI355X (14 Q4_K waves of 4 rows, 8
+Q8_0, 9 Q6_K per CU) and one row past it, several row sets, with x quantized in the kernel and
+with Q8_K blocks from the workspace.
 """
 
 import numpy as np
@@ -73,12 +72,12 @@ def test_one_row_wave_kernel_round_edge(gpu, oracle, ggml_type, extra) -> None:
     run_both(gpu, oracle, ggml_type, ROUND_EDGE[ggml_type] + extra, 4096, seed=7 + extra)
 
 
-# More rows than one round of workgroups holds (Q4_K: up to four row sets per wave; Q8_0: up to
-# four rounds, later workgroups starting as earlier ones finish), and one row past four (another
-# kernel).
+# More rows than one pass of the CUs' waves holds: several row sets per wave, for every type and
+# row length (the Q6_K vocabulary head included).
 ROUNDS_CASES = [(D.Q4_K, 28672, 4096), (D.Q8_0, 14336, 4096), (D.Q4_K, 14336, 8192),
                 (D.Q4_K, 57344, 4096), (D.Q4_K, 57345, 4096), (D.Q4_K, 14336, 14336),
-                (D.Q8_0, 4097, 14336)]
+                (D.Q8_0, 4097, 14336), (D.Q6_K, 14336, 4096), (D.Q6_K, 4096, 14336),
+                (D.Q6_K, 8192, 16384), (D.Q6_K, 128256, 4096), (D.Q4_K, 4096, 14336)]
 
 
 @pytest.mark.parametrize("ggml_type,n,k", ROUNDS_CASES)
