@@ -136,6 +136,21 @@ int mxa_gemm_moe(int ggml_type, const void *w, long long expert_stride, int n_ex
                  float *y, int out_features, int in_features, void *workspace,
                  size_t workspace_bytes, void *stream);
 
+/* One token's routed experts (MoE decode), one launch: pair p of n_pairs multiplies expert
+ * ids[p] (a DEVICE int32 array; ids outside [0, n_experts) are clamped) at w + ids[p] *
+ * expert_stride (out_features x row bytes) by activation row p of x (x_rows == n_pairs) or by the
+ * one row they share (x_rows == 1), writing row p of y (n_pairs, out_features). x == NULL:
+ * `workspace` already holds the Q8_K activations of the x_rows rows; else x is quantized in the
+ * kernel, or first into `workspace` (mxa_quantize_q8_k's layout for x_rows rows) for shapes that
+ * need it. Each row equals mxa_gemm of that row alone bit for bit. Q4_K, Q6_K, Q8_0 with
+ * in_features / 256 in {4, 8, 16, 32, 56, 64}, 16-byte aligned rows and expert_stride; -1 for
+ * other shapes (the caller uses mxa_gemm_moe). Replaces the per-expert calls of
+ * `QuantizedMoEExperts.forward` for one token (app/architectures/moe_experts.py:81-88). */
+int mxa_gemm_moe_pairs(int ggml_type, const void *w, long long expert_stride, int n_experts,
+                       const int32_t *ids, int n_pairs, const float *x, int x_rows, float *y,
+                       int out_features, int in_features, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
 /* Up to 4 packed weights sharing one input (q/k/v, gate/up): one activation quantization, then
  * each weight's output columns written after the previous weight's, y (n_tokens, sum outs).
  * `types`, `ws` (device pointers) and `outs` are HOST arrays of n entries.

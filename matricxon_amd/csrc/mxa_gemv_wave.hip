@@ -329,6 +329,26 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
     wave_rows<T_Q6_K, NB, FUSEQ, false>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
 }
 
+// One token's routed experts (MoE decode): pair p multiplies expert ids[p] (a device array; an id
+// outside [0, n_experts) is clamped, so a bad routing reads a valid expert, never past the
+// weights) by activation row p * x_step (0: every pair shares the token's row). G workgroups per
+// pair run the single-weight form.
+template <int TYPE, int NB, bool FUSEQ, bool ACTREG, bool LOOP>
+__global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_pairs_kernel(
+    const uint8_t* __restrict__ w, long long expert_stride, const int32_t* __restrict__ ids,
+    int n_experts, const float* __restrict__ x, int x_step, float* __restrict__ y, int N,
+    int row_bytes, uint32_t pack, int G, const int8_t* __restrict__ aq,
+    const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
+  constexpr int K = NB * QK;
+  const int p = (int)blockIdx.x / G, wg = (int)blockIdx.x - p * G;
+  const int e = min(max(ids[p], 0), n_experts - 1);
+  const size_t r = (size_t)p * x_step;  // the pair's activation row
+  wave_rows<TYPE, NB, FUSEQ, ACTREG, 1, LOOP>(
+      w + (size_t)e * expert_stride, FUSEQ ? x + r * K : x, y + (size_t)p * N, N, row_bytes,
+      pack & 0xFF, (pack >> 8) & 0xFF, 1, 0, FUSEQ ? aq : aq + r * K, FUSEQ ? ad : ad + r * NB,
+      FUSEQ ? abs_ : abs_ + r * NB * 16, wg, G);
+}
+
 template <int TYPE, int NB, bool FUSEQ, int MAXM>
 int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                   int M, int N, hipStream_t stream) {
@@ -456,6 +476,66 @@ int launch_wave_multi_nb(const DecodeSeg* seg, int count, const Act& act, hipStr
                           : launch_wave_multi_t<NB, false>(seg, count, act, stream);
 }
 
+// n_pairs experts' weights of one token at once: the pairs share the CUs, G workgroups each.
+template <int TYPE, int NB, bool FUSEQ>
+int launch_pairs_t(const uint8_t* w, long long row_bytes, long long expert_stride,
+                   const int32_t* ids, int n_experts, int n_pairs, int x_step, const Act& act,
+                   float* y, int N, hipStream_t stream) {
+  constexpr bool kReg = TYPE != T_Q6_K;
+  constexpr int R = 64 / NB;
+  if constexpr (NB == 56 && FUSEQ && TYPE != T_Q4_K) return -1;
+  const int ncu = cu_count();
+  const int act_lds = wave_act_bytes(NB, FUSEQ, 1);
+  const int region = wave_region_bytes<TYPE, NB, 1>();
+  const int fit = (kWaveLds - act_lds) / region;
+  const long long total = (long long)n_pairs * N;
+  const int per_cu = (int)((total + ncu - 1) / ncu);
+  const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
+  if (waves < 1) return -1;
+  const int G = min((N + waves * R - 1) / (waves * R), max(1, ncu / n_pairs));
+  constexpr int kSets = 64;
+  if ((long long)waves * R * G * kSets < N || (long long)G * n_pairs > 0x7FFFFFFF) return -1;
+  const int nq = min(kWaveMaxWaves, NB / 4);
+  const int nw = max(waves, nq);
+  const int lds = act_lds + waves * region;
+  auto kern = (long long)G * waves * R < N ? gemv_wave_pairs_kernel<TYPE, NB, FUSEQ, kReg, true>
+                                          : gemv_wave_pairs_kernel<TYPE, NB, FUSEQ, kReg, false>;
+  allow_lds((const void*)kern, kWaveLds);
+  hipLaunchKernelGGL(kern, dim3(G * n_pairs), dim3(64 * nw), lds, stream, w, expert_stride, ids,
+                     n_experts, act.x, x_step, y, N, (int)row_bytes,
+                     (uint32_t)waves | (uint32_t)nq << 8 | 1u << 16, G, act.q, act.d, act.bsums);
+  return 0;
+}
+
+template <int TYPE, int NB>
+int launch_pairs_nb(const uint8_t* w, long long row_bytes, long long expert_stride,
+                    const int32_t* ids, int n_experts, int n_pairs, int x_step, const Act& act,
+                    float* y, int N, hipStream_t stream) {
+  return act.q == nullptr
+             ? launch_pairs_t<TYPE, NB, true>(w, row_bytes, expert_stride, ids, n_experts, n_pairs,
+                                              x_step, act, y, N, stream)
+             : launch_pairs_t<TYPE, NB, false>(w, row_bytes, expert_stride, ids, n_experts, n_pairs,
+                                               x_step, act, y, N, stream);
+}
+
+template <int TYPE>
+int launch_pairs_type(const uint8_t* w, long long row_bytes, long long expert_stride,
+                      const int32_t* ids, int n_experts, int n_pairs, int x_step, const Act& act,
+                      float* y, int N, hipStream_t stream) {
+  switch (act.nb) {
+#define MXA_PAIRS_NB(nb) \
+  case nb: return launch_pairs_nb<TYPE, nb>(w, row_bytes, expert_stride, ids, n_experts, n_pairs, x_step, act, y, N, stream);
+    MXA_PAIRS_NB(4)
+    MXA_PAIRS_NB(8)
+    MXA_PAIRS_NB(16)
+    MXA_PAIRS_NB(32)
+    MXA_PAIRS_NB(56)
+    MXA_PAIRS_NB(64)
+#undef MXA_PAIRS_NB
+    default: return -1;
+  }
+}
+
 }  // namespace
 
 int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
@@ -497,6 +577,25 @@ int launch_gemv_wave_multi(const DecodeSeg* seg, int count, const Act& act, hipS
     case 8: return launch_wave_multi_nb<8>(seg, count, act, stream);
     case 16: return launch_wave_multi_nb<16>(seg, count, act, stream);
     case 32: return launch_wave_multi_nb<32>(seg, count, act, stream);
+    default: return -1;
+  }
+}
+
+int launch_gemv_wave_pairs(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                           const int32_t* ids, int n_experts, int n_pairs, int x_step,
+                           const Act& act, float* y, int n_rows, hipStream_t stream) {
+  if (n_rows < 1 || n_pairs < 1 || n_experts < 1 || ids == nullptr || (x_step != 0 && x_step != 1))
+    return -1;
+  if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF ||
+      expert_stride % 16 != 0 || expert_stride < (long long)n_rows * row_bytes)
+    return -1;
+  if (act.q == nullptr ? ((uintptr_t)act.x & 15) != 0
+                       : (((uintptr_t)act.q | (uintptr_t)act.bsums | (uintptr_t)act.d) & 15) != 0)
+    return -1;
+  switch (type) {
+    case T_Q4_K: return launch_pairs_type<T_Q4_K>(w, row_bytes, expert_stride, ids, n_experts, n_pairs, x_step, act, y, n_rows, stream);
+    case T_Q8_0: return launch_pairs_type<T_Q8_0>(w, row_bytes, expert_stride, ids, n_experts, n_pairs, x_step, act, y, n_rows, stream);
+    case T_Q6_K: return launch_pairs_type<T_Q6_K>(w, row_bytes, expert_stride, ids, n_experts, n_pairs, x_step, act, y, n_rows, stream);
     default: return -1;
   }
 }

@@ -157,6 +157,14 @@ struct DecodeSeg {
   int n;     // output rows of the weight
 };
 
+// One token's routed experts in the floor-shaped kernel: pair p of n_pairs writes y + p * n_rows
+// from expert ids[p] (device int32, clamped to [0, n_experts)) at w + ids[p] * expert_stride and
+// activation row p * x_step (x_step 0: one row shared by all pairs). -1 when the shape does not
+// suit it.
+int launch_gemv_wave_pairs(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                           const int32_t* ids, int n_experts, int n_pairs, int x_step,
+                           const Act& act, float* y, int n_rows, hipStream_t stream);
+
 // One-row decode over up to 4 Q4_K / Q6_K / Q8_0 weights sharing the activations, in the
 // floor-shaped kernel (mxa_gemv_wave.hip); -1 when the weights do not suit it.
 int launch_gemv_wave_multi(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream);

@@ -376,6 +376,43 @@ class HipGemm:
         self._calls += 1
         return out
 
+    def matmul_moe_pairs(self, ggml_type: int, experts: torch.Tensor, ids: torch.Tensor,
+                         x: torch.Tensor, out_features: int, in_features: int,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor | None:
+        """One token's routed experts in one launch (`mxa_gemm_moe_pairs`): row p of the result
+        (n_pairs, out_features) float32 is expert ids[p] of `experts` (n_experts, out_features,
+        row_bytes) times row p of `x` (n_pairs rows) or the single row of `x` (one row shared by
+        all pairs). `ids`: int32 on the device, so no host sync. None when the shape does not
+        suit the launch (the caller takes `matmul_moe`). Replaces the per-expert calls of
+        QuantizedMoEExperts.forward for one token (app/architectures/moe_experts.py:81-88)."""
+        ggml_type = int(ggml_type)
+        _require_device_tensor("experts", experts)
+        device = experts.device
+        rb = self.row_bytes(ggml_type, in_features)
+        if experts.dtype != torch.uint8 or experts.dim() != 3 or \
+                tuple(experts.shape[1:]) != (out_features, rb) or not experts.is_contiguous():
+            raise ValueError(f"experts must be contiguous uint8 (n_experts, {out_features}, {rb})")
+        n_pairs = ids.numel()
+        if ids.dtype != torch.int32 or ids.device != device or not ids.is_contiguous():
+            raise ValueError(f"ids must be contiguous int32 on {device}")
+        x32 = _aligned16(x.detach().reshape(-1, in_features).to(device=device,
+                                                                dtype=torch.float32).contiguous())
+        x_rows = x32.shape[0]
+        if x_rows not in (1, n_pairs):
+            raise ValueError(f"x must have 1 or {n_pairs} rows, not {x_rows}")
+        if workspace is None:
+            workspace = torch.empty(q8k_bytes(x_rows, in_features), dtype=torch.uint8, device=device)
+        out = torch.empty((n_pairs, out_features), dtype=torch.float32, device=device)
+        status = self._lib.mxa_gemm_moe_pairs(
+            ggml_type, experts.data_ptr(), rb * out_features, experts.shape[0], ids.data_ptr(),
+            n_pairs, x32.data_ptr(), x_rows, out.data_ptr(), out_features, in_features,
+            workspace.data_ptr(), workspace.numel(), _stream(device))
+        if status == -1:
+            return None
+        self._check(status, "mxa_gemm_moe_pairs", ggml_type)
+        self._calls += 1
+        return out
+
     def matmul_multi_q8k(self, items: list[tuple[int, torch.Tensor, int]], workspace: torch.Tensor,
                          n_tokens: int, in_features: int,
                          out: torch.Tensor | None = None) -> list[torch.Tensor]:

@@ -77,6 +77,11 @@ class HipPackedMoEExperts(nn.Module):
             if w.dim() != 3 or w.shape[0] != self.num_experts or (w.shape[1] * w.shape[2]) % 4:
                 raise ValueError(f"{name} experts must be (num_experts, out, row_bytes) with each "
                                  "expert's bytes a multiple of 4")
+        # the one-token pairs launch takes K / 256 in {4, 8, 16, 32, 56, 64} and 16-byte aligned
+        # rows; other shapes go straight to the grouped launch
+        self._pairs = all(k // 256 in (4, 8, 16, 32, 56, 64) and
+                          self._gemm.row_bytes(int(t), k) % 16 == 0
+                          for t, k in ((gate_type, n_embd), (up_type, n_embd), (down_type, ffn_len)))
         self.register_buffer("gate_packed", gate, persistent=False)
         self.register_buffer("up_packed", up, persistent=False)
         self.register_buffer("down_packed", down, persistent=False)
@@ -85,6 +90,10 @@ class HipPackedMoEExperts(nn.Module):
                 top_k_idx: torch.Tensor) -> torch.Tensor:
         n_tokens, n_embd = x.shape
         top_k = top_k_idx.shape[1]
+        if n_tokens == 1 and self._pairs:
+            out = self._one_token(x, top_k_weights, top_k_idx)
+            if out is not None:
+                return out
         order, offsets, pair_tok = route_pairs(top_k_idx, self.num_experts)
         g = self._gemm
         # the reference casts x to the layer dtype before each matmul (device_packed.py:54)
@@ -98,6 +107,31 @@ class HipPackedMoEExperts(nn.Module):
         w = top_k_weights.reshape(-1).index_select(0, order).unsqueeze(-1)
         contrib = (down.to(self.dtype) * w).to(torch.float32)  # sorted pair order
         return combine_in_expert_order(contrib, order, top_k_idx).to(x.dtype)
+
+    def _one_token(self, x: torch.Tensor, top_k_weights: torch.Tensor,
+                   top_k_idx: torch.Tensor) -> torch.Tensor | None:
+        """Decode: each routed expert is a distinct pair of the one token, so the projections
+        run as pairs (`mxa_gemm_moe_pairs`, expert ids read on the device) without sorting the
+        routing. None when a projection's shape does not suit that launch."""
+        g = self._gemm
+        gt, ut, dt = self.types
+        ids = top_k_idx.reshape(-1).to(torch.int32)
+        # the reference casts x to the layer dtype before each matmul (device_packed.py:54)
+        xs = x.to(self.dtype)
+        gate = g.matmul_moe_pairs(gt, self.gate_packed, ids, xs, self.ffn_len, self.n_embd)
+        if gate is None:
+            return None
+        up = g.matmul_moe_pairs(ut, self.up_packed, ids, xs, self.ffn_len, self.n_embd)
+        if up is None:
+            return None
+        act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
+        down = g.matmul_moe_pairs(dt, self.down_packed, ids, act, self.n_embd, self.ffn_len)
+        if down is None:
+            return None
+        w = top_k_weights.reshape(-1).unsqueeze(-1)
+        contrib = (down.to(self.dtype) * w).to(torch.float32)  # slot order
+        slot = torch.arange(ids.numel(), device=x.device)
+        return combine_in_expert_order(contrib, slot, top_k_idx).to(x.dtype)
 
     @classmethod
     def from_packed_bytes(cls, gate_raw, up_raw, down_raw, types: tuple[int, int, int],

@@ -141,6 +141,9 @@ def routing(n_tokens, n_experts, top_k, seed, device="cuda"):
 MODULE_CASES = [
     # (types gate/up/down, n_experts, n_embd, ffn_len, n_tokens, top_k, dtype)
     ((D.Q4_K, D.Q4_K, D.Q6_K), 8, 1024, 512, 24, 2, torch.float32),
+    # one token on the pairs launch (every projection's K / 256 in the kernel's set)
+    ((D.Q4_K, D.Q4_K, D.Q6_K), 8, 4096, 2048, 1, 2, torch.bfloat16),
+    ((D.Q8_0, D.Q8_0, D.Q4_K), 16, 2048, 2048, 1, 4, torch.float32),
     ((D.Q8_0, D.Q8_0, D.Q8_0), 4, 512, 768, 7, 2, torch.float32),
     ((D.Q4_K, D.Q4_K, D.Q4_K), 16, 512, 256, 40, 4, torch.bfloat16),
     ((D.Q6_K, D.Q6_K, D.Q4_K), 8, 256, 512, 1, 2, torch.float32),
@@ -176,3 +179,40 @@ def test_module_rejects_types_without_grouped_launch() -> None:
     z = torch.zeros((2, 256, 136), dtype=torch.uint8, device="cuda")
     with pytest.raises(ValueError):
         HipPackedMoEExperts(z, z, z, D.IQ4_XS, D.IQ4_XS, D.IQ4_XS, 256, 256, F.silu)
+
+
+PAIR_CASES = [
+    # (type, n_experts, out, in, n_pairs, x shared by the pairs)
+    (D.Q4_K, 8, 1024, 4096, 2, True),
+    (D.Q4_K, 8, 1000, 4096, 8, False),
+    (D.Q6_K, 4, 512, 2048, 3, True),
+    (D.Q8_0, 6, 777, 2048, 4, False),
+    (D.Q6_K, 3, 256, 14336, 2, False),  # 56-block rows: x quantized into the workspace first
+    (D.Q4_K, 2, 4096, 14336, 1, True),
+    (D.Q4_K, 4, 20000, 4096, 2, True),  # row sets: more rows than one pass holds
+]
+
+
+@pytest.mark.parametrize("case", range(len(PAIR_CASES)))
+def test_pairs_rows_match_oracle(gpu, oracle, case) -> None:
+    t, n_experts, n, k, n_pairs, shared = PAIR_CASES[case]
+    w = expert_weights(t, n_experts, n, k, seed=case * 11)
+    ids = np.random.default_rng(case).permutation(n_experts)[:n_pairs].astype(np.int32)
+    x = S.activations(1 if shared else n_pairs, k, seed=case + 5)
+    got = gpu.matmul_moe_pairs(t, torch.from_numpy(w).cuda(), torch.from_numpy(ids).cuda(),
+                               torch.from_numpy(x).cuda(), n, k)
+    assert got is not None, "the pairs launch declined a shape it is built for"
+    got = got.cpu().numpy()
+    for p in range(n_pairs):
+        xr = x[:1] if shared else x[p:p + 1]
+        assert_bit_exact(got[p:p + 1], oracle.gemm(t, w[ids[p]], xr, n, k), f"pair {p}")
+
+
+def test_pairs_decline_shapes_they_do_not_take(gpu) -> None:
+    ids = torch.zeros(1, dtype=torch.int32, device="cuda")
+    w = torch.zeros((2, 64, 3 * 144), dtype=torch.uint8, device="cuda")  # K = 768: 3 blocks
+    x = torch.zeros((1, 768), dtype=torch.float32, device="cuda")
+    assert gpu.matmul_moe_pairs(D.Q4_K, w, ids, x, 64, 768) is None
+    w = torch.zeros((2, 64, 4 * 210), dtype=torch.uint8, device="cuda")  # rows of 840 bytes
+    x = torch.zeros((1, 1024), dtype=torch.float32, device="cuda")
+    assert gpu.matmul_moe_pairs(D.Q6_K, w, ids, x, 64, 1024) is None
