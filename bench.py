@@ -501,8 +501,8 @@ TRAFFIC_KERNELS = [
      weight_bytes() + q8k_act_bytes(16, K) + 16 * N * 4,
      "Q4_K 14336x4096, M=16, on Q8_K activations (weight + Q8_K x + fp32 y)",
      ("mxa_bflow.hip",)),
-    ("q6k_head_128256x4096_m1", r"gemv_pipe_kernel<14, 1, ", HEAD_N * 3360 + K * 4 + HEAD_N * 4,
-     "Q6_K 128256x4096 (config 3 head), M=1 (weight + fp32 x + fp32 y)", ("mxa_gemv_lpb.hip",)),
+    ("q6k_head_128256x4096_m1", r"gemv_wave_kernel<14, 16, true, ", HEAD_N * 3360 + K * 4 + HEAD_N * 4,
+     "Q6_K 128256x4096 (config 3 head), M=1 (weight + fp32 x + fp32 y)", ("mxa_gemv_wave.hip",)),
     ("q6k_head_128256x4096_m16", r"(bflow|bres|bstream)_kernel<14, ",
      HEAD_N * 3360 + q8k_act_bytes(16, K) + 16 * HEAD_N * 4,
      "Q6_K 128256x4096 (config 3 head), M=16, on Q8_K activations",
