@@ -7,7 +7,7 @@
 // blocks, in two buffers: the next chunk is loaded into registers while the current one is
 // computed and written to the other buffer afterwards, so one barrier per chunk suffices (a
 // buffer is rewritten only after every wave has passed the barrier that ends its last use). Each
-// wave loads its rows' next block while it computes the current one.
+// wave loads its rows' block two ahead while it computes the current one.
 //
 // Operands: the tile builders of mxa_tiles.hpp, with A (16 activation rows x 64 k) read from LDS.
 // The blocks are folded in order 0..nb-1, so the outputs equal the oracle and the decode kernels
@@ -59,9 +59,14 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
 
-  W cur[NT], nxt[NT];
+  // weight blocks two ahead of the one computed (one ahead measured 4-6% slower: a block's
+  // compute does not cover the load latency; three ahead no faster)
+  W cur[NT], nxt[NT], nx2[NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) cur[nt] = Tile::load(row[nt], 0, g);
+  for (int nt = 0; nt < NT; ++nt) {
+    cur[nt] = Tile::load(row[nt], 0, g);
+    nxt[nt] = Tile::load(row[nt], min(1, nb - 1), g);
+  }
 
   // Activation staging, software-pipelined: chunk c + 1 is loaded into registers while chunk c
   // is computed, and written to LDS between the two barriers. Thread tid owns the same pieces of
@@ -150,9 +155,9 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
     for (int i = 0; i < kCB; ++i) {
       if (i < cn) {
         const int b = c0 + i;
-        if (b + 1 < nb) {
+        if (b + 2 < nb) {
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) nxt[nt] = Tile::load(row[nt], b + 1, g);
+          for (int nt = 0; nt < NT; ++nt) nx2[nt] = Tile::load(row[nt], b + 2, g);
         }
         typename Tile::P pp[NT];
 #pragma unroll
@@ -170,7 +175,10 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
           // M = 512 and 6% at M = 2048 than one tile at a time)
         }
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) cur[nt] = nxt[nt];
+        for (int nt = 0; nt < NT; ++nt) {
+          cur[nt] = nxt[nt];
+          nxt[nt] = nx2[nt];
+        }
       }
     }
     if (more) store_stage(st, buf ^ 1);
