@@ -143,13 +143,17 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
     }
   }
 
-  // Row set s (rows R s .. R s + R - 1): the workgroup's waves take sets (tile * waves + wave),
-  // then every n_wg * waves further, each set's copies issued once the previous set is computed.
-  // Every copy of a set's range is issued (the last ones may pass it: they read the next set's
-  // rows, or stop at the matrix's last 16-byte word, and land in this wave's stage).
+  // Row set s (rows R s .. R s + R - 1), in rounds of n_wg * waves sets: in the first round the
+  // workgroup's waves take sets tile * waves + wave (contiguous per workgroup); in later rounds
+  // wave v of every workgroup takes set v * n_wg + tile of the round, so a partial last round
+  // spreads over all workgroups rather than filling the first ones. Each set's copies are issued
+  // once the previous set is computed. Every copy of a set's range is issued (the last ones may
+  // pass it: they read the next set's rows, or stop at the matrix's last 16-byte word, and land
+  // in this wave's stage).
   const bool has_rows = wave < waves;
   const int n_sets = (N + R - 1) / R, set_stride = n_wg * waves;
-  int set = xcd_tile(wg, n_wg) * waves + wave;
+  const int tile = xcd_tile(wg, n_wg);
+  int set = tile * waves + wave, round0 = 0;
   const uintptr_t last = ((uintptr_t)(w + (size_t)N * row_bytes) - 1) & ~(uintptr_t)15;
   const uint32_t lds_w = lds_addr(wreg), lane16 = 16u * (uint32_t)lane;
   // Copies clamped to the matrix's last 16-byte word. With the set loop: a wave-uniform base and
@@ -251,7 +255,8 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
       L::template compute<1, ActRegs>(wreg, jl * L::kBytes, &areg, 1, V, D);
     else
       L::template compute<MAXM, ActPieces>(wreg, jl * L::kBytes, ap, M, V, D);
-    const int next = set + set_stride;
+    round0 += set_stride;
+    const int next = round0 + wave * n_wg + tile;
 #pragma unroll
     for (int m = 0; m < MAXM; ++m)
       if (m < M) Vbuf[64 * m + lane] = V[m];
