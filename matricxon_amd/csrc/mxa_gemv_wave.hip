@@ -1,7 +1,7 @@
 // Decode GEMV for one activation row in the shape of the read floor: one workgroup per CU whose
 // waves request every byte of their rows at their first instructions, then compute each row set
 // as it lands. y[n] = sum_k x[k] * W[n, k] for K-quant / Q8_0 weights with nb = K / 256 in
-// {4, 8, 16, 32, 56, 64} (56 with x quantized in the kernel: Q4_K only).
+// {4, 8, 16, 32, 56, 64}.
 //
 // Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, or one row of 56
 // with eight lanes idle; one byte range, 16-byte aligned because row_bytes is) and issues all of
@@ -368,13 +368,12 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   // More rows than one round of workgroups holds: one workgroup per CU whose waves take further
   // row sets, each requested once the previous set is computed (measured on MI355X against the
   // pipelined kernel and against rounds of workgroups: Q4_K 28672 x 4096 14.8 vs 17.1 and 15.7
-  // us, 128256 x 4096 47.3 vs 52.9 us pipelined; Q6_K 14336 x 4096 12.2 vs 13.7, the 128256 x 4096
-  // head 74.4 vs 77.2, 8192 x 16384 27.9 vs 29.4; Q8_0 14336 x 4096 11.3 vs 13.1). 56-block rows
-  // (K = 14336) with fp32 x staged in the kernel leave room for few weight waves (56 KB of x):
-  // Q4_K only (4096 x 14336 10.4 vs 11.3 us; Q6_K 15.5 vs 15.6, Q8_0 16.1 vs 15.7 stay
-  // pipelined); on workspace Q8_K all three (Q4_K 8.9 vs 11.9, Q6_K 14.6 vs 15.8, Q8_0 14.2 vs
-  // 15.5 us).
-  if constexpr (NB == 56 && FUSEQ && TYPE != T_Q4_K) return -1;
+  // us, 128256 x 4096 47.3 vs 52.9 us pipelined; Q6_K 14336 x 4096 10.2 vs 13.7, the 128256 x 4096
+  // head 71.5 vs 77.2, 8192 x 16384 27.9 vs 29.4; Q8_0 14336 x 4096 11.3 vs 13.1). 56-block rows
+  // (K = 14336) with fp32 x staged in the kernel leave room for few weight waves (56 KB of x) and
+  // still measured faster (4096 x 14336: Q4_K 10.0 vs 11.3 us, Q6_K 14.8 vs 15.4, Q8_0 15.6 vs
+  // 15.8; Q6_K 6144 x 14336 18.8 vs 22.3); on workspace Q8_K more waves fit (Q4_K 8.9, Q6_K 13.1,
+  // Q8_0 13.8 us).
   if (waves < 1 || ldy > 0x7FFFFFFF) return -1;
   constexpr int kSets = 64;  // row sets per wave at most
   const int grid = min((N + waves * R - 1) / (waves * R), ncu);

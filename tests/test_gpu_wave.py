@@ -2,7 +2,7 @@
 the CPU oracle, through the C ABI: bit-exact for Q8_0 / Q4_K / Q6_K.
 
 The kernel takes every one-token K-quant / Q8_0 call whose blocks per row nb = K / 256 are in
-{4, 8, 16, 32, 56, 64} (56 with x quantized in the kernel: Q4_K only), one workgroup per CU;
+{4, 8, 16, 32, 56, 64}, one workgroup per CU;
 past one pass its waves take up to 64 row sets each. A wave owns 64 / nb rows (one row of 56
 blocks at nb = 56, eight lanes idle); the shapes cover each nb it is built for, N that leaves the
 last wave or workgroup partial, N so small that some workgroups' waves only stage the
@@ -77,7 +77,8 @@ def test_one_row_wave_kernel_round_edge(gpu, oracle, ggml_type, extra) -> None:
 ROUNDS_CASES = [(D.Q4_K, 28672, 4096), (D.Q8_0, 14336, 4096), (D.Q4_K, 14336, 8192),
                 (D.Q4_K, 57344, 4096), (D.Q4_K, 57345, 4096), (D.Q4_K, 14336, 14336),
                 (D.Q8_0, 4097, 14336), (D.Q6_K, 14336, 4096), (D.Q6_K, 4096, 14336),
-                (D.Q6_K, 8192, 16384), (D.Q6_K, 128256, 4096), (D.Q4_K, 4096, 14336)]
+                (D.Q6_K, 8192, 16384), (D.Q6_K, 128256, 4096), (D.Q4_K, 4096, 14336),
+                (D.Q6_K, 6144, 14336), (D.Q8_0, 6000, 14336), (D.Q4_K, 20000, 4096)]
 
 
 @pytest.mark.parametrize("ggml_type,n,k", ROUNDS_CASES)
