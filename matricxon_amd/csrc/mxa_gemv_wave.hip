@@ -316,7 +316,7 @@ struct WaveSegs {
   int count;
 };
 
-template <int NB, bool FUSEQ>
+template <int NB, bool FUSEQ, bool LOOP>
 __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
     WaveSegs segs, const float* __restrict__ x, int nq, const int8_t* __restrict__ aq,
     const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
@@ -327,11 +327,14 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
   const WaveSeg& g = segs.s[si];
   const int wg = (int)blockIdx.x - g.wg0;
   if (g.type == T_Q4_K)
-    wave_rows<T_Q4_K, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
+    wave_rows<T_Q4_K, NB, FUSEQ, true, 1, LOOP>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq,
+                                                ad, abs_, wg, g.n_wg);
   else if (g.type == T_Q8_0)
-    wave_rows<T_Q8_0, NB, FUSEQ, true>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
+    wave_rows<T_Q8_0, NB, FUSEQ, true, 1, LOOP>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq,
+                                                ad, abs_, wg, g.n_wg);
   else
-    wave_rows<T_Q6_K, NB, FUSEQ, false>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq, ad, abs_, wg, g.n_wg);
+    wave_rows<T_Q6_K, NB, FUSEQ, false, 1, LOOP>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0,
+                                                 aq, ad, abs_, wg, g.n_wg);
 }
 
 // One token's routed experts (MoE decode): pair p multiplies expert ids[p] (a device array; an id
@@ -435,39 +438,53 @@ int region_of(int type) {
                         : wave_region_bytes<T_Q6_K, NB>();
 }
 
-// Each weight gets workgroups in proportion to its bytes (at least one), and its workgroups as
-// many row waves as spread its rows over them; the grid must fit the rounds the single-weight form
-// allows its types.
+// Each weight gets CUs in proportion to its bytes (at least one), one workgroup each, with as many
+// row waves as spread its rows over them; a weight with more rows than one pass of its
+// workgroups holds takes further row sets, as in the single-weight form.
 template <int NB, bool FUSEQ>
 int launch_wave_multi_t(const DecodeSeg* seg, int count, const Act& act, hipStream_t stream) {
   constexpr int R = 64 / NB;
+  constexpr int kSets = 64;  // row sets per wave at most
   const int ncu = cu_count();
   const int act_lds = wave_act_bytes(NB, FUSEQ);
   double total = 0.0;
-  bool heavy = NB > 32;
+  for (int i = 0; i < count; ++i) total += (double)seg[i].n * (double)seg[i].row_bytes;
+  // CU shares: rounded down, at least one, the CUs left over to the largest weights in turn
+  int share[kWaveMaxSegs], used = 0;
   for (int i = 0; i < count; ++i) {
-    total += (double)seg[i].n * (double)seg[i].row_bytes;
-    heavy = heavy || seg[i].type == T_Q6_K;
+    share[i] = max(1, (int)((double)ncu * seg[i].n * seg[i].row_bytes / total));
+    used += share[i];
+  }
+  for (int left = ncu - used; left > 0;) {
+    int best = 0;
+    for (int i = 1; i < count; ++i)
+      if ((double)seg[i].n * seg[i].row_bytes / share[i] >
+          (double)seg[best].n * seg[best].row_bytes / share[best])
+        best = i;
+    ++share[best];
+    --left;
   }
   WaveSegs segs{};
   segs.count = count;
   int grid = 0, nw = min(kWaveMaxWaves, NB / 4), lds = act_lds;
+  bool loop = false;
   for (int i = 0; i < count; ++i) {
     const int region = region_of<NB>(seg[i].type);
     const int fit = (kWaveLds - act_lds) / region;
-    const int share = max(1, (int)((double)ncu * seg[i].n * seg[i].row_bytes / total + 0.5));
-    const int per_wg = (seg[i].n + share - 1) / share;
+    const int per_wg = (seg[i].n + share[i] - 1) / share[i];
     const int waves = min(min(kWaveMaxWaves, fit), (per_wg + R - 1) / R);
     if (waves < 1) return -1;
-    const int wgs = (seg[i].n + waves * R - 1) / (waves * R);
+    const int wgs = min(share[i], (seg[i].n + waves * R - 1) / (waves * R));
+    if ((long long)waves * R * wgs * kSets < seg[i].n) return -1;
+    loop = loop || (long long)waves * R * wgs < seg[i].n;
     segs.s[i] = WaveSeg{seg[i].w, seg[i].y, seg[i].n, (int)seg[i].row_bytes, seg[i].type, grid,
                         waves, wgs};
     grid += wgs;
     nw = max(nw, waves);
     lds = max(lds, act_lds + waves * region);
   }
-  if (grid > ncu * (heavy ? 1 : 4)) return -1;
-  auto kern = gemv_wave_multi_kernel<NB, FUSEQ>;
+  if (grid > ncu) return -1;
+  auto kern = loop ? gemv_wave_multi_kernel<NB, FUSEQ, true> : gemv_wave_multi_kernel<NB, FUSEQ, false>;
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, segs, act.x,
                      min(kWaveMaxWaves, NB / 4), act.q, act.d, act.bsums);

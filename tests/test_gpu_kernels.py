@@ -218,13 +218,17 @@ MULTI_CASES = [
     # q|k|v shape: segments of different types and tile counts
     ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 9),
     # one token (the floor-shaped multi-weight kernel): q|k|v and gate|up at full size (gate|up
-    # in two rounds of workgroups), four segments of 8-block rows, 4-block rows, and a Q6_K group
-    # past one round (taken by the pipelined kernel instead)
+    # with two row sets per wave), four segments of 8-block rows, 4-block rows, groups past one
+    # pass for every type (row sets), mixed types past one pass, and a segment of one workgroup
     ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 1),
     ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 1),
     ([(D.Q8_0, 96), (D.Q6_K, 33), (D.Q4_K, 65), (D.Q4_K, 1)], 2048, 1),
     ([(D.Q8_0, 3000), (D.Q4_K, 5000)], 1024, 1),
     ([(D.Q6_K, 9000), (D.Q4_K, 100)], 4096, 1),
+    ([(D.Q6_K, 14336), (D.Q6_K, 14336)], 4096, 1),
+    ([(D.Q8_0, 14336), (D.Q8_0, 14335)], 4096, 1),
+    ([(D.Q4_K, 28673), (D.Q6_K, 4096), (D.Q8_0, 2048)], 4096, 1),
+    ([(D.Q4_K, 8192), (D.Q4_K, 8191)], 8192, 1),
 ]
 
 
