@@ -328,11 +328,14 @@ def test_one_row_decode_weight_off_16_byte_boundary(gpu, oracle, ggml_type) -> N
 # resident (N = 14336: 56 rows, a half last tile; Q6_K / Q8_0 at N = 8192: two tiles; 3000 x
 # 2304: 12 rows per workgroup, odd block count; 14000 x 512: 55 rows of 2 blocks); more tiles than
 # LDS slots cycle through them (30000 x 4096: 8 tiles; 40000 x 2048: 10 tiles, Q4_K in 8 slots;
-# 50000 x 4096: 13 tiles); rows of more than 16 blocks stream.
+# 50000 x 4096: 13 tiles); rows of more than 16 blocks stream, several tiles per workgroup with
+# their sums carried across parts (9000 x 5120: three tiles, the last of four rows; 40000 x 4608:
+# ten tiles of three parts, past the eight-tile output ring).
 BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
                 (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6),
                 (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10),
-                (30000, 4096, 9), (40000, 2048, 5), (50000, 4096, 16)]
+                (30000, 4096, 9), (40000, 2048, 5), (50000, 4096, 16), (9000, 5120, 12),
+                (40000, 4608, 4)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
