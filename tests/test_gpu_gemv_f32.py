@@ -106,6 +106,16 @@ def test_gemv_f32_keeps_activations_unquantized(gpu, t) -> None:
         assert e_q8k > 100 * e_f32, (e_q8k, e_f32)
 
 
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (333, 2304, 1), (30000, 512, 1), (700, 4096, 3)])
+def test_gemv_f32_iq4_xs_equals_matmul(gpu, n, k, m) -> None:
+    # IQ4_XS multiplies float activations on both paths, every kernel in one summation order (one
+    # row: the resident kernel where the weight fits it, else the pipelined one): the same bits
+    w = S.packed_weight(D.IQ4_XS, n, k, seed=7500 + n + m)
+    x = dev(S.activations(m, k, seed=7501 + m))
+    wd = dev(w)
+    assert torch.equal(gpu.gemv_f32(D.IQ4_XS, wd, x, n, k), gpu.matmul(D.IQ4_XS, wd, x, n, k))
+
+
 def test_qgemv_mirror_and_registry(gpu) -> None:
     n, k = 300, 4096
     w = S.packed_weight(D.Q4_K, n, k, seed=7400)
