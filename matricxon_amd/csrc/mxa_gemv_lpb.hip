@@ -841,7 +841,7 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
     if (launch_gemv_wave(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
     if (launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
   }
-  if (m_rows == 2 && launch_gemv_wave_m(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream) == 0)
+  if (m_rows >= 2 && launch_gemv_wave_m(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream) == 0)
     return 0;
   switch (type) {
     case T_Q4_K: return launch_lpb_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);

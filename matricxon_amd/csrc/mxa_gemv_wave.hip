@@ -403,17 +403,22 @@ int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* 
              : launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
-// One activation row: every nb the kernel is built for. Two rows: 8-, 16- and 32-block rows
-// (measured on MI355X against the pipelined kernel: Q4_K 4096 x 4096 4.8 vs 6.5 us, 28672 x 4096
-// 15.9 vs 19.3, 14336 x 4096 10.7 vs 10.7; Q6_K 4096 x 4096 6.3 vs 7.9; Q8_0 6.4 vs 7.4). Three
-// and four rows measured mixed (Q4_K 14336 x 4096 at three rows 12.9 vs 12.1 us, Q8_0 4096 x 4096
-// at four 14.3 vs 9.0) and stay on the pipelined kernel.
+// One activation row: every nb the kernel is built for. Two to four rows: 8-, 16- and 32-block
+// rows, measured on MI355X against the pipelined kernel (same bits): two rows Q4_K 4096 x 4096 5.1
+// vs 6.5 us, 14336 x 4096 8.5 vs 10.7, 28672 x 4096 13.4 vs 19.3; Q6_K 4096 x 4096 6.5 vs 7.9;
+// Q8_0 6.6 vs 7.4. Three rows: Q4_K 4096 x 4096 6.5 vs 7.5, 14336 x 4096 12.0 vs 12.2, 28672 x
+// 4096 18.4 vs 21.0; Q6_K 4096 x 4096 8.0 vs 8.9, 14336 x 4096 18.4 vs 19.8; Q8_0 7.9 vs 8.2.
+// Four rows for Q4_K only (14336 x 4096 13.7 vs 16.2 us; Q8_0 11.5 vs 9.0 and Q6_K 14336 x 4096
+// 23.6 vs 22.1 stay pipelined).
 template <int TYPE, int NB>
 int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                    int M, int N, hipStream_t stream) {
   if (M == 1) return launch_wave_m<TYPE, NB, 1>(w, row_bytes, act, y, ldy, M, N, stream);
-  if constexpr (NB == 8 || NB == 16 || NB == 32)
+  if constexpr (NB == 8 || NB == 16 || NB == 32) {
     if (M == 2) return launch_wave_m<TYPE, NB, 2>(w, row_bytes, act, y, ldy, M, N, stream);
+    if (M == 3 || (M == 4 && TYPE == T_Q4_K))
+      return launch_wave_m<TYPE, NB, 4>(w, row_bytes, act, y, ldy, M, N, stream);
+  }
   return -1;
 }
 

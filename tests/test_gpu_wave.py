@@ -110,14 +110,27 @@ def run_rows(gpu, oracle, t, n, k, m, seed):
     assert_bit_exact(host(gpu.matmul_q8k(t, wd, ws, None, out, m, n, k)), want)  # Q8_K given
 
 
-# Two activation rows (8-, 16- and 32-block rows; three and four rows run the pipelined kernel
-# and are checked here too): every row's block values from one read of the weight, the last wave
-# partial, Q4_K past one pass (row sets), Q6_K and Q8_0 rows.
+# Two and three activation rows (8-, 16- and 32-block rows; four rows run the matrix-core kernels
+# by default and are checked here too): every row's block values from one read of the weight, the
+# last wave partial, Q4_K past one pass (row sets), Q6_K and Q8_0 rows.
 ROWS_CASES = [(D.Q4_K, 14336, 4096), (D.Q4_K, 1001, 2048), (D.Q6_K, 4100, 4096),
-              (D.Q8_0, 3000, 8192), (D.Q4_K, 28672, 4096), (D.Q4_K, 5000, 8192)]
+              (D.Q8_0, 3000, 8192), (D.Q4_K, 28672, 4096), (D.Q4_K, 5000, 8192),
+              (D.Q6_K, 14336, 4096), (D.Q8_0, 700, 2048)]
 
 
 @pytest.mark.parametrize("m", [2, 3, 4])
 @pytest.mark.parametrize("ggml_type,n,k", ROWS_CASES)
 def test_decode_two_to_four_rows(gpu, oracle, ggml_type, n, k, m) -> None:
     run_rows(gpu, oracle, ggml_type, n, k, m, seed=n + k + m)
+
+
+@pytest.mark.parametrize("ggml_type,n,k", ROWS_CASES)
+def test_decode_four_rows_on_the_decode_kernels(gpu, oracle, ggml_type, n, k) -> None:
+    # with the crossover raised to four tokens, four rows take the decode kernels (Q4_K: the
+    # floor-shaped kernel; Q6_K and Q8_0: the pipelined one)
+    before = gpu.fused_max_tokens
+    gpu.set_fused_max_tokens(4)
+    try:
+        run_rows(gpu, oracle, ggml_type, n, k, 4, seed=n + k + 40)
+    finally:
+        gpu.set_fused_max_tokens(before)
