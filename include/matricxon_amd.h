@@ -151,6 +151,19 @@ int mxa_gemm_moe_pairs(int ggml_type, const void *w, long long expert_stride, in
                        int out_features, int in_features, void *workspace,
                        size_t workspace_bytes, void *stream);
 
+/* Routing-weighted combine of MoE expert outputs, one launch: out (n_tokens, n_embd) fp32, row t =
+ * the sum over token t's top_k slots k, in ascending expert id ids[t * top_k + k] (a DEVICE int32
+ * array; equal ids in slot order), of down[r] * weights[t * top_k + k] with r = rows[t * top_k +
+ * k] (a DEVICE int32 array of down rows; NULL: r = t * top_k + k), from a float zero, each
+ * product and sum rounded to float32. round_bf16 != 0 rounds each down value to bfloat16 first.
+ * down (rows, n_embd) fp32 and weights fp32 are device arrays; top_k <= 16 (else -1). The
+ * combine of `QuantizedMoEExperts.forward` (app/architectures/moe_experts.py:81-88: the
+ * projection output cast to the layer dtype, times the float32 weight, `index_add_`ed into a
+ * float32 zero tensor expert by expert in ascending id), bit for bit. */
+int mxa_moe_combine(const float *down, const int32_t *rows, const int32_t *ids,
+                    const float *weights, int n_tokens, int top_k, int n_embd, int round_bf16,
+                    float *out, void *stream);
+
 /* Up to 4 packed weights sharing one input (q/k/v, gate/up): one activation quantization, then
  * each weight's output columns written after the previous weight's, y (n_tokens, sum outs).
  * `types`, `ws` (device pointers) and `outs` are HOST arrays of n entries.

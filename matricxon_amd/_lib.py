@@ -27,6 +27,7 @@ EXPORTS = (
     "mxa_gemm_q8k",
     "mxa_gemm_moe",
     "mxa_gemm_moe_pairs",
+    "mxa_moe_combine",
     "mxa_gemm_multi",
     "mxa_gemm_multi_q8k",
     "mxa_quantize_q8_k",
@@ -86,6 +87,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_gemm_moe.restype = _i
     lib.mxa_gemm_moe_pairs.argtypes = [_i, _vp, _ll, _i, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_moe_pairs.restype = _i
+    lib.mxa_moe_combine.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]
+    lib.mxa_moe_combine.restype = _i
     lib.mxa_gemm_multi.argtypes = [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_multi.restype = _i
     lib.mxa_gemm_multi_q8k.argtypes = [_i, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]

@@ -223,6 +223,17 @@ int mxa_gemm_moe_pairs(int ggml_type, const void* w, long long expert_stride, in
   return check_launch();
 }
 
+int mxa_moe_combine(const float* down, const int32_t* rows, const int32_t* ids,
+                    const float* weights, int n_tokens, int top_k, int n_embd, int round_bf16,
+                    float* out, void* stream) {
+  if (down == nullptr || ids == nullptr || weights == nullptr || out == nullptr)
+    return MXA_ERR_UNSUPPORTED;
+  if (mxa::launch_moe_combine(down, rows, ids, weights, n_tokens, top_k, n_embd, round_bf16 != 0,
+                              out, (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
 int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* outs,
                    const float* x, float* y, int n_tokens, int in_features, void* workspace,
                    size_t workspace_bytes, void* stream) {

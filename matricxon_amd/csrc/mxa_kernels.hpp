@@ -190,6 +190,15 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
                    int n_experts, const Act& act, const int32_t* offsets, int total_rows,
                    int max_rows, float* y, long long ldy, int n_rows, hipStream_t stream);
 
+// out[t] (n_tokens x n_embd fp32) = the routing-weighted sum of token t's expert outputs:
+// down row rows[t top_k + k] (rows == nullptr: row t top_k + k) of slot k, times weights[t top_k
+// + k], slots in ascending ids[t top_k + k] (ties in slot order), bf16 != 0: each down value
+// rounded to bfloat16 first. top_k <= kMoeMaxTopK; -1 otherwise.
+constexpr int kMoeMaxTopK = 16;
+int launch_moe_combine(const float* down, const int32_t* rows, const int32_t* ids,
+                       const float* weights, int n_tokens, int top_k, int n_embd, int bf16,
+                       float* out, hipStream_t stream);
+
 // Batched decode (m_rows <= 16) on the matrix cores with the weight rows streamed into LDS by
 // coalesced copies, one persistent workgroup per CU: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
 // workspace. -1 when the shape does not suit it (the caller uses launch_mtile).

@@ -413,6 +413,37 @@ class HipGemm:
         self._calls += 1
         return out
 
+    def moe_combine(self, down: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                    rows: torch.Tensor | None = None, round_bf16: bool = False) -> torch.Tensor:
+        """The weighted combine of MoE expert outputs in one launch (`mxa_moe_combine`): row t of
+        the result (n_tokens, n_embd) float32 adds, in ascending expert id of token t's slots
+        (`ids` (n_tokens, top_k) int32; equal ids in slot order), down row rows[t, k] (`rows`
+        int32 like `ids`, or None for row t * top_k + k) times weights[t, k] (float32), from a
+        float zero; `round_bf16` rounds each down value to bfloat16 first, as the module's cast
+        to a bfloat16 layer dtype does. The combine of QuantizedMoEExperts.forward
+        (app/architectures/moe_experts.py:81-88), bit for bit."""
+        _require_device_tensor("down", down)
+        device = down.device
+        if down.dtype != torch.float32 or down.dim() != 2 or not down.is_contiguous():
+            raise ValueError("down must be a contiguous float32 (rows, n_embd) tensor")
+        if ids.dim() != 2:
+            raise ValueError("ids must be (n_tokens, top_k)")
+        n_tokens, top_k = ids.shape
+        for name, t, dt in (("ids", ids, torch.int32), ("weights", weights, torch.float32)) + (
+                (("rows", rows, torch.int32),) if rows is not None else ()):
+            if t.dtype != dt or t.device != device or not t.is_contiguous() or \
+                    tuple(t.shape) != (n_tokens, top_k):
+                raise ValueError(f"{name} must be a contiguous {dt} ({n_tokens}, {top_k}) tensor "
+                                 f"on {device}")
+        out = torch.empty((n_tokens, down.shape[1]), dtype=torch.float32, device=device)
+        status = self._lib.mxa_moe_combine(
+            down.data_ptr(), rows.data_ptr() if rows is not None else None, ids.data_ptr(),
+            weights.data_ptr(), n_tokens, top_k, down.shape[1], int(bool(round_bf16)),
+            out.data_ptr(), _stream(device))
+        self._check(status, "mxa_moe_combine", 0)
+        self._calls += 1
+        return out
+
     def matmul_multi_q8k(self, items: list[tuple[int, torch.Tensor, int]], workspace: torch.Tensor,
                          n_tokens: int, in_features: int,
                          out: torch.Tensor | None = None) -> list[torch.Tensor]:

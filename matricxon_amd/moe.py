@@ -104,9 +104,31 @@ class HipPackedMoEExperts(nn.Module):
         up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd)
         act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
         down = g.matmul_moe(dt, self.down_packed, act, offsets, bound, n_embd, self.ffn_len)
+        if self._fused_combine(top_k_weights):
+            # down row of pair p = its place in the sorted order
+            rows = torch.empty_like(order)
+            rows[order] = torch.arange(order.numel(), device=order.device)
+            return self._combine(down, rows, top_k_idx, top_k_weights).to(x.dtype)
         w = top_k_weights.reshape(-1).index_select(0, order).unsqueeze(-1)
         contrib = (down.to(self.dtype) * w).to(torch.float32)  # sorted pair order
         return combine_in_expert_order(contrib, order, top_k_idx).to(x.dtype)
+
+    def _fused_combine(self, top_k_weights: torch.Tensor) -> bool:
+        """Whether the weighted combine runs as one `mxa_moe_combine` launch: float32 routing
+        weights, a float32 or bfloat16 layer dtype, at most 16 experts per token."""
+        return (top_k_weights.dtype == torch.float32 and top_k_weights.shape[-1] <= 16
+                and self.dtype in (torch.float32, torch.bfloat16))
+
+    def _combine(self, down: torch.Tensor, rows: torch.Tensor | None, top_k_idx: torch.Tensor,
+                 top_k_weights: torch.Tensor) -> torch.Tensor:
+        """float32 (n_tokens, n_embd): the reference's `down.to(dtype) * weight` contributions
+        `index_add_`ed in ascending expert order, in one launch."""
+        shape = top_k_idx.shape
+        ids = top_k_idx.to(torch.int32).contiguous()
+        if rows is not None:
+            rows = rows.to(torch.int32).reshape(shape).contiguous()
+        return self._gemm.moe_combine(down, ids, top_k_weights.contiguous(), rows,
+                                      round_bf16=self.dtype == torch.bfloat16)
 
     def _one_token(self, x: torch.Tensor, top_k_weights: torch.Tensor,
                    top_k_idx: torch.Tensor) -> torch.Tensor | None:
@@ -128,6 +150,8 @@ class HipPackedMoEExperts(nn.Module):
         down = g.matmul_moe_pairs(dt, self.down_packed, ids, act, self.n_embd, self.ffn_len)
         if down is None:
             return None
+        if self._fused_combine(top_k_weights):
+            return self._combine(down, None, top_k_idx, top_k_weights).to(x.dtype)
         w = top_k_weights.reshape(-1).unsqueeze(-1)
         contrib = (down.to(self.dtype) * w).to(torch.float32)  # slot order
         slot = torch.arange(ids.numel(), device=x.device)

@@ -216,3 +216,59 @@ def test_pairs_decline_shapes_they_do_not_take(gpu) -> None:
     w = torch.zeros((2, 64, 4 * 210), dtype=torch.uint8, device="cuda")  # rows of 840 bytes
     x = torch.zeros((1, 1024), dtype=torch.float32, device="cuda")
     assert gpu.matmul_moe_pairs(D.Q6_K, w, ids, x, 64, 1024) is None
+
+
+def combine_reference(down, rows, ids, weights, bf16):
+    """The module's torch combine restated on the CPU: per token, slots in stable ascending id
+    order, `down.to(dtype)` (bf16: rounded) times the float32 weight added to a float32 zero."""
+    n_tokens, top_k = ids.shape
+    out = torch.zeros(n_tokens, down.shape[1], dtype=torch.float32)
+    for t in range(n_tokens):
+        for k in torch.argsort(ids[t], stable=True).tolist():
+            v = down[rows[t, k]]
+            if bf16:
+                v = v.to(torch.bfloat16).to(torch.float32)
+            out[t] = out[t] + v * weights[t, k]
+    return out
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("n_tokens,top_k,n_embd", [(1, 2, 4096), (5, 8, 1000), (3, 16, 300)])
+def test_moe_combine_matches_torch_steps(gpu, bf16, n_tokens, top_k, n_embd) -> None:
+    # repeated expert ids (slot order decides), rows in a shuffled order, and special values: NaN,
+    # infinities, -0.0 and float32 values halfway between two bfloat16 values (ties to even)
+    g = torch.Generator().manual_seed(n_tokens * 100 + top_k + int(bf16))
+    total = n_tokens * top_k
+    down = torch.randn(total, n_embd, generator=g) * 8
+    down[0, :6] = torch.tensor([float("nan"), float("inf"), -0.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8,
+                                -float("inf")])
+    ids = torch.randint(0, max(2, top_k // 2), (n_tokens, top_k), generator=g, dtype=torch.int32)
+    rows = torch.randperm(total, generator=g).to(torch.int32).view(n_tokens, top_k)
+    weights = torch.rand(n_tokens, top_k, generator=g)
+    weights[0, 0] = -0.0
+    got = gpu.moe_combine(down.cuda(), ids.cuda(), weights.cuda(), rows.cuda(), round_bf16=bf16)
+    want = combine_reference(down, rows, ids, weights, bf16)
+    got = got.cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    fin = ~torch.isnan(want)
+    assert torch.equal(got[fin].view(torch.int32), want[fin].view(torch.int32))
+    # identity rows (NULL): pair p's row is p
+    got2 = gpu.moe_combine(down.cuda(), ids.cuda(), weights.cuda(), None, round_bf16=bf16).cpu()
+    ident = torch.arange(total, dtype=torch.int32).view(n_tokens, top_k)
+    want2 = combine_reference(down, ident, ids, weights, bf16)
+    fin2 = ~torch.isnan(want2)
+    assert torch.equal(torch.isnan(got2), torch.isnan(want2))
+    assert torch.equal(got2[fin2].view(torch.int32), want2[fin2].view(torch.int32))
+
+
+def test_module_bf16_routing_weights_take_the_torch_combine() -> None:
+    # routing weights in bfloat16: the product stays bfloat16 in torch, so the module keeps the
+    # torch combine; still the reference loop's bits
+    types = (D.Q4_K, D.Q4_K, D.Q6_K)
+    mod, per_expert = build_experts(types, 8, 4096, 2048, torch.bfloat16, seed=21)
+    x = torch.from_numpy(S.activations(1, 4096, seed=22)).cuda().to(torch.bfloat16)
+    tw, tidx = routing(1, 8, 2, seed=23)
+    tw = tw.to(torch.bfloat16)
+    got = mod(x, tw, tidx)
+    want = reference_forward(x, tw, tidx, per_expert, F.silu)
+    assert torch.equal(got.float().view(torch.int32), want.float().view(torch.int32))
