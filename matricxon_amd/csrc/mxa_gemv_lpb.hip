@@ -863,9 +863,11 @@ int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float
     case T_Q6_K: return launch_lpb_type<T_Q6_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q8_0: return launch_lpb_type<T_Q8_0_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_IQ4_XS:
-      // IQ4_XS always multiplies float activations; one row takes the resident kernel where the
-      // weight fits it, as mxa_gemm does (the same summation order, so the same bits)
-      if (m_rows == 1 && launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
+      // IQ4_XS always multiplies float activations; one row takes the kernels mxa_gemm uses for it
+      // (the same summation order in every kernel, so the same bits)
+      if (m_rows == 1 && (launch_gemv_wave(type, w, row_bytes, act, y, n_rows, stream) == 0 ||
+                          launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0))
+        return 0;
       return launch_lpb_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }

@@ -1,7 +1,7 @@
 // Decode GEMV for one activation row in the shape of the read floor: one workgroup per CU whose
 // waves request every byte of their rows at their first instructions, then compute each row set
 // as it lands. y[n] = sum_k x[k] * W[n, k] for K-quant / Q8_0 weights with nb = K / 256 in
-// {4, 8, 16, 32, 56, 64}.
+// {4, 8, 16, 32, 56, 64}, and for IQ4_XS on float activations (one row).
 //
 // Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, or one row of 56
 // with eight lanes idle; one byte range, 16-byte aligned because row_bytes is) and issues all of
@@ -26,8 +26,11 @@
 // lane-per-block arithmetic of the pipelined decode kernel (mxa_lpb.hpp), Q4_K and Q8_0 with the
 // lane's activation block in registers; one lane per row folds the row's block values in order
 // with the CPU oracle's fused steps, so results equal it bit for bit
-// (app/native/src/mx_dot_k_ssse3.c:115-209, mx_dot_q8_0.c:5-22). nb is a template parameter: as
-// a run-time value it costs the compute section ~1.7x the instructions (measured 8.0 vs 7.3 us).
+// (app/native/src/mx_dot_k_ssse3.c:115-209, mx_dot_q8_0.c:5-22). IQ4_XS keeps float
+// activations: the stagers copy x as [16-byte piece][block] (consecutive lanes read consecutive
+// 16-byte words) and lanes run the IQ4_XS block arithmetic every IQ4_XS kernel here shares, so a
+// row's result does not depend on the kernel. nb is a template parameter: as a run-time value it
+// costs the compute section ~1.7x the instructions (measured 8.0 vs 7.3 us).
 #include "mxa_kernels.hpp"
 #include "mxa_lpb.hpp"
 
@@ -37,6 +40,7 @@ namespace mxa {
 namespace {
 
 constexpr int kWaveMaxWaves = 16;
+constexpr long long kWaveIq4MinBytes = 4ll << 20;
 constexpr int kWaveLds = 160 * 1024;
 
 template <int TYPE, int NB>
@@ -60,6 +64,10 @@ __host__ __device__ constexpr int wave_x_off(int nb, int m) { return wave_flag_o
 __host__ __device__ constexpr int wave_act_bytes(int nb, bool fuseq, int m = 1) {
   return wave_x_off(nb, m) + (fuseq ? m * nb * 1024 : 0);
 }
+// Float activations kept as they are (IQ4_XS): row m's fp32 x as [16-byte piece][block] at
+// m nb KB, then the counter.
+__host__ __device__ constexpr int wave_xf_flag_off(int nb, int m) { return m * nb * 1024; }
+__host__ __device__ constexpr int wave_xf_act_bytes(int nb, int m) { return m * nb * 1024 + 16; }
 
 // Q8_K activations staged as [piece i][block b][16 bytes]: the accessor of block b.
 struct ActPieces {
@@ -70,6 +78,14 @@ struct ActPieces {
   __device__ u32x4a4 bs8(int h) const { return *(const u32x4a4*)(bsums + 8 * h); }
   __device__ uint32_t bs2(int j) const { return *(const uint32_t*)(bsums + 2 * j); }
   __device__ float4 x4(int) const { return float4{0.0f, 0.0f, 0.0f, 0.0f}; }
+};
+
+// fp32 activations staged as [16-byte piece][block]: the accessor of block b (consecutive lanes
+// read consecutive 16-byte words).
+struct ActXPieces {
+  const float* x;  // piece 0 of the block
+  int stride;      // floats between pieces (4 nb)
+  __device__ float4 x4(int off) const { return *(const float4*)(x + (off >> 2) * stride); }
 };
 
 typedef __attribute__((address_space(3))) int lds_int;
@@ -91,6 +107,8 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
                                           const int16_t* __restrict__ abs_, int wg, int n_wg) {
   using L = Lpb<TYPE>;
   static_assert(!ACTREG || MAXM == 1, "activations in registers for one row only");
+  constexpr bool kXF = TYPE == T_IQ4_XS;  // float activations (IQ4_XS multiplies them unquantized)
+  static_assert(!kXF || (!FUSEQ && !ACTREG), "float activations are staged, not quantized");
   constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
   constexpr int R = 64 / NB, kRounds = NB / 4, kRowAct = wave_row_act(NB), K = NB * QK;
   if constexpr (MAXM == 1) M = 1;  // constant LDS offsets for the one-row kernel
@@ -101,9 +119,10 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   const auto act_q = [&](int m) { return smem + kRowAct * m; };
   const auto act_bs = [&](int m) { return (int16_t*)(smem + kRowAct * m + wave_bs_off(NB)); };
   const auto act_d = [&](int m) { return (float*)(smem + kRowAct * m + wave_d_off(NB)); };
-  lds_int* flag = (lds_int*)(lds_u8*)(smem + wave_flag_off(NB, M));
+  lds_int* flag = (lds_int*)(lds_u8*)(smem + (kXF ? wave_xf_flag_off(NB, M) : wave_flag_off(NB, M)));
   float* xs = (float*)(smem + wave_x_off(NB, M));  // fp32 x: row m at xs + m K
-  uint8_t* wreg = smem + wave_act_bytes(NB, FUSEQ, M) + wave * wave_region_bytes<TYPE, NB, MAXM>();
+  uint8_t* wreg = smem + (kXF ? wave_xf_act_bytes(NB, M) : wave_act_bytes(NB, FUSEQ, M)) +
+                  wave * wave_region_bytes<TYPE, NB, MAXM>();
   float* Vbuf = (float*)(wreg + kStage);  // row m's block values at Vbuf + 64 m
   float* Dbuf = Vbuf + 64 * MAXM;
 
@@ -116,7 +135,15 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   const bool stager = wave < nq;
   constexpr int kQ = NB / 4, kBs = (NB * 2 + 63) / 64, kPer = kQ + kBs + 1;  // gather copies per row
   if (stager) {
-    if constexpr (FUSEQ) {
+    if constexpr (kXF) {
+      // float x as [16-byte piece][block]: copy j of row m moves slots s = 64 j + lane (piece
+      // s / NB of block s % NB)
+      for (int jm = wave; jm < NB * M; jm += nq) {
+        const int m = jm / NB, j = jm % NB, sl = 64 * j + lane;
+        copy16_to_lds((const void*)(x + (size_t)m * K + (sl % NB) * QK + 4 * (sl / NB)),
+                      lds_addr(smem + m * NB * 1024) + 1024u * (uint32_t)j);
+      }
+    } else if constexpr (FUSEQ) {
       for (int r = wave; r < kRounds * M; r += nq) {
         const int m = r / kRounds, g0 = 4 * (r % kRounds);
         for (int g = g0; g < g0 + 4; ++g)
@@ -228,11 +255,14 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
 
   const int b = lane % NB;
   ActPieces ap[MAXM];
+  ActXPieces xp[MAXM];
 #pragma unroll
   for (int m = 0; m < MAXM; ++m) {
     ap[m].q = (const int8_t*)(act_q(m) + b * 16);
     ap[m].stride = NB * 16;
     ap[m].bsums = act_bs(m) + b * 16;
+    xp[m].x = (const float*)(smem + m * NB * 1024) + 4 * b;
+    xp[m].stride = 4 * NB;
   }
   // fold lanes: lane l folds row l % R of the set against activation row l / R
   const int fr = lane % R, fm = lane / R;
@@ -251,7 +281,9 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
     }
     wait_vmcnt(0);
     float V[MAXM], D;
-    if constexpr (ACTREG)
+    if constexpr (kXF)
+      L::template compute<MAXM, ActXPieces>(wreg, jl * L::kBytes, xp, M, V, D);
+    else if constexpr (ACTREG)
       L::template compute<1, ActRegs>(wreg, jl * L::kBytes, &areg, 1, V, D);
     else
       L::template compute<MAXM, ActPieces>(wreg, jl * L::kBytes, ap, M, V, D);
@@ -274,7 +306,7 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
 #pragma unroll
         for (int i = 0; i < kC; ++i) {
           vv[i] = Vbuf[64 * fm + fr * NB + bb + i];
-          xx[i] = xd[bb + i];
+          xx[i] = kXF ? 0.0f : xd[bb + i];
           dd[i] = L::kHasD ? Dbuf[fr * NB + bb + i] : 0.0f;
         }
 #pragma unroll
@@ -360,11 +392,13 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_pairs_kernel(
 template <int TYPE, int NB, bool FUSEQ, int MAXM>
 int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                   int M, int N, hipStream_t stream) {
-  constexpr bool kReg = TYPE != T_Q6_K && MAXM == 1;  // Q6_K's compute leaves no room for them
+  constexpr bool kXF = TYPE == T_IQ4_XS;
+  // activation registers: not for Q6_K (its compute leaves no room for them) or float x
+  constexpr bool kReg = !kXF && TYPE != T_Q6_K && MAXM == 1;
   constexpr int R = 64 / NB;
   const int ncu = cu_count();
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
-  const int act_lds = wave_act_bytes(NB, FUSEQ, M);
+  const int act_lds = kXF ? wave_xf_act_bytes(NB, M) : wave_act_bytes(NB, FUSEQ, M);
   const int region = wave_region_bytes<TYPE, NB, MAXM>();
   const int fit = (kWaveLds - act_lds) / region;
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
@@ -398,9 +432,13 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
 template <int TYPE, int NB, int MAXM>
 int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                   int M, int N, hipStream_t stream) {
-  return act.q == nullptr
-             ? launch_wave_t<TYPE, NB, true, MAXM>(w, row_bytes, act, y, ldy, M, N, stream)
-             : launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream);
+  if constexpr (TYPE == T_IQ4_XS)  // float activations, staged unquantized
+    return act.q == nullptr ? launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream)
+                            : -1;
+  else
+    return act.q == nullptr
+               ? launch_wave_t<TYPE, NB, true, MAXM>(w, row_bytes, act, y, ldy, M, N, stream)
+               : launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
 // One activation row: every nb the kernel is built for. Two to four rows: 8-, 16- and 32-block
@@ -414,7 +452,7 @@ template <int TYPE, int NB>
 int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                    int M, int N, hipStream_t stream) {
   if (M == 1) return launch_wave_m<TYPE, NB, 1>(w, row_bytes, act, y, ldy, M, N, stream);
-  if constexpr (NB == 8 || NB == 16 || NB == 32) {
+  if constexpr (TYPE != T_IQ4_XS && (NB == 8 || NB == 16 || NB == 32)) {
     if (M == 2) return launch_wave_m<TYPE, NB, 2>(w, row_bytes, act, y, ldy, M, N, stream);
     if (M == 3 || (M == 4 && TYPE == T_Q4_K))
       return launch_wave_m<TYPE, NB, 4>(w, row_bytes, act, y, ldy, M, N, stream);
@@ -577,6 +615,12 @@ int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Ac
     case T_Q4_K: return launch_wave_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q8_0: return launch_wave_type<T_Q8_0>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q6_K: return launch_wave_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_IQ4_XS:
+      // one row on float activations; below ~4 MB of weight the resident kernel is faster
+      // (measured on MI355X, the same bits: 14336 x 4096 12.9 vs 17.7 us, 4096 x 14336 15.7 vs
+      // 24.5, the 128256 x 4096 head 79.3 vs 92, 4096 x 4096 6.5 vs 7.1; 1024 x 4096 4.9 vs 4.7)
+      if (m_rows != 1 || (long long)n_rows * row_bytes < kWaveIq4MinBytes) return -1;
+      return launch_wave_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }
 }

@@ -134,3 +134,22 @@ def test_decode_four_rows_on_the_decode_kernels(gpu, oracle, ggml_type, n, k) ->
         run_rows(gpu, oracle, ggml_type, n, k, 4, seed=n + k + 40)
     finally:
         gpu.set_fused_max_tokens(before)
+
+
+# IQ4_XS on float activations (one row, weights of 4 MB and more): every IQ4_XS kernel sums in one
+# order, so the one-row result equals row 0 of a two-row call (the pipelined kernel) bit for bit
+# (the float64 bound of that order is tested with the other decode kernels); shapes past one pass
+# (row sets), 56- and 64-block rows, and the 4 MB boundary on either side.
+IQ4_CASES = [(14336, 4096), (4096, 14336), (30000, 4096), (2000, 16384), (7710, 1024),
+             (7711, 1024), (4096, 4096)]
+
+
+@pytest.mark.parametrize("n,k", IQ4_CASES)
+def test_one_row_iq4_xs_equals_two_row_call(gpu, n, k) -> None:
+    w = dev(S.packed_weight(D.IQ4_XS, n, k, seed=n + k))
+    x2 = S.activations(2, k, seed=n + 1)
+    one = host(gpu.matmul(D.IQ4_XS, w, dev(x2[:1]), n, k))
+    two = host(gpu.matmul(D.IQ4_XS, w, dev(x2), n, k))
+    assert_bit_exact(one, two[:1])
+    f32 = host(gpu.gemv_f32(D.IQ4_XS, w, dev(x2[:1]), n, k))
+    assert_bit_exact(f32, one)
