@@ -1,7 +1,8 @@
 // Decode GEMV for one activation row in the shape of the read floor: one workgroup per CU whose
 // waves request every byte of their rows at their first instructions, then compute each row set
 // as it lands. y[n] = sum_k x[k] * W[n, k] for K-quant / Q8_0 weights with nb = K / 256 in
-// {4, 8, 16, 32, 56, 64}, and for IQ4_XS on float activations (one row).
+// {4, 8, 16, 32, 56, 64}, and on float activations (one row): IQ4_XS and the fp32-activation
+// forms of the K-quants and Q8_0.
 //
 // Memory. Wave v of a workgroup owns R = 64 / nb consecutive rows (64 blocks, or one row of 56
 // with eight lanes idle; one byte range, 16-byte aligned because row_bytes is) and issues all of
@@ -64,10 +65,14 @@ __host__ __device__ constexpr int wave_x_off(int nb, int m) { return wave_flag_o
 __host__ __device__ constexpr int wave_act_bytes(int nb, bool fuseq, int m = 1) {
   return wave_x_off(nb, m) + (fuseq ? m * nb * 1024 : 0);
 }
-// Float activations kept as they are (IQ4_XS): row m's fp32 x as [16-byte piece][block] at
-// m nb KB, then the counter.
-__host__ __device__ constexpr int wave_xf_flag_off(int nb, int m) { return m * nb * 1024; }
-__host__ __device__ constexpr int wave_xf_act_bytes(int nb, int m) { return m * nb * 1024 + 16; }
+// Float activations kept as they are (IQ4_XS and the fp32-activation types): per row, fp32 x as
+// [16-byte piece][block] (nb KB), then for the fp32-activation types the sixteen sums of 16 of each
+// block ([block][16] floats); after the rows, the counter.
+__host__ __device__ constexpr int wave_xf_row(int nb, bool sums) { return nb * (sums ? 1088 : 1024); }
+__host__ __device__ constexpr int wave_xf_flag_off(int nb, int m, bool sums) { return m * wave_xf_row(nb, sums); }
+__host__ __device__ constexpr int wave_xf_act_bytes(int nb, int m, bool sums) {
+  return m * wave_xf_row(nb, sums) + 16;
+}
 
 // Q8_K activations staged as [piece i][block b][16 bytes]: the accessor of block b.
 struct ActPieces {
@@ -83,9 +88,12 @@ struct ActPieces {
 // fp32 activations staged as [16-byte piece][block]: the accessor of block b (consecutive lanes
 // read consecutive 16-byte words).
 struct ActXPieces {
-  const float* x;  // piece 0 of the block
-  int stride;      // floats between pieces (4 nb)
+  const float* x;     // piece 0 of the block
+  int stride;         // floats between pieces (4 nb)
+  const float* sums;  // the block's sixteen sums of 16 (fp32-activation types)
   __device__ float4 x4(int off) const { return *(const float4*)(x + (off >> 2) * stride); }
+  __device__ float4 s4(int c) const { return *(const float4*)(sums + 4 * c); }  // sums 4c .. 4c + 3
+  __device__ float s1(int j) const { return sums[j]; }
 };
 
 typedef __attribute__((address_space(3))) int lds_int;
@@ -107,7 +115,9 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
                                           const int16_t* __restrict__ abs_, int wg, int n_wg) {
   using L = Lpb<TYPE>;
   static_assert(!ACTREG || MAXM == 1, "activations in registers for one row only");
-  constexpr bool kXF = TYPE == T_IQ4_XS;  // float activations (IQ4_XS multiplies them unquantized)
+  // float activations, unquantized (IQ4_XS, the fp32-activation types; these also use sums of 16)
+  constexpr bool kXF = ActTraits<TYPE>::kFloat, kSums = ActTraits<TYPE>::kSums;
+  constexpr int kXRow = wave_xf_row(NB, kSums);
   static_assert(!kXF || (!FUSEQ && !ACTREG), "float activations are staged, not quantized");
   constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
   constexpr int R = 64 / NB, kRounds = NB / 4, kRowAct = wave_row_act(NB), K = NB * QK;
@@ -119,9 +129,10 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   const auto act_q = [&](int m) { return smem + kRowAct * m; };
   const auto act_bs = [&](int m) { return (int16_t*)(smem + kRowAct * m + wave_bs_off(NB)); };
   const auto act_d = [&](int m) { return (float*)(smem + kRowAct * m + wave_d_off(NB)); };
-  lds_int* flag = (lds_int*)(lds_u8*)(smem + (kXF ? wave_xf_flag_off(NB, M) : wave_flag_off(NB, M)));
+  lds_int* flag =
+      (lds_int*)(lds_u8*)(smem + (kXF ? wave_xf_flag_off(NB, M, kSums) : wave_flag_off(NB, M)));
   float* xs = (float*)(smem + wave_x_off(NB, M));  // fp32 x: row m at xs + m K
-  uint8_t* wreg = smem + (kXF ? wave_xf_act_bytes(NB, M) : wave_act_bytes(NB, FUSEQ, M)) +
+  uint8_t* wreg = smem + (kXF ? wave_xf_act_bytes(NB, M, kSums) : wave_act_bytes(NB, FUSEQ, M)) +
                   wave * wave_region_bytes<TYPE, NB, MAXM>();
   float* Vbuf = (float*)(wreg + kStage);  // row m's block values at Vbuf + 64 m
   float* Dbuf = Vbuf + 64 * MAXM;
@@ -141,7 +152,7 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
       for (int jm = wave; jm < NB * M; jm += nq) {
         const int m = jm / NB, j = jm % NB, sl = 64 * j + lane;
         copy16_to_lds((const void*)(x + (size_t)m * K + (sl % NB) * QK + 4 * (sl / NB)),
-                      lds_addr(smem + m * NB * 1024) + 1024u * (uint32_t)j);
+                      lds_addr(smem + m * kXRow) + 1024u * (uint32_t)j);
       }
     } else if constexpr (FUSEQ) {
       for (int r = wave; r < kRounds * M; r += nq) {
@@ -242,13 +253,38 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
     }
+    if constexpr (kSums) {
+      // sum j of block b: the pieces 4j .. 4j + 3 come from every stager's copies, so once all
+      // have counted; each piece (x0 + x1) + (x2 + x3), then (p0 + p1) + (p2 + p3), the order of
+      // the pipelined kernel's staging
+      __builtin_amdgcn_wave_barrier();
+      if (lane == 0) __hip_atomic_fetch_add(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      int sspin = 0;
+      while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nq &&
+             ++sspin < kWaveSpinLimit)
+        __builtin_amdgcn_s_sleep(1);
+      if (sspin >= kWaveSpinLimit) return;  // the compute waves then give up too (NaN)
+      for (int r = wave * 64 + lane; r < M * NB * 16; r += nq * 64) {
+        const int m = r / (NB * 16), bb = (r / 16) % NB, j = r % 16;
+        const float* xr = (const float*)(smem + m * kXRow);
+        float ps[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 v = *(const float4*)(xr + 4 * ((4 * j + i) * NB + bb));
+          ps[i] = (v.x + v.y) + (v.z + v.w);
+        }
+        ((float*)(smem + m * kXRow + NB * 1024))[bb * 16 + j] = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the sums are written
+    }
     __builtin_amdgcn_wave_barrier();
     if (lane == 0) __hip_atomic_fetch_add(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
   if (!has_rows) return;
   int spin = 0;
-  while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nq &&
+  const int staged = kSums ? 2 * nq : nq;  // the stagers count twice when they also sum
+  while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < staged &&
          ++spin < kWaveSpinLimit)
     __builtin_amdgcn_s_sleep(1);
   const bool gave_up = spin >= kWaveSpinLimit;
@@ -261,8 +297,9 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
     ap[m].q = (const int8_t*)(act_q(m) + b * 16);
     ap[m].stride = NB * 16;
     ap[m].bsums = act_bs(m) + b * 16;
-    xp[m].x = (const float*)(smem + m * NB * 1024) + 4 * b;
+    xp[m].x = (const float*)(smem + m * kXRow) + 4 * b;
     xp[m].stride = 4 * NB;
+    xp[m].sums = (const float*)(smem + m * kXRow + NB * 1024) + 16 * b;
   }
   // fold lanes: lane l folds row l % R of the set against activation row l / R
   const int fr = lane % R, fm = lane / R;
@@ -392,13 +429,13 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_pairs_kernel(
 template <int TYPE, int NB, bool FUSEQ, int MAXM>
 int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                   int M, int N, hipStream_t stream) {
-  constexpr bool kXF = TYPE == T_IQ4_XS;
+  constexpr bool kXF = ActTraits<TYPE>::kFloat, kSums = ActTraits<TYPE>::kSums;
   // activation registers: not for Q6_K (its compute leaves no room for them) or float x
   constexpr bool kReg = !kXF && TYPE != T_Q6_K && MAXM == 1;
   constexpr int R = 64 / NB;
   const int ncu = cu_count();
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
-  const int act_lds = kXF ? wave_xf_act_bytes(NB, M) : wave_act_bytes(NB, FUSEQ, M);
+  const int act_lds = kXF ? wave_xf_act_bytes(NB, M, kSums) : wave_act_bytes(NB, FUSEQ, M);
   const int region = wave_region_bytes<TYPE, NB, MAXM>();
   const int fit = (kWaveLds - act_lds) / region;
   const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
@@ -432,7 +469,7 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
 template <int TYPE, int NB, int MAXM>
 int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                   int M, int N, hipStream_t stream) {
-  if constexpr (TYPE == T_IQ4_XS)  // float activations, staged unquantized
+  if constexpr (ActTraits<TYPE>::kFloat)  // float activations, staged unquantized
     return act.q == nullptr ? launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream)
                             : -1;
   else
@@ -452,7 +489,7 @@ template <int TYPE, int NB>
 int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                    int M, int N, hipStream_t stream) {
   if (M == 1) return launch_wave_m<TYPE, NB, 1>(w, row_bytes, act, y, ldy, M, N, stream);
-  if constexpr (TYPE != T_IQ4_XS && (NB == 8 || NB == 16 || NB == 32)) {
+  if constexpr (!ActTraits<TYPE>::kFloat && (NB == 8 || NB == 16 || NB == 32)) {
     if (M == 2) return launch_wave_m<TYPE, NB, 2>(w, row_bytes, act, y, ldy, M, N, stream);
     if (M == 3 || (M == 4 && TYPE == T_Q4_K))
       return launch_wave_m<TYPE, NB, 4>(w, row_bytes, act, y, ldy, M, N, stream);
@@ -621,6 +658,18 @@ int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Ac
       // 24.5, the 128256 x 4096 head 79.3 vs 92, 4096 x 4096 6.5 vs 7.1; 1024 x 4096 4.9 vs 4.7)
       if (m_rows != 1 || (long long)n_rows * row_bytes < kWaveIq4MinBytes) return -1;
       return launch_wave_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    default: return -1;
+  }
+}
+
+int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+                         int n_rows, hipStream_t stream) {
+  if (n_rows < 1 || act.q != nullptr || ((uintptr_t)act.x & 15) != 0) return -1;
+  if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF) return -1;
+  switch (type) {
+    case T_Q4_K: return launch_wave_type<T_Q4_K_F>(w, row_bytes, act, y, n_rows, 1, n_rows, stream);
+    case T_Q6_K: return launch_wave_type<T_Q6_K_F>(w, row_bytes, act, y, n_rows, 1, n_rows, stream);
+    case T_Q8_0: return launch_wave_type<T_Q8_0_F>(w, row_bytes, act, y, n_rows, 1, n_rows, stream);
     default: return -1;
   }
 }

@@ -106,6 +106,19 @@ def test_gemv_f32_keeps_activations_unquantized(gpu, t) -> None:
         assert e_q8k > 100 * e_f32, (e_q8k, e_f32)
 
 
+@pytest.mark.parametrize("t", [D.Q8_0, D.Q4_K, D.Q6_K])
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336), (1000, 2048), (30000, 4096),
+                                 (5, 16384), (777, 1024)])
+def test_gemv_f32_one_row_equals_two_row_call(gpu, t, n, k) -> None:
+    # one row takes the floor-shaped kernel (float x staged as [piece][block] with its sums of 16),
+    # two rows the pipelined kernel: one summation order, the same bits for the shared row
+    w = dev(S.packed_weight(t, n, k, seed=7700 + n + t))
+    x2 = S.activations(2, k, seed=7701 + k)
+    one = host(gpu.gemv_f32(t, w, dev(x2[:1]), n, k))
+    two = host(gpu.gemv_f32(t, w, dev(x2), n, k))
+    assert np.array_equal(one.view(np.uint32), two[:1].view(np.uint32))
+
+
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (333, 2304, 1), (30000, 512, 1), (700, 4096, 3)])
 def test_gemv_f32_iq4_xs_equals_matmul(gpu, n, k, m) -> None:
     # IQ4_XS multiplies float activations on both paths, every kernel in one summation order (one
