@@ -858,21 +858,22 @@ int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float
   Act act;
   act.q = nullptr, act.d = nullptr, act.bsums = nullptr, act.x = x;
   act.k = k, act.nb = k / QK, act.xsplit = nullptr;
-  // one row: the floor-shaped kernel where it applies (the same bits as the pipelined kernel;
-  // measured on MI355X: Q4_K 14336 x 4096 11.3 vs 17.2 us, 4096 x 4096 5.7 vs 11.1, Q8_0 4096 x
-  // 4096 7.0 vs 11.9, Q6_K 4096 x 14336 18.7 vs 27.7, the 128256 x 4096 head 83 vs 94)
-  if (m_rows == 1 && type != T_IQ4_XS &&
-      launch_gemv_wave_f32(type, w, row_bytes, act, y, n_rows, stream) == 0)
+  // the floor-shaped kernel where it applies (the same bits as the pipelined kernel; measured on
+  // MI355X, one row: Q4_K 14336 x 4096 11.3 vs 17.2 us, 4096 x 4096 5.7 vs 11.1, Q8_0 4096 x 4096
+  // 7.0 vs 11.9, Q6_K 4096 x 14336 18.7 vs 27.7, the 128256 x 4096 head 83 vs 94; four rows Q4_K
+  // 14336 x 4096 31.2 vs 50.3)
+  if (type != T_IQ4_XS &&
+      launch_gemv_wave_f32(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream) == 0)
     return 0;
   switch (type) {
     case T_Q4_K: return launch_lpb_type<T_Q4_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q6_K: return launch_lpb_type<T_Q6_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q8_0: return launch_lpb_type<T_Q8_0_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_IQ4_XS:
-      // IQ4_XS always multiplies float activations; one row takes the kernels mxa_gemm uses for it
-      // (the same summation order in every kernel, so the same bits)
-      if (m_rows == 1 && (launch_gemv_wave(type, w, row_bytes, act, y, n_rows, stream) == 0 ||
-                          launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0))
+      // IQ4_XS always multiplies float activations: the kernels mxa_gemm uses for it (the same
+      // summation order in every kernel, so the same bits)
+      if (launch_gemv_wave_m(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream) == 0 ||
+          (m_rows == 1 && launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0))
         return 0;
       return launch_lpb_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;

@@ -483,15 +483,18 @@ int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* 
 // vs 6.5 us, 14336 x 4096 8.5 vs 10.7, 28672 x 4096 13.4 vs 19.3; Q6_K 4096 x 4096 6.5 vs 7.9;
 // Q8_0 6.6 vs 7.4. Three rows: Q4_K 4096 x 4096 6.5 vs 7.5, 14336 x 4096 12.0 vs 12.2, 28672 x
 // 4096 18.4 vs 21.0; Q6_K 4096 x 4096 8.0 vs 8.9, 14336 x 4096 18.4 vs 19.8; Q8_0 7.9 vs 8.2.
-// Four rows for Q4_K only (14336 x 4096 13.7 vs 16.2 us; Q8_0 11.5 vs 9.0 and Q6_K 14336 x 4096
-// 23.6 vs 22.1 stay pipelined).
+// Four rows for Q4_K (14336 x 4096 13.7 vs 16.2 us; Q8_0 11.5 vs 9.0 and Q6_K 14336 x 4096
+// 23.6 vs 22.1 stay pipelined). Float activations (IQ4_XS, the fp32-activation forms), two to
+// four rows: Q4_K 14336 x 4096 16.9 / 24.6 / 31.2 vs 26.3 / 35.8 / 50.3 us, Q6_K 14336 x 4096
+// 20.4 / 28 / 40 vs 28.7 / 38.8 / 58.9, IQ4_XS 14336 x 4096 22.8 / 27.7 / 37.8 vs 31.9 / 43.3 /
+// 50.3; Q8_0 two rows only (4096 x 4096 10.8 vs 13.4; three rows 15.2 vs 14.5).
 template <int TYPE, int NB>
 int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
                    int M, int N, hipStream_t stream) {
   if (M == 1) return launch_wave_m<TYPE, NB, 1>(w, row_bytes, act, y, ldy, M, N, stream);
-  if constexpr (!ActTraits<TYPE>::kFloat && (NB == 8 || NB == 16 || NB == 32)) {
+  if constexpr (NB == 8 || NB == 16 || NB == 32) {
     if (M == 2) return launch_wave_m<TYPE, NB, 2>(w, row_bytes, act, y, ldy, M, N, stream);
-    if (M == 3 || (M == 4 && TYPE == T_Q4_K))
+    if (TYPE != T_Q8_0_F && (M == 3 || (M == 4 && (TYPE == T_Q4_K || ActTraits<TYPE>::kFloat))))
       return launch_wave_m<TYPE, NB, 4>(w, row_bytes, act, y, ldy, M, N, stream);
   }
   return -1;
@@ -653,23 +656,24 @@ int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Ac
     case T_Q8_0: return launch_wave_type<T_Q8_0>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q6_K: return launch_wave_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_IQ4_XS:
-      // one row on float activations; below ~4 MB of weight the resident kernel is faster
+      // float activations; below ~4 MB of weight the resident kernel is faster (one row)
       // (measured on MI355X, the same bits: 14336 x 4096 12.9 vs 17.7 us, 4096 x 14336 15.7 vs
       // 24.5, the 128256 x 4096 head 79.3 vs 92, 4096 x 4096 6.5 vs 7.1; 1024 x 4096 4.9 vs 4.7)
-      if (m_rows != 1 || (long long)n_rows * row_bytes < kWaveIq4MinBytes) return -1;
+      if ((long long)n_rows * row_bytes < kWaveIq4MinBytes) return -1;
       return launch_wave_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }
 }
 
 int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
-                         int n_rows, hipStream_t stream) {
-  if (n_rows < 1 || act.q != nullptr || ((uintptr_t)act.x & 15) != 0) return -1;
+                         long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+  if (n_rows < 1 || m_rows < 1 || m_rows > 4 || act.q != nullptr || ((uintptr_t)act.x & 15) != 0)
+    return -1;
   if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF) return -1;
   switch (type) {
-    case T_Q4_K: return launch_wave_type<T_Q4_K_F>(w, row_bytes, act, y, n_rows, 1, n_rows, stream);
-    case T_Q6_K: return launch_wave_type<T_Q6_K_F>(w, row_bytes, act, y, n_rows, 1, n_rows, stream);
-    case T_Q8_0: return launch_wave_type<T_Q8_0_F>(w, row_bytes, act, y, n_rows, 1, n_rows, stream);
+    case T_Q4_K: return launch_wave_type<T_Q4_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q6_K: return launch_wave_type<T_Q6_K_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
+    case T_Q8_0: return launch_wave_type<T_Q8_0_F>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }
 }

@@ -140,10 +140,10 @@ int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Ac
 // The same for one activation row.
 int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
                      int n_rows, hipStream_t stream);
-// One row on float activations (the fp32-activation forms of Q4_K, Q6_K, Q8_0: d * sc * q met
-// by unquantized x) on the floor-shaped kernel; -1 where it does not apply.
+// The fp32-activation forms of Q4_K, Q6_K, Q8_0 (d * sc * q met by unquantized x) on the
+// floor-shaped kernel, m_rows <= 4; -1 where it does not apply.
 int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
-                         int n_rows, hipStream_t stream);
+                         long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Decode GEMV for one activation row on a workgroup-resident weight share (mxa_gemv_res.hip):
 // y[n] for n < n_rows. Quantizes act.x to Q8_K in the kernel when act.q == nullptr (IQ4_XS reads

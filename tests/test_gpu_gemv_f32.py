@@ -119,6 +119,21 @@ def test_gemv_f32_one_row_equals_two_row_call(gpu, t, n, k) -> None:
     assert np.array_equal(one.view(np.uint32), two[:1].view(np.uint32))
 
 
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n,k", [(14336, 4096), (8000, 2048), (3000, 8192)])
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_float_activation_rows_equal_single_rows(gpu, t, n, k, m) -> None:
+    # two to four float-activation rows in one call (the floor-shaped kernel's multi-row forms)
+    # give each row the bits of that row alone (IQ4_XS through matmul: it always keeps x float)
+    w = dev(S.packed_weight(t, n, k, seed=7800 + n + t + m))
+    x = S.activations(m, k, seed=7801 + m)
+    call = gpu.matmul if t == D.IQ4_XS else gpu.gemv_f32
+    rows = host(call(t, w, dev(x), n, k))
+    for r in range(m):
+        one = host(call(t, w, dev(x[r:r + 1]), n, k))
+        assert np.array_equal(rows[r:r + 1].view(np.uint32), one.view(np.uint32)), f"row {r}"
+
+
 @pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (333, 2304, 1), (30000, 512, 1), (700, 4096, 3)])
 def test_gemv_f32_iq4_xs_equals_matmul(gpu, n, k, m) -> None:
     # IQ4_XS multiplies float activations on both paths, every kernel in one summation order (one
