@@ -124,7 +124,8 @@ class HipPackedMoEExperts(nn.Module):
         """float32 (n_tokens, n_embd): the reference's `down.to(dtype) * weight` contributions
         `index_add_`ed in ascending expert order, in one launch."""
         shape = top_k_idx.shape
-        ids = top_k_idx.to(torch.int32).contiguous()
+        ids = top_k_idx if top_k_idx.dtype == torch.int32 else top_k_idx.to(torch.int32)
+        ids = ids.contiguous()
         if rows is not None:
             rows = rows.to(torch.int32).reshape(shape).contiguous()
         return self._gemm.moe_combine(down, ids, top_k_weights.contiguous(), rows,
@@ -137,21 +138,22 @@ class HipPackedMoEExperts(nn.Module):
         routing. None when a projection's shape does not suit that launch."""
         g = self._gemm
         gt, ut, dt = self.types
-        ids = top_k_idx.reshape(-1).to(torch.int32)
-        # the reference casts x to the layer dtype before each matmul (device_packed.py:54)
-        xs = x.to(self.dtype)
-        gate = g.matmul_moe_pairs(gt, self.gate_packed, ids, xs, self.ffn_len, self.n_embd)
+        ids = top_k_idx.to(torch.int32).contiguous()
+        # the reference casts x to the layer dtype before each matmul (device_packed.py:54); the
+        # kernels take float32, so the cast values are widened once for both projections
+        xs = x.to(self.dtype).to(torch.float32)
+        gate = g.matmul_moe_pairs(gt, self.gate_packed, ids.view(-1), xs, self.ffn_len, self.n_embd)
         if gate is None:
             return None
-        up = g.matmul_moe_pairs(ut, self.up_packed, ids, xs, self.ffn_len, self.n_embd)
+        up = g.matmul_moe_pairs(ut, self.up_packed, ids.view(-1), xs, self.ffn_len, self.n_embd)
         if up is None:
             return None
         act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
-        down = g.matmul_moe_pairs(dt, self.down_packed, ids, act, self.n_embd, self.ffn_len)
+        down = g.matmul_moe_pairs(dt, self.down_packed, ids.view(-1), act, self.n_embd, self.ffn_len)
         if down is None:
             return None
         if self._fused_combine(top_k_weights):
-            return self._combine(down, None, top_k_idx, top_k_weights).to(x.dtype)
+            return self._combine(down, None, ids, top_k_weights).to(x.dtype)
         w = top_k_weights.reshape(-1).unsqueeze(-1)
         contrib = (down.to(self.dtype) * w).to(torch.float32)  # slot order
         slot = torch.arange(ids.numel(), device=x.device)
