@@ -115,8 +115,10 @@ class HipPackedMoEExperts(nn.Module):
 
     def _fused_combine(self, top_k_weights: torch.Tensor) -> bool:
         """Whether the weighted combine runs as one `mxa_moe_combine` launch: float32 routing
-        weights, a float32 or bfloat16 layer dtype, at most 16 experts per token."""
+        weights, a float32 or bfloat16 layer dtype, at most 16 experts per token and 65535 tokens
+        (the launch's grid)."""
         return (top_k_weights.dtype == torch.float32 and top_k_weights.shape[-1] <= 16
+                and top_k_weights.shape[0] <= 65535
                 and self.dtype in (torch.float32, torch.bfloat16))
 
     def _combine(self, down: torch.Tensor, rows: torch.Tensor | None, top_k_idx: torch.Tensor,

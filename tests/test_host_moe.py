@@ -47,3 +47,19 @@ def test_combine_adds_in_ascending_expert_order() -> None:
         got = combine_in_expert_order(contrib, order, idx)
         want = reference_combine(per_pair, idx)
         assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def test_fused_combine_gate() -> None:
+    # the one-launch combine takes float32 weights, float32 / bfloat16 layers, at most 16 slots
+    # and 65535 tokens; anything else keeps the torch steps
+    import torch
+    from matricxon_amd.moe import HipPackedMoEExperts
+
+    mod = HipPackedMoEExperts.__new__(HipPackedMoEExperts)
+    mod.dtype = torch.bfloat16
+    assert mod._fused_combine(torch.zeros(4, 2))
+    assert not mod._fused_combine(torch.zeros(4, 2, dtype=torch.bfloat16))
+    assert not mod._fused_combine(torch.zeros(4, 17))
+    assert not mod._fused_combine(torch.zeros(65536, 2))
+    mod.dtype = torch.float16
+    assert not mod._fused_combine(torch.zeros(4, 2))
