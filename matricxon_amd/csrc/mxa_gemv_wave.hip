@@ -112,7 +112,8 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
                                           float* __restrict__ y, int N, int row_bytes, int waves,
                                           int nq, int M, int ldy, const int8_t* __restrict__ aq,
                                           const float* __restrict__ ad,
-                                          const int16_t* __restrict__ abs_, int wg, int n_wg) {
+                                          const int16_t* __restrict__ abs_, int wg, int n_wg,
+                                          int late = 0) {
   using L = Lpb<TYPE>;
   static_assert(!ACTREG || MAXM == 1, "activations in registers for one row only");
   // float activations, unquantized (IQ4_XS, the fp32-activation types; these also use sums of 16)
@@ -132,8 +133,15 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   lds_int* flag =
       (lds_int*)(lds_u8*)(smem + (kXF ? wave_xf_flag_off(NB, M, kSums) : wave_flag_off(NB, M)));
   float* xs = (float*)(smem + wave_x_off(NB, M));  // fp32 x: row m at xs + m K
-  uint8_t* wreg = smem + (kXF ? wave_xf_act_bytes(NB, M, kSums) : wave_act_bytes(NB, FUSEQ, M)) +
-                  wave * wave_region_bytes<TYPE, NB, MAXM>();
+  // late: the last `late` row waves have their regions in the fp32 x staging area, free once the
+  // stagers have quantized x, so those waves request their rows only then (more row waves than
+  // the LDS holds beside the staging area)
+  constexpr bool kLate = FUSEQ && !kXF && NB == 56;  // the launcher uses them for these alone
+  const int late_idx = kLate ? wave - (waves - late) : -1;
+  const bool late_wave = late_idx >= 0;
+  uint8_t* wreg = late_wave ? (uint8_t*)xs + late_idx * wave_region_bytes<TYPE, NB, MAXM>()
+                            : smem + (kXF ? wave_xf_act_bytes(NB, M, kSums) : wave_act_bytes(NB, FUSEQ, M)) +
+                                  wave * wave_region_bytes<TYPE, NB, MAXM>();
   float* Vbuf = (float*)(wreg + kStage);  // row m's block values at Vbuf + 64 m
   float* Dbuf = Vbuf + 64 * MAXM;
 
@@ -212,10 +220,11 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
                          lds_w + c * 1024);
     }
   };
-  if (has_rows) issue(set);
+  if (has_rows && !late_wave) issue(set);
 
   if (stager) {
-    wait_vmcnt(has_rows ? kCopies : 0);  // the activation copies, issued first, have landed
+    // the activation copies, issued first, have landed (a late wave has requested no rows yet)
+    wait_vmcnt(has_rows && !late_wave ? kCopies : 0);
     if constexpr (FUSEQ) {
       const int p = lane & 15;
       for (int r = wave; r < kRounds * M; r += nq) {
@@ -288,6 +297,7 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
          ++spin < kWaveSpinLimit)
     __builtin_amdgcn_s_sleep(1);
   const bool gave_up = spin >= kWaveSpinLimit;
+  if (late_wave) issue(set);  // the stagers are done with x
 
   const int b = lane % NB;
   ActPieces ap[MAXM];
@@ -368,7 +378,8 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
     int row_bytes, uint32_t pack, int ldy, const int8_t* __restrict__ aq,
     const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
   wave_rows<TYPE, NB, FUSEQ, ACTREG, MAXM, LOOP>(w, x, y, N, row_bytes, pack & 0xFF, (pack >> 8) & 0xFF,
-                                           pack >> 16, ldy, aq, ad, abs_, blockIdx.x, gridDim.x);
+                                           (pack >> 16) & 0xFF, ldy, aq, ad, abs_, blockIdx.x,
+                                           gridDim.x, (int)(pack >> 24));
 }
 
 // Several weights that share the activation row (q|k|v, gate|up), one launch: each weight's
@@ -438,7 +449,12 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   const int act_lds = kXF ? wave_xf_act_bytes(NB, M, kSums) : wave_act_bytes(NB, FUSEQ, M);
   const int region = wave_region_bytes<TYPE, NB, MAXM>();
   const int fit = (kWaveLds - act_lds) / region;
-  const int waves = min(min(kWaveMaxWaves, fit), (per_cu + R - 1) / R);
+  // with x quantized in the kernel, further row waves in the fp32 x staging area (they request
+  // their rows once x is quantized; 4096 x 14336 on MI355X: Q4_K 10.0 -> 8.95 us, Q6_K 14.9 ->
+  // 12.9, Q8_0 15.6 -> 13.6, Q6_K 2048 x 14336 10.2 -> 8.7); only 56-block rows stage x enough
+  const int late_fit = FUSEQ && !kXF && NB == 56 ? (M * NB * 1024) / region : 0;
+  const int waves = min(min(kWaveMaxWaves, fit + late_fit), (per_cu + R - 1) / R);
+  const int late = max(0, waves - fit);
   // More rows than one round of workgroups holds: one workgroup per CU whose waves take further
   // row sets, each requested once the previous set is computed (measured on MI355X against the
   // pipelined kernel and against rounds of workgroups: Q4_K 28672 x 4096 14.8 vs 17.1 and 15.7
@@ -456,12 +472,13 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   // row waves (quantizing a round is ~140 VALU: four rounds on one wave cost ~1 us at N = 1024)
   const int nq = min(kWaveMaxWaves, M * NB / 4);
   const int nw = max(waves, nq);
-  const int lds = act_lds + waves * region;  // row waves only
+  const int lds = act_lds + (waves - late) * region;  // row waves only
   auto kern = (long long)grid * waves * R < N ? gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, true>
                                               : gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, false>;
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N, (int)row_bytes,
-                     (uint32_t)waves | (uint32_t)nq << 8 | (uint32_t)M << 16, (int)ldy, act.q,
+                     (uint32_t)waves | (uint32_t)nq << 8 | (uint32_t)M << 16 | (uint32_t)late << 24,
+                     (int)ldy, act.q,
                      act.d, act.bsums);
   return 0;
 }
