@@ -136,7 +136,8 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   // late: the last `late` row waves have their regions in the fp32 x staging area, free once the
   // stagers have quantized x, so those waves request their rows only then (more row waves than
   // the LDS holds beside the staging area)
-  constexpr bool kLate = FUSEQ && !kXF && NB == 56;  // the launcher uses them for these alone
+  // the launcher uses them for these alone
+  constexpr bool kLate = FUSEQ && !kXF && (NB == 56 || (TYPE == T_Q6_K && MAXM == 4));
   const int late_idx = kLate ? wave - (waves - late) : -1;
   const bool late_wave = late_idx >= 0;
   uint8_t* wreg = late_wave ? (uint8_t*)xs + late_idx * wave_region_bytes<TYPE, NB, MAXM>()
@@ -451,8 +452,11 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
   const int fit = (kWaveLds - act_lds) / region;
   // with x quantized in the kernel, further row waves in the fp32 x staging area (they request
   // their rows once x is quantized; 4096 x 14336 on MI355X: Q4_K 10.0 -> 8.95 us, Q6_K 14.9 ->
-  // 12.9, Q8_0 15.6 -> 13.6, Q6_K 2048 x 14336 10.2 -> 8.7); only 56-block rows stage x enough
-  const int late_fit = FUSEQ && !kXF && NB == 56 ? (M * NB * 1024) / region : 0;
+  // 12.9, Q8_0 15.6 -> 13.6, Q6_K 2048 x 14336 10.2 -> 8.7; Q6_K three rows 14336 x 4096 18.5 ->
+  // 15.9). Only 56-block rows and Q6_K's three rows gain: on Q4_K two rows 14336 x 4096 went
+  // from 8.5 to 10.4 us, elsewhere within 2%.
+  const int late_fit =
+      FUSEQ && !kXF && (NB == 56 || (TYPE == T_Q6_K && MAXM == 4)) ? (M * NB * 1024) / region : 0;
   const int waves = min(min(kWaveMaxWaves, fit + late_fit), (per_cu + R - 1) / R);
   const int late = max(0, waves - fit);
   // More rows than one round of workgroups holds: one workgroup per CU whose waves take further
