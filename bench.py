@@ -184,6 +184,50 @@ def capture(fn, steps: int, warmup: int):
     return graph
 
 
+def eager_us(fn, steps: int, warmup: int) -> float:
+    """Device microseconds per call of `steps` eager calls of fn(i), queued behind a GPU-side wait
+    long enough for the host to submit them all, so the events time the device alone. For library
+    calls kept out of HIP graphs (a reduction may record memset nodes there)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(LEAD_CYCLES * max(1, steps // 10))
+    e0.record()
+    for i in range(steps):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def vendor_ceilings(weights, copies: int, steps: int, warmup: int) -> dict:
+    """Vendor (torch / ROCm) kernels over the same rotated weight bytes, timed like the GEMV: a
+    device-to-device copy (graph replay; reads and writes the bytes), a sum of the bytes viewed as
+    int32 (eager, behind a GPU-side wait) and an empty kernel (graph replay: the fixed cost of one
+    launch). They bound from outside what one launch over these bytes achieves on this box."""
+    import torch
+
+    nbytes = weights[0].numel()
+    dst = torch.empty_like(weights[0])
+    copy_us = _graph_us(lambda i: dst.copy_(weights[i % copies]), steps, warmup)
+    sums = [torch.zeros((), dtype=torch.int64, device=dst.device)]
+    sum_us = eager_us(lambda i: sums.__setitem__(0, weights[i % copies].view(torch.int32).sum()),
+                      steps, warmup)
+    empty_us = _graph_us(lambda i: torch.cuda._sleep(0), steps, warmup)
+    del dst
+    return {
+        "vendor_copy_us": round(copy_us, 3),
+        "vendor_copy_read_gbs": round(nbytes / copy_us / 1e3, 1),
+        "vendor_copy_read_write_gbs": round(2 * nbytes / copy_us / 1e3, 1),
+        "vendor_sum_i32_us": round(sum_us, 3),
+        "vendor_sum_i32_read_gbs": round(nbytes / sum_us / 1e3, 1),
+        "empty_kernel_us": round(empty_us, 3),
+    }
+
+
 def _graph_us(fn, steps: int, warmup: int) -> float:
     """Device microseconds per step of a HIP-graph replay of `steps` calls of fn(i)."""
     graph = capture(fn, steps, warmup)
@@ -734,15 +778,21 @@ def main() -> int:
     if args.kernel_only and args.head:
         kernel_only_head(gemm, dev, args.steps)
 
-    # The read floor: one launch that only reads the same 33 MB (mxa_stream_read), over the same
-    # rotated copies, timed the same way. No single-launch kernel over these bytes can be faster.
-    floor_us = None
+    # The read floor: one launch of this library that only reads the same 33 MB
+    # (mxa_stream_read), over the same rotated copies, timed the same way; beside it, vendor
+    # kernels over the same bytes (a copy, an int32 sum) and an empty launch.
+    floor_us, vendor = None, {}
     if not args.kernel_only:
         sink = torch.zeros(1, dtype=torch.int32, device=dev)
         floor_us = _graph_us(lambda i: gemm.stream_read(weights[i % copies], sink), args.steps,
                              args.warmup)
         log(f"read floor: {floor_us:.2f} us/launch for the same bytes, "
             f"{weight_bytes() / floor_us / 1e3:.0f} GB/s")
+        vendor = vendor_ceilings(weights, copies, args.steps, args.warmup)
+        log(f"vendor kernels over the same bytes: copy {vendor['vendor_copy_us']:.2f} us "
+            f"({vendor['vendor_copy_read_gbs']:.0f} GB/s read), int32 sum "
+            f"{vendor['vendor_sum_i32_us']:.2f} us ({vendor['vendor_sum_i32_read_gbs']:.0f} GB/s), "
+            f"empty launch {vendor['empty_kernel_us']:.2f} us")
 
     if args.configs:
         bench_configs(gemm, dev, max(20, args.steps // 4), args.warmup)
@@ -816,6 +866,7 @@ def main() -> int:
             "read_floor_weight_gbs": round(weight_bytes() / floor_us / 1e3, 1),
             "read_floor_frac_of_peak": round(weight_bytes() / floor_us / 1e3 / HBM_PEAK_GBS, 4),
             "kernel_vs_floor": round(floor_us / r1["kernel_us"], 4),
+            **vendor,
         },
         "cpu_baseline": cpu,
     }

@@ -101,7 +101,9 @@ int mxa_gemv_f32(int ggml_type, const void *w, const float *x, float *y, int n_t
 
 /* mxa_gemm with no workspace argument and no device allocation anywhere on its path, for callers
  * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
- * it). No counterpart in the reference, whose mx_gemm mallocs its scratch per call. The workspace
+ * it). No counterpart in the reference, whose mx_gemm mallocs its scratch per call. The first call
+ * on a device does that device's set-up (the array's address, kernel attributes) and must not be
+ * under graph capture; calls after one eager call of the same shape may be captured. The workspace
  * mxa_gemm would take (mxa_workspace_bytes) is a file-scope device array of
  * MXA_STATIC_SCRATCH_BYTES per device, kept until the process ends; a call that needs more
  * returns -2. Calls on one device share that array: calls that overlap on one device (other
@@ -124,7 +126,8 @@ int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_t
  * rows [offsets[e], offsets[e + 1]) of x (n_rows, in_features) fp32, writing the same rows of
  * y (n_rows, out_features). `offsets` is a DEVICE int32 array of n_experts + 1 ascending values
  * from 0 to n_rows (the rows grouped by expert), so routing needs no host sync;
- * max_rows_per_expert is a host bound on any expert's rows (n_rows always is one). x == NULL:
+ * max_rows_per_expert sizes the launch (the rows an expert usually has, e.g. n_tokens); an
+ * expert with more rows is still computed whole, by looping. x == NULL:
  * `workspace` already holds the Q8_K activations of the n_rows rows (mxa_quantize_q8_k,
  * mxa_silu_mul_q8_k). workspace: mxa_quantize_q8_k's layout for n_rows rows. Each row equals
  * mxa_gemm of that row alone bit for bit. Q4_K, Q6_K, Q8_0 (IQ4_XS: -1).

@@ -322,10 +322,12 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
 }
 
 // Grouped MoE projection: expert e = blockIdx.y multiplies its rows [offsets[e], offsets[e + 1])
-// of the Q8_K activations (16 per blockIdx.z) by its packed weight (w + e * expert_stride); the
-// outputs go to the same rows of y. A workgroup whose expert has no row in its chunk exits. The
-// offsets come from the device (no host sync), so they are clamped to [0, total_rows): a bad
-// table gives wrong rows, never an access outside the activations or y.
+// of the Q8_K activations by its packed weight (w + e * expert_stride); the outputs go to the same
+// rows of y. The expert's rows are taken 16 at a time, chunk z by the workgroups of blockIdx.z ==
+// z mod gridDim.z, so every row is computed whatever the grid's depth (the host sizes it from a
+// bound it knows without a sync; an expert with more rows loops). A workgroup whose expert has no
+// row in its chunks exits. The offsets come from the device, so they are clamped to
+// [0, total_rows): a bad table gives wrong rows, never an access outside the activations or y.
 template <int TYPE, int kDecRT>
 __global__ __launch_bounds__(256) void moe_dec_kernel(const uint8_t* w, long long row_bytes,
                                                       long long expert_stride, Act act,
@@ -335,15 +337,16 @@ __global__ __launch_bounds__(256) void moe_dec_kernel(const uint8_t* w, long lon
   const int e = blockIdx.y;
   const int begin = min(max(offsets[e], 0), total_rows);
   const int end = min(max(offsets[e + 1], begin), total_rows);
-  const int p0 = begin + 16 * (int)blockIdx.z;
-  const int M = min(16, end - p0);
-  if (M <= 0) return;  // uniform over the workgroup
-  Act a = act;
-  a.q = act.q + (size_t)p0 * act.k;
-  a.d = act.d + (size_t)p0 * act.nb;
-  a.bsums = act.bsums + (size_t)p0 * act.nb * 16;
-  mdec_rows<TYPE, kDecRT>(w + (size_t)e * expert_stride, row_bytes, a, y + (size_t)p0 * ldy, ldy, M,
-                          N, blockIdx.x, gridDim.x);
+  for (int p0 = begin + 16 * (int)blockIdx.z; p0 < end; p0 += 16 * (int)gridDim.z) {
+    const int M = min(16, end - p0);  // uniform over the workgroup
+    Act a = act;
+    a.q = act.q + (size_t)p0 * act.k;
+    a.d = act.d + (size_t)p0 * act.nb;
+    a.bsums = act.bsums + (size_t)p0 * act.nb * 16;
+    mdec_rows<TYPE, kDecRT>(w + (size_t)e * expert_stride, row_bytes, a, y + (size_t)p0 * ldy, ldy,
+                            M, N, blockIdx.x, gridDim.x);
+    __syncthreads();  // the next chunk rewrites the LDS tiles this one read
+  }
 }
 
 template <int TYPE, int MT, int NT, int WAVES>

@@ -40,7 +40,10 @@ from matricxon_amd.quant_types import GEOMETRY
 
 _IQ4_XS = 23
 GEMV_BACKENDS = ("native", "numba")
-F32_GEMV_MAX_ROWS = 4  # "numba" backend: rows per call that take the fp32-activation GEMV
+# "numba" backend: rows per call that take the fp32-activation GEMV; the reference's
+# QuantizedLinear takes its GEMV only for one token (batch == 1 and seq_len == 1,
+# app/architectures/quantized_linear.py:94-98)
+F32_GEMV_MAX_ROWS = 1
 
 
 def gemv_backend() -> str:
@@ -150,12 +153,12 @@ class DevicePackedLinear(nn.Module):
         return self._dtype
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # The reference casts x to the layer dtype before its matmul (device_packed.py:54).
-        x = x.to(self._dtype)
         lead = x.shape[:-1]
         k = self.in_features
         if self.backend == "numba":
             return self.finish(self._forward_f32(x.reshape(-1, k)), lead)
+        # The reference casts x to the layer dtype before its matmul (device_packed.py:54).
+        x = x.to(self._dtype)
         ws = HANDOFF.claim(x) if self._ggml_type != _IQ4_XS else None
         if ws is not None:  # x came from a fused producer that also wrote its Q8_K blocks
             n = x.numel() // k
@@ -167,12 +170,13 @@ class DevicePackedLinear(nn.Module):
         return self.finish(y, lead)
 
     def _forward_f32(self, x2: torch.Tensor) -> torch.Tensor:
-        """The "numba" backend: float32 activations against the dequantized weight values, through
-        the fp32-activation GEMV for decode-sized calls, else a transient dequantization to the
-        layer dtype and a matmul (quantized_linear.py:101-106). (M, N) float32."""
+        """The "numba" backend, as the reference's QuantizedLinear without its native library
+        (quantized_linear.py:94-106): one token goes through the fp32-activation GEMV on x cast
+        straight to float32; more rows take a transient dequantization to the layer dtype and a
+        matmul of x in that dtype. (M, N) float32."""
         k, n = self.in_features, self.out_features
         if x2.shape[0] <= F32_GEMV_MAX_ROWS:
-            return self._gemm.gemv_f32(self._ggml_type, self.packed, x2, n, k)
+            return self._gemm.gemv_f32(self._ggml_type, self.packed, x2.to(torch.float32), n, k)
         weight = self._gemm.dequantize(self.packed, self._ggml_type).reshape(n, k).to(self._dtype)
         y = (x2.to(self._dtype) @ weight.T).to(torch.float32)
         del weight

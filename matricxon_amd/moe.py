@@ -98,7 +98,9 @@ class HipPackedMoEExperts(nn.Module):
         g = self._gemm
         # the reference casts x to the layer dtype before each matmul (device_packed.py:54)
         xs = x.to(self.dtype).index_select(0, pair_tok)  # each pair's token, by expert
-        bound = n_tokens  # an expert takes each token at most once
+        # the launch is sized for one row per token and expert; an expert that a token's routing
+        # names twice (the reference computes both slots) gets its extra rows by the kernel's loop
+        bound = n_tokens
         gt, ut, dt = self.types
         gate = g.matmul_moe(gt, self.gate_packed, xs, offsets, bound, self.ffn_len, n_embd)
         up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd)

@@ -177,3 +177,19 @@ def test_device_packed_linear_numba_backend(gpu, m) -> None:
     assert native.backend == "native"
     with pytest.raises(ValueError):
         DevicePackedLinear(dev(w), k, D.Q6_K, backend="cuda")
+
+
+def test_numba_backend_follows_the_reference_split(gpu) -> None:
+    # QuantizedLinear without its native library (quantized_linear.py:94-106): one token takes the
+    # GEMV on x cast straight to float32; two rows take the transient dequantization to the layer
+    # dtype and `x.to(dtype) @ weight.T`
+    n, k = 256, 2048
+    w = dev(S.packed_weight(D.Q4_K, n, k, seed=7600))
+    mod = DevicePackedLinear(w, k, D.Q4_K, dtype=torch.bfloat16, backend="numba")
+    x1 = dev(S.activations(1, k, seed=7601)).reshape(1, 1, k)
+    want1 = gpu.gemv_f32(D.Q4_K, w, x1.reshape(1, k), n, k).to(torch.bfloat16).reshape(1, 1, n)
+    assert torch.equal(mod(x1), want1)
+    x2 = dev(S.activations(2, k, seed=7602)).reshape(1, 2, k)
+    weight = gpu.dequantize(w, D.Q4_K).reshape(n, k).to(torch.bfloat16)
+    want2 = (x2.reshape(2, k).to(torch.bfloat16) @ weight.T).to(torch.float32).to(torch.bfloat16)
+    assert torch.equal(mod(x2), want2.reshape(1, 2, n))

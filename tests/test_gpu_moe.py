@@ -91,6 +91,23 @@ def test_grouped_rows_with_loose_bound(gpu, oracle) -> None:
                              oracle.gemm(t, w[e], x[off[e]:off[e + 1]], n, k), f"expert {e}")
 
 
+def test_grouped_rows_past_the_bound(gpu, oracle) -> None:
+    """max_rows_per_expert below an expert's count (a token routed twice to one expert gives it
+    more rows than tokens): the launch's chunks loop until every row is computed."""
+    counts = [40, 0, 3, 33]
+    n, k, t = 256, 1024, D.Q6_K
+    w = expert_weights(t, len(counts), n, k, seed=7)
+    x = S.activations(sum(counts), k, seed=8)
+    off = offsets_of(counts)
+    out = torch.full((sum(counts), n), float("nan"), dtype=torch.float32, device="cuda")
+    got = gpu.matmul_moe(t, torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(),
+                         torch.from_numpy(off).cuda(), 16, n, k, out=out).cpu().numpy()
+    for e in range(len(counts)):
+        if counts[e]:
+            assert_bit_exact(got[off[e]:off[e + 1]],
+                             oracle.gemm(t, w[e], x[off[e]:off[e + 1]], n, k), f"expert {e}")
+
+
 def test_route_pairs_on_device_matches_host() -> None:
     idx = torch.tensor([[3, 0], [1, 3], [0, 2], [3, 1]], device="cuda")
     order, offsets, pair_tok = route_pairs(idx, 5)
@@ -173,6 +190,23 @@ def test_module_all_tokens_on_one_expert() -> None:
     got = mod(x, tw, tidx)
     want = reference_forward(x, tw, tidx, per_expert, F.silu)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_module_repeated_expert_in_a_tokens_routing(dtype) -> None:
+    """Every token names expert 2 in both slots (and a few name expert 1 twice): expert 2 gets
+    2 * n_tokens rows, more than the launch is sized for; the reference computes both slots."""
+    types = (D.Q4_K, D.Q4_K, D.Q6_K)
+    n_tokens = 20
+    mod, per_expert = build_experts(types, 4, 512, 256, dtype, seed=31)
+    x = torch.from_numpy(S.activations(n_tokens, 512, seed=32)).cuda().to(dtype)
+    tidx = torch.full((n_tokens, 2), 2, dtype=torch.int64, device="cuda")
+    tidx[::7] = 1
+    tw = torch.rand(n_tokens, 2, generator=torch.Generator().manual_seed(33)).cuda()
+    got = mod(x, tw, tidx)
+    want = reference_forward(x, tw, tidx, per_expert, F.silu)
+    assert torch.equal(got.float().view(torch.int32), want.float().view(torch.int32)), \
+        f"max |diff| {(got.float() - want.float()).abs().max().item()}"
 
 
 def test_module_rejects_types_without_grouped_launch() -> None:

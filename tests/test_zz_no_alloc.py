@@ -67,3 +67,39 @@ def test_static_refuses_a_workspace_beyond_the_array(gpu) -> None:
     assert st == -2
     assert b"static scratch" in lib.mxa_last_error()
     assert bool((host(y) == 7.0).all())  # nothing was launched
+
+
+@pytest.mark.parametrize("t,n,k,m", [(D.Q4_K, 1024, 4096, 1), (D.Q4_K, 512, 4096, 16),
+                                     (D.IQ4_XS, 256, 4096, 20)])
+def test_static_under_graph_capture(gpu, t, n, k, m) -> None:
+    """A call captured into a HIP graph (after one eager call of the same shape on the device,
+    which does the per-device set-up) replays to mxa_gemm's bits, replay after replay, with eager
+    work of the program between the replays."""
+    lib = _lib.load()
+    w = dev(S.packed_weight(t, n, k, seed=90 + m))
+    x = dev(S.activations(m, k, seed=91))
+    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    want = host(gpu.matmul(t, w, x, n, k))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        assert lib.mxa_gemm_static(t, w.data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k,
+                                   _stream(y.device)) == 0
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(host(y)), bits(want))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = lib.mxa_gemm_static(t, w.data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k,
+                                 _stream(y.device))
+    assert st == 0, (st, lib.mxa_last_error())
+    x2 = dev(S.activations(max(1, m // 2), k, seed=92))
+    want2 = host(gpu.matmul(t, w, x2, n, k))
+    for r in range(3):
+        y.fill_(float("nan"))
+        other = host(_static(lib, t, w, x2, n, k))  # eager call on the same scratch array
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(host(y)), bits(want)), f"replay {r}"
+        assert np.array_equal(bits(other), bits(want2)), f"eager call before replay {r}"
+    del graph
