@@ -228,6 +228,52 @@ def vendor_ceilings(weights, copies: int, steps: int, warmup: int) -> dict:
     }
 
 
+def eager_module_call(gemm, dev, weights, copies: int, steps: int, warmup: int) -> dict:
+    """One eager call of a bfloat16 `DevicePackedLinear` (the reference's GPU layer dtype) on the
+    headline weight at M=1, as the reference's decode makes it (batch_decode.py:70-87 ->
+    llama.py:265-279): host microseconds per call (wall time of `steps` calls back to back, one
+    synchronization at the end) and device microseconds per call (HIP events around `steps` calls
+    queued behind a GPU-side wait). Beside it, the same call through the float32 kernel with the
+    casts a float32-only library needs (x to float32, y to bfloat16: two more launches). Calls
+    rotate over the weight copies, as the timed GEMV does."""
+    import torch
+
+    from matricxon_amd import synthetic as S
+    from matricxon_amd.device_packed import DevicePackedLinear
+
+    mods = [DevicePackedLinear(w, K, Q4_K, dtype=torch.bfloat16) for w in weights[:copies]]
+    x = torch.from_numpy(S.activations(1, K, seed=2)).to(dev).to(torch.bfloat16).reshape(1, 1, K)
+
+    def module(i):
+        return mods[i % copies](x)
+
+    def cast_path(i):
+        y = gemm.matmul(Q4_K, weights[i % copies], x.reshape(1, K).to(torch.float32), N, K)
+        return y.to(torch.bfloat16).reshape(1, 1, N)
+
+    def host_us(fn) -> float:
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            fn(i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / steps
+
+    same = torch.equal(module(0), cast_path(0))
+    res = {
+        "module_host_us": round(host_us(module), 2),
+        "module_device_us": round(eager_us(module, steps, warmup), 2),
+        "cast_path_host_us": round(host_us(cast_path), 2),
+        "cast_path_device_us": round(eager_us(cast_path, steps, warmup), 2),
+        "same_bits": bool(same),
+        "call": "DevicePackedLinear(Q4_K 14336x4096, dtype=bfloat16)(x bf16 (1, 1, 4096))",
+    }
+    del mods
+    return res
+
+
 def _graph_us(fn, steps: int, warmup: int) -> float:
     """Device microseconds per step of a HIP-graph replay of `steps` calls of fn(i)."""
     graph = capture(fn, steps, warmup)
@@ -794,6 +840,14 @@ def main() -> int:
             f"{vendor['vendor_sum_i32_us']:.2f} us ({vendor['vendor_sum_i32_read_gbs']:.0f} GB/s), "
             f"empty launch {vendor['empty_kernel_us']:.2f} us")
 
+    eager = None
+    if not args.kernel_only:
+        eager = eager_module_call(gemm, dev, weights, copies, args.steps, args.warmup)
+        log(f"eager bf16 module call, M=1: host {eager['module_host_us']:.1f} us, device "
+            f"{eager['module_device_us']:.2f} us per call (float32 kernel + casts: host "
+            f"{eager['cast_path_host_us']:.1f}, device {eager['cast_path_device_us']:.2f}); "
+            f"same bits: {eager['same_bits']}")
+
     if args.configs:
         bench_configs(gemm, dev, max(20, args.steps // 4), args.warmup)
 
@@ -869,6 +923,7 @@ def main() -> int:
             **vendor,
         },
         "cpu_baseline": cpu,
+        "eager_bf16_call": eager,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -85,6 +85,62 @@ int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_token
              int out_features, int in_features, void *workspace, size_t workspace_bytes,
              void *stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * bfloat16 activations and outputs. The reference's packed GPU module computes in its layer dtype,
+ * bfloat16 on a GPU (app/runtime/compute_device.py:74-78; app/architectures/device_packed.py:53-63:
+ * x.to(dtype), then F.linear in that dtype). These entry points take bfloat16 x (16-byte aligned)
+ * and write bfloat16 y (2-byte aligned), each output the float32 result of the float32 entry point
+ * on the widened x, rounded to nearest even (NaN -> 0x7FC0), as torch's float -> bfloat16 cast
+ * rounds it. No counterpart in the reference's C library (its native kernels are CPU float32). */
+
+/* Workspace bytes of the _bf16 entry points: Q8_0 / Q4_K / Q6_K the Q8_K activations for every
+ * n_tokens (x is quantized into them whenever the decode kernel that reads bfloat16 x itself does
+ * not take the call); IQ4_XS x widened to float32 (4 * n_tokens * in_features bytes) plus, from 17
+ * rows, the prefill split (mxa_workspace_bytes). mxa_gemm_multi_bf16 over both kinds needs the sum
+ * of the largest of each kind. Host-only. */
+size_t mxa_workspace_bytes_bf16(int ggml_type, int n_tokens, int in_features);
+
+/* mxa_gemm on bfloat16 x, writing bfloat16 y. */
+int mxa_gemm_bf16(int ggml_type, const void *w, const void *x, void *y, int n_tokens,
+                  int out_features, int in_features, void *workspace, size_t workspace_bytes,
+                  void *stream);
+
+/* mxa_gemm_multi on bfloat16 x, writing bfloat16 y (n_tokens, sum outs). */
+int mxa_gemm_multi_bf16(int n, const int *types, const void *const *ws, const int *outs,
+                        const void *x, void *y, int n_tokens, int in_features, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/* mxa_gemm_q8k writing bfloat16 y (K-quant and Q8_0 weights: the Q8_K activations are all the
+ * input). */
+int mxa_gemm_q8k_bf16(int ggml_type, const void *w, void *y, int n_tokens, int out_features,
+                      int in_features, const void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* mxa_gemm_multi_q8k writing bfloat16 y. */
+int mxa_gemm_multi_q8k_bf16(int n, const int *types, const void *const *ws, const int *outs,
+                            void *y, int n_tokens, int in_features, const void *workspace,
+                            size_t workspace_bytes, void *stream);
+
+/* mxa_quantize_q8_k of bfloat16 x (the values widened exactly). */
+int mxa_quantize_q8_k_bf16(const void *x, int n_tokens, int in_features, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
+/* RMSNorm of a bfloat16 layer with the steps of the reference's torch forward for bfloat16 x and
+ * weight (app/architectures/layers.py:77-81): x widened to float32, variance = the mean of x^2,
+ * out = bf16(bf16(x * rsqrt(variance + eps)) * weight), written to out (bfloat16, may be NULL) and
+ * its Q8_K blocks to the workspace (mxa_quantize_q8_k's layout). dim <= 16384; x, weight and out
+ * 8-byte aligned; else -1. The fused RMSNorm that `FusedOps.rms_norm` provides on the CPU
+ * (app/native/fused_ops.py:152-158), for the GPU's bfloat16 layers. */
+int mxa_rms_norm_q8_k_bf16(const void *x, const void *weight, float eps, int n_tokens, int dim,
+                           void *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* silu(gate) * up of a bfloat16 layer with torch's steps for bfloat16 tensors
+ * (app/architectures/layers.py:53-57: F.silu(gate) * up): out = bf16(bf16(g / (1 + expf(-g))) *
+ * u), written to out (bfloat16, contiguous, may be NULL) and its Q8_K blocks to the workspace.
+ * gate and up rows are ld >= dim values apart (ld % 4 == 0; operands 8-byte aligned; else -1). */
+int mxa_silu_mul_q8_k_bf16(const void *gate, const void *up, long long ld, int n_tokens, int dim,
+                           void *out, void *workspace, size_t workspace_bytes, void *stream);
+
 /* y (n_tokens, out_features) = x @ W.T with x kept in float32 (never quantized to Q8_K): each
  * weight value is its dequantized float (d * sc * q - dmin * m) meeting an unquantized activation,
  * the numerics of the reference's fp32-activation GEMV backend. Decode-sized calls: the

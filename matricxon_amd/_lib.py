@@ -38,6 +38,14 @@ EXPORTS = (
     "mxa_gather_rows",
     "mxa_stream_read",
     "mxa_last_error",
+    "mxa_workspace_bytes_bf16",
+    "mxa_gemm_bf16",
+    "mxa_gemm_multi_bf16",
+    "mxa_gemm_q8k_bf16",
+    "mxa_gemm_multi_q8k_bf16",
+    "mxa_quantize_q8_k_bf16",
+    "mxa_rms_norm_q8_k_bf16",
+    "mxa_silu_mul_q8_k_bf16",
 )
 
 _vp = ctypes.c_void_p
@@ -97,6 +105,22 @@ def load() -> ctypes.CDLL:
     lib.mxa_quantize_q8_k.restype = _i
     lib.mxa_rms_norm_q8_k.argtypes = [_vp, _vp, ctypes.c_float, _i, _i, _vp, _vp, _sz, _vp]
     lib.mxa_rms_norm_q8_k.restype = _i
+    lib.mxa_workspace_bytes_bf16.argtypes = [_i, _i, _i]
+    lib.mxa_workspace_bytes_bf16.restype = _sz
+    lib.mxa_gemm_bf16.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]
+    lib.mxa_gemm_bf16.restype = _i
+    lib.mxa_gemm_multi_bf16.argtypes = [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]
+    lib.mxa_gemm_multi_bf16.restype = _i
+    lib.mxa_gemm_q8k_bf16.argtypes = [_i, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]
+    lib.mxa_gemm_q8k_bf16.restype = _i
+    lib.mxa_gemm_multi_q8k_bf16.argtypes = [_i, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]
+    lib.mxa_gemm_multi_q8k_bf16.restype = _i
+    lib.mxa_quantize_q8_k_bf16.argtypes = [_vp, _i, _i, _vp, _sz, _vp]
+    lib.mxa_quantize_q8_k_bf16.restype = _i
+    lib.mxa_rms_norm_q8_k_bf16.argtypes = [_vp, _vp, ctypes.c_float, _i, _i, _vp, _vp, _sz, _vp]
+    lib.mxa_rms_norm_q8_k_bf16.restype = _i
+    lib.mxa_silu_mul_q8_k_bf16.argtypes = [_vp, _vp, _ll, _i, _i, _vp, _vp, _sz, _vp]
+    lib.mxa_silu_mul_q8_k_bf16.restype = _i
     lib.mxa_silu_mul_q8_k.argtypes = [_vp, _vp, _ll, _i, _i, _vp, _vp, _sz, _vp]
     lib.mxa_silu_mul_q8_k.restype = _i
     lib.mxa_dequantize.argtypes = [_i, _vp, _ll, _vp, _vp]

@@ -59,6 +59,7 @@ mxa::Act make_act(const float* x, const mxa::ActBuffers* a, int k) {
   act.k = k;
   act.nb = k / mxa::QK;
   act.xsplit = nullptr;
+  act.xbf16 = 0;
   return act;
 }
 
@@ -69,6 +70,163 @@ size_t q8k_part(bool any_q8k, int n_tokens, int k, int fmax) {
 }
 size_t split_part(bool any_iq4, int n_tokens, int k) {
   return any_iq4 && n_tokens >= mxa::kIq4MfmaMinRows ? mxa::iq4_prefill_workspace(n_tokens, k) : 0;
+}
+
+
+// Workspace parts of a call on bfloat16 x, each 256-byte aligned: the Q8_K activations (any
+// K-quant / Q8_0 weight: x is quantized into them whenever the floor-shaped decode kernel, which
+// reads bfloat16 x itself, does not take the call), then x widened to float32 (any IQ4_XS weight,
+// which multiplies float activations), then the IQ4_XS prefill split.
+size_t widen_part(bool any_iq4, int n_tokens, int k) {
+  return any_iq4 ? mxa::align256((size_t)n_tokens * k * 4) : 0;
+}
+
+int gemm_multi_core(int n, const int* types, const void* const* ws, const int* outs,
+                    const void* x, bool xbf16, mxa::YOut y, int n_tokens, int in_features,
+                    void* workspace, size_t workspace_bytes, hipStream_t s) {
+  if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr)
+    return MXA_ERR_UNSUPPORTED;
+  if (x == nullptr || (y.v & ~(uintptr_t)1) == 0 || n_tokens <= 0 || !aligned(x, 16) ||
+      !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  bool any_q8k = false, any_iq4 = false;
+  long long total = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!mxa_supports(types[i], in_features) || ws[i] == nullptr || outs[i] <= 0 ||
+        !aligned(ws[i], 4))
+      return MXA_ERR_UNSUPPORTED;
+    any_q8k |= needs_q8k(types[i]);
+    any_iq4 |= !needs_q8k(types[i]);
+    total += outs[i];
+  }
+  const int fmax = mxa::fused_max_rows();
+  const size_t q8k_bytes = xbf16 ? (any_q8k ? mxa::align256(mxa::act_bytes(n_tokens, in_features)) : 0)
+                                 : q8k_part(any_q8k, n_tokens, in_features, fmax);
+  const size_t widen_bytes = xbf16 ? widen_part(any_iq4, n_tokens, in_features) : 0;
+  const size_t split_bytes = split_part(any_iq4, n_tokens, in_features);
+  const size_t need = q8k_bytes + widen_bytes + split_bytes;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MXA_ERR_WORKSPACE;
+  mxa::DecodeSeg seg[4];
+  long long c0 = 0;
+  for (int i = 0; i < n; ++i) {
+    seg[i] = mxa::DecodeSeg{types[i], (const uint8_t*)ws[i],
+                            (long long)mxa_row_bytes(types[i], in_features), y.at(c0), outs[i]};
+    c0 += outs[i];
+  }
+  if (xbf16 && !any_iq4 && n_tokens <= fmax) {
+    // the floor-shaped decode kernel reads bfloat16 x and quantizes it itself (one launch)
+    mxa::Act a = make_act((const float*)x, nullptr, in_features);
+    a.xbf16 = 1;
+    const int st = n == 1 ? mxa::launch_gemv_wave_m(types[0], seg[0].w, seg[0].row_bytes, a, y,
+                                                    total, n_tokens, outs[0], s)
+                 : n_tokens == 1 ? mxa::launch_gemv_wave_multi(seg, n, a, s)
+                                 : -1;
+    if (st == 0) return check_launch();
+  }
+  const float* xf = xbf16 ? nullptr : (const float*)x;
+  if (widen_bytes > 0) {
+    float* wide = (float*)((uint8_t*)workspace + q8k_bytes);
+    mxa::launch_widen_bf16((const uint16_t*)x, wide, (long long)n_tokens * in_features, s);
+    xf = wide;
+  }
+  mxa::ActBuffers buf{};
+  const mxa::ActBuffers* abuf = nullptr;
+  if (q8k_bytes > 0) {
+    buf = mxa::act_layout(workspace, n_tokens, in_features);
+    abuf = &buf;
+    if (xbf16)
+      mxa::launch_quantize_q8k_bf16((const uint16_t*)x, buf, n_tokens, in_features, s);
+    else
+      mxa::launch_quantize_q8k(xf, buf, n_tokens, in_features, s);
+  }
+  const int qst = check_launch();
+  if (qst != MXA_OK) return qst;
+  mxa::Act act = make_act(xf, abuf, in_features);
+  if (split_bytes > 0) act.xsplit = (uint8_t*)workspace + q8k_bytes + widen_bytes;
+  if (n > 1 && !any_iq4 && n_tokens <= 16) {  // decode: one launch for all weights
+    int st = -1;
+    if (n_tokens <= fmax) {
+      st = mxa::launch_decode_multi(seg, n, act, total, n_tokens, s);
+    } else {
+      st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+      if (st != 0) st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
+    }
+    if (st == 0) return check_launch();
+  }
+  for (int i = 0; i < n; ++i) {
+    if (mxa::launch_matmul(types[i], seg[i].w, seg[i].row_bytes, act, seg[i].y, total, n_tokens,
+                           outs[i], s) != 0)
+      return MXA_ERR_UNSUPPORTED;
+    const int st = check_launch();
+    if (st != MXA_OK) return st;
+  }
+  return MXA_OK;
+}
+
+int gemm_q8k_core(int ggml_type, const void* w, const float* x, mxa::YOut y, int n_tokens,
+                  int out_features, int in_features, const void* workspace,
+                  size_t workspace_bytes, hipStream_t s) {
+  if (!mxa_supports(ggml_type, in_features) || w == nullptr || n_tokens <= 0 ||
+      out_features <= 0 || !aligned(w, 4) || !aligned(x, 16) || !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  mxa::ActBuffers buf{};
+  const mxa::ActBuffers* abuf = nullptr;
+  if (needs_q8k(ggml_type)) {
+    if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+      return MXA_ERR_WORKSPACE;
+    buf = mxa::act_layout((void*)workspace, n_tokens, in_features);
+    abuf = &buf;
+  } else if (x == nullptr) {
+    return MXA_ERR_UNSUPPORTED;
+  }
+  const mxa::Act act = make_act(x, abuf, in_features);
+  const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
+  if (mxa::launch_matmul(ggml_type, (const uint8_t*)w, rb, act, y, out_features, n_tokens,
+                         out_features, s) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
+int gemm_multi_q8k_core(int n, const int* types, const void* const* ws, const int* outs,
+                        mxa::YOut y, int n_tokens, int in_features, const void* workspace,
+                        size_t workspace_bytes, hipStream_t s) {
+  if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr || n_tokens <= 0 ||
+      !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  long long total = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!mxa_supports(types[i], in_features) || !needs_q8k(types[i]) || ws[i] == nullptr ||
+        outs[i] <= 0 || !aligned(ws[i], 4))
+      return MXA_ERR_UNSUPPORTED;
+    total += outs[i];
+  }
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+    return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers buf = mxa::act_layout((void*)workspace, n_tokens, in_features);
+  const mxa::Act act = make_act(nullptr, &buf, in_features);
+  mxa::DecodeSeg seg[4];
+  long long c0 = 0;
+  for (int i = 0; i < n; ++i) {
+    seg[i] = mxa::DecodeSeg{types[i], (const uint8_t*)ws[i],
+                            (long long)mxa_row_bytes(types[i], in_features), y.at(c0), outs[i]};
+    c0 += outs[i];
+  }
+  if (n > 1 && n_tokens <= 16) {  // one launch for the group
+    const int fmax = mxa::fused_max_rows();
+    int st = n_tokens <= fmax ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
+                              : mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+    if (st != 0 && n_tokens > fmax)
+      st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
+    if (st == 0) return check_launch();
+  }
+  for (int i = 0; i < n; ++i) {
+    if (mxa::launch_matmul(types[i], seg[i].w, seg[i].row_bytes, act, seg[i].y, total, n_tokens,
+                           outs[i], s) != 0)
+      return MXA_ERR_UNSUPPORTED;
+    const int st = check_launch();
+    if (st != MXA_OK) return st;
+  }
+  return MXA_OK;
 }
 
 }  // namespace
@@ -105,6 +263,24 @@ size_t mxa_workspace_bytes(int ggml_type, int n_tokens, int in_features) {
   return split_part(true, n_tokens, in_features);
 }
 
+size_t mxa_workspace_bytes_bf16(int ggml_type, int n_tokens, int in_features) {
+  if (!mxa_supports(ggml_type, in_features) || n_tokens <= 0) return 0;
+  if (needs_q8k(ggml_type)) return mxa::align256(mxa::act_bytes(n_tokens, in_features));
+  return widen_part(true, n_tokens, in_features) + split_part(true, n_tokens, in_features);
+}
+
+int mxa_quantize_q8_k_bf16(const void* x, int n_tokens, int in_features, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (x == nullptr || n_tokens <= 0 || in_features <= 0 || in_features % mxa::QK != 0 ||
+      !aligned(x, 16) || !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
+    return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, in_features);
+  mxa::launch_quantize_q8k_bf16((const uint16_t*)x, a, n_tokens, in_features, (hipStream_t)stream);
+  return check_launch();
+}
+
 int mxa_quantize_q8_k(const float* x, int n_tokens, int in_features, void* workspace,
                       size_t workspace_bytes, void* stream) {
   if (x == nullptr || n_tokens <= 0 || in_features <= 0 || in_features % mxa::QK != 0 ||
@@ -123,8 +299,19 @@ int mxa_gemm(int ggml_type, const void* w, const float* x, float* y, int n_token
   const int outs[1] = {out_features};
   const int types[1] = {ggml_type};
   const void* ws[1] = {w};
-  return mxa_gemm_multi(1, types, ws, outs, x, y, n_tokens, in_features, workspace,
-                        workspace_bytes, stream);
+  return gemm_multi_core(1, types, ws, outs, x, false, mxa::YOut::f32(y), n_tokens, in_features,
+                         workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mxa_gemm_bf16(int ggml_type, const void* w, const void* x, void* y, int n_tokens,
+                  int out_features, int in_features, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  if (!aligned(y, 2)) return MXA_ERR_UNSUPPORTED;
+  const int outs[1] = {out_features};
+  const int types[1] = {ggml_type};
+  const void* ws[1] = {w};
+  return gemm_multi_core(1, types, ws, outs, x, true, mxa::YOut::bf16(y), n_tokens, in_features,
+                         workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int mxa_gemv_f32(int ggml_type, const void* w, const float* x, float* y, int n_tokens,
@@ -133,10 +320,11 @@ int mxa_gemv_f32(int ggml_type, const void* w, const float* x, float* y, int n_t
       n_tokens <= 0 || out_features <= 0 || !aligned(w, 4) || !aligned(x, 16))
     return MXA_ERR_UNSUPPORTED;
   const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
+  const mxa::YOut yo = mxa::YOut::f32(y);
   for (int m0 = 0; m0 < n_tokens; m0 += 4) {  // activation rows m0 .. m0 + 3
     const int rows = n_tokens - m0 < 4 ? n_tokens - m0 : 4;
     if (mxa::launch_gemv_f32(ggml_type, (const uint8_t*)w, rb, x + (size_t)m0 * in_features,
-                             in_features, y + (size_t)m0 * out_features, out_features, rows,
+                             in_features, yo.at((long long)m0 * out_features), out_features, rows,
                              out_features, (hipStream_t)stream) != 0)
       return MXA_ERR_UNSUPPORTED;
   }
@@ -146,25 +334,17 @@ int mxa_gemv_f32(int ggml_type, const void* w, const float* x, float* y, int n_t
 int mxa_gemm_q8k(int ggml_type, const void* w, const float* x, float* y, int n_tokens,
                  int out_features, int in_features, const void* workspace,
                  size_t workspace_bytes, void* stream) {
-  if (!mxa_supports(ggml_type, in_features) || w == nullptr || y == nullptr || n_tokens <= 0 ||
-      out_features <= 0 || !aligned(w, 4) || !aligned(x, 16) || !aligned(workspace, 16))
-    return MXA_ERR_UNSUPPORTED;
-  mxa::ActBuffers buf{};
-  const mxa::ActBuffers* abuf = nullptr;
-  if (needs_q8k(ggml_type)) {
-    if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
-      return MXA_ERR_WORKSPACE;
-    buf = mxa::act_layout((void*)workspace, n_tokens, in_features);
-    abuf = &buf;
-  } else if (x == nullptr) {
-    return MXA_ERR_UNSUPPORTED;
-  }
-  const mxa::Act act = make_act(x, abuf, in_features);
-  const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
-  if (mxa::launch_matmul(ggml_type, (const uint8_t*)w, rb, act, y, out_features, n_tokens,
-                         out_features, (hipStream_t)stream) != 0)
-    return MXA_ERR_UNSUPPORTED;
-  return check_launch();
+  if (y == nullptr) return MXA_ERR_UNSUPPORTED;
+  return gemm_q8k_core(ggml_type, w, x, mxa::YOut::f32(y), n_tokens, out_features, in_features,
+                       workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mxa_gemm_q8k_bf16(int ggml_type, const void* w, void* y, int n_tokens, int out_features,
+                      int in_features, const void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  if (y == nullptr || !aligned(y, 2) || !needs_q8k(ggml_type)) return MXA_ERR_UNSUPPORTED;
+  return gemm_q8k_core(ggml_type, w, nullptr, mxa::YOut::bf16(y), n_tokens, out_features,
+                       in_features, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_experts,
@@ -186,8 +366,8 @@ int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_ex
   if (x != nullptr) mxa::launch_quantize_q8k(x, buf, n_rows, in_features, s);
   const mxa::Act act = make_act(x, &buf, in_features);
   if (mxa::launch_moe_dec(ggml_type, (const uint8_t*)w, rb, expert_stride, n_experts, act,
-                          offsets, n_rows, min(max_rows_per_expert, n_rows), y, out_features,
-                          out_features, s) != 0)
+                          offsets, n_rows, min(max_rows_per_expert, n_rows), mxa::YOut::f32(y),
+                          out_features, out_features, s) != 0)
     return MXA_ERR_UNSUPPORTED;
   return check_launch();
 }
@@ -204,10 +384,11 @@ int mxa_gemm_moe_pairs(int ggml_type, const void* w, long long expert_stride, in
   if (expert_stride < (long long)out_features * rb) return MXA_ERR_UNSUPPORTED;
   const hipStream_t s = (hipStream_t)stream;
   const int x_step = x_rows == 1 ? 0 : 1;
+  const mxa::YOut yo = mxa::YOut::f32(y);
   if (x != nullptr) {  // x quantized in the kernel where it can be
     const mxa::Act act = make_act(x, nullptr, in_features);
     if (mxa::launch_gemv_wave_pairs(ggml_type, (const uint8_t*)w, rb, expert_stride, ids,
-                                    n_experts, n_pairs, x_step, act, y, out_features, s) == 0)
+                                    n_experts, n_pairs, x_step, act, yo, out_features, s) == 0)
       return check_launch();
   }
   if (workspace == nullptr || workspace_bytes < mxa::act_bytes(x_rows, in_features))
@@ -218,7 +399,7 @@ int mxa_gemm_moe_pairs(int ggml_type, const void* w, long long expert_stride, in
   // kernel does not take, only it has been written)
   if (x != nullptr) mxa::launch_quantize_q8k(x, buf, x_rows, in_features, s);
   if (mxa::launch_gemv_wave_pairs(ggml_type, (const uint8_t*)w, rb, expert_stride, ids, n_experts,
-                                  n_pairs, x_step, act, y, out_features, s) != 0)
+                                  n_pairs, x_step, act, yo, out_features, s) != 0)
     return MXA_ERR_UNSUPPORTED;
   return check_launch();
 }
@@ -237,108 +418,32 @@ int mxa_moe_combine(const float* down, const int32_t* rows, const int32_t* ids,
 int mxa_gemm_multi(int n, const int* types, const void* const* ws, const int* outs,
                    const float* x, float* y, int n_tokens, int in_features, void* workspace,
                    size_t workspace_bytes, void* stream) {
-  if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr)
-    return MXA_ERR_UNSUPPORTED;
-  if (x == nullptr || y == nullptr || n_tokens <= 0 || !aligned(x, 16) || !aligned(workspace, 16))
-    return MXA_ERR_UNSUPPORTED;
-  bool any_q8k = false, any_iq4 = false;
-  long long total = 0;
-  for (int i = 0; i < n; ++i) {
-    if (!mxa_supports(types[i], in_features) || ws[i] == nullptr || outs[i] <= 0 ||
-        !aligned(ws[i], 4))
-      return MXA_ERR_UNSUPPORTED;
-    any_q8k |= needs_q8k(types[i]);
-    any_iq4 |= !needs_q8k(types[i]);
-    total += outs[i];
-  }
-  hipStream_t s = (hipStream_t)stream;
-  const int fmax = mxa::fused_max_rows();
-  const size_t q8k_bytes = q8k_part(any_q8k, n_tokens, in_features, fmax);
-  const size_t split_bytes = split_part(any_iq4, n_tokens, in_features);
-  const size_t need = q8k_bytes + split_bytes;
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MXA_ERR_WORKSPACE;
-  mxa::ActBuffers buf{};
-  const mxa::ActBuffers* abuf = nullptr;
-  if (q8k_bytes > 0) {
-    buf = mxa::act_layout(workspace, n_tokens, in_features);
-    abuf = &buf;
-    mxa::launch_quantize_q8k(x, buf, n_tokens, in_features, s);
-    const int st = check_launch();
-    if (st != MXA_OK) return st;
-  }
-  mxa::Act act = make_act(x, abuf, in_features);
-  if (split_bytes > 0) act.xsplit = (uint8_t*)workspace + q8k_bytes;
-  if (n > 1 && !any_iq4 && n_tokens <= 16) {  // decode: one launch for all weights
-    mxa::DecodeSeg seg[4];
-    long long c0 = 0;
-    for (int i = 0; i < n; ++i) {
-      seg[i] = mxa::DecodeSeg{types[i], (const uint8_t*)ws[i],
-                              (long long)mxa_row_bytes(types[i], in_features), y + c0, outs[i]};
-      c0 += outs[i];
-    }
-    int st = -1;
-    if (n_tokens <= fmax) {
-      st = mxa::launch_decode_multi(seg, n, act, total, n_tokens, s);
-    } else {
-      st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
-      if (st != 0) st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
-    }
-    if (st == 0) return check_launch();
-  }
-  long long col = 0;
-  for (int i = 0; i < n; ++i) {
-    const long long rb = (long long)mxa_row_bytes(types[i], in_features);
-    if (mxa::launch_matmul(types[i], (const uint8_t*)ws[i], rb, act, y + col, total, n_tokens,
-                           outs[i], s) != 0)
-      return MXA_ERR_UNSUPPORTED;
-    const int st = check_launch();
-    if (st != MXA_OK) return st;
-    col += outs[i];
-  }
-  return MXA_OK;
+  return gemm_multi_core(n, types, ws, outs, x, false, mxa::YOut::f32(y), n_tokens, in_features,
+                         workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mxa_gemm_multi_bf16(int n, const int* types, const void* const* ws, const int* outs,
+                        const void* x, void* y, int n_tokens, int in_features, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (!aligned(y, 2)) return MXA_ERR_UNSUPPORTED;
+  return gemm_multi_core(n, types, ws, outs, x, true, mxa::YOut::bf16(y), n_tokens, in_features,
+                         workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int mxa_gemm_multi_q8k(int n, const int* types, const void* const* ws, const int* outs, float* y,
                        int n_tokens, int in_features, const void* workspace,
                        size_t workspace_bytes, void* stream) {
-  if (n < 1 || n > 4 || types == nullptr || ws == nullptr || outs == nullptr || y == nullptr ||
-      n_tokens <= 0 || !aligned(workspace, 16))
-    return MXA_ERR_UNSUPPORTED;
-  long long total = 0;
-  for (int i = 0; i < n; ++i) {
-    if (!mxa_supports(types[i], in_features) || !needs_q8k(types[i]) || ws[i] == nullptr ||
-        outs[i] <= 0 || !aligned(ws[i], 4))
-      return MXA_ERR_UNSUPPORTED;
-    total += outs[i];
-  }
-  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, in_features))
-    return MXA_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  const mxa::ActBuffers buf = mxa::act_layout((void*)workspace, n_tokens, in_features);
-  const mxa::Act act = make_act(nullptr, &buf, in_features);
-  mxa::DecodeSeg seg[4];
-  long long c0 = 0;
-  for (int i = 0; i < n; ++i) {
-    seg[i] = mxa::DecodeSeg{types[i], (const uint8_t*)ws[i],
-                            (long long)mxa_row_bytes(types[i], in_features), y + c0, outs[i]};
-    c0 += outs[i];
-  }
-  if (n > 1 && n_tokens <= 16) {  // one launch for the group
-    const int fmax = mxa::fused_max_rows();
-    int st = n_tokens <= fmax ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
-                              : mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
-    if (st != 0 && n_tokens > fmax)
-      st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
-    if (st == 0) return check_launch();
-  }
-  for (int i = 0; i < n; ++i) {
-    if (mxa::launch_matmul(types[i], seg[i].w, seg[i].row_bytes, act, seg[i].y, total, n_tokens,
-                           outs[i], s) != 0)
-      return MXA_ERR_UNSUPPORTED;
-    const int st = check_launch();
-    if (st != MXA_OK) return st;
-  }
-  return MXA_OK;
+  if (y == nullptr) return MXA_ERR_UNSUPPORTED;
+  return gemm_multi_q8k_core(n, types, ws, outs, mxa::YOut::f32(y), n_tokens, in_features,
+                             workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int mxa_gemm_multi_q8k_bf16(int n, const int* types, const void* const* ws, const int* outs,
+                            void* y, int n_tokens, int in_features, const void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (y == nullptr || !aligned(y, 2)) return MXA_ERR_UNSUPPORTED;
+  return gemm_multi_q8k_core(n, types, ws, outs, mxa::YOut::bf16(y), n_tokens, in_features,
+                             workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int mxa_rms_norm_q8_k(const float* x, const float* weight, float eps, int n_tokens, int dim,
@@ -361,6 +466,32 @@ int mxa_silu_mul_q8_k(const float* gate, const float* up, long long ld, int n_to
   if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, dim)) return MXA_ERR_WORKSPACE;
   const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, dim);
   mxa::launch_silu_mul_q8k(gate, up, ld, out, a, n_tokens, dim, (hipStream_t)stream);
+  return check_launch();
+}
+
+int mxa_rms_norm_q8_k_bf16(const void* x, const void* weight, float eps, int n_tokens, int dim,
+                           void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr || weight == nullptr || n_tokens <= 0 || dim <= 0 || dim % mxa::QK != 0 ||
+      !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, dim)) return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, dim);
+  if (mxa::launch_rms_norm_q8k_bf16((const uint16_t*)x, (const uint16_t*)weight, eps,
+                                    (uint16_t*)out, a, n_tokens, dim, (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
+int mxa_silu_mul_q8_k_bf16(const void* gate, const void* up, long long ld, int n_tokens, int dim,
+                           void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (gate == nullptr || up == nullptr || n_tokens <= 0 || dim <= 0 || dim % mxa::QK != 0 ||
+      ld < dim || !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_tokens, dim)) return MXA_ERR_WORKSPACE;
+  const mxa::ActBuffers a = mxa::act_layout(workspace, n_tokens, dim);
+  if (mxa::launch_silu_mul_q8k_bf16((const uint16_t*)gate, (const uint16_t*)up, ld, (uint16_t*)out,
+                                    a, n_tokens, dim, (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
   return check_launch();
 }
 

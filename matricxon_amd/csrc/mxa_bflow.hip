@@ -97,7 +97,7 @@ __device__ __forceinline__ BfCopies bf_offsets(long long row_bytes, int rs, int 
 
 template <int TYPE, int C>
 __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
-                                           const Act& act, float* __restrict__ y, long long ldy,
+                                           const Act& act, YOut y, long long ldy,
                                            int M, int N, const BfGeo& geo, int wg) {
   using Tile = typename TileOf<TYPE>::T;
   using F = typename Tile::F;
@@ -207,7 +207,7 @@ __device__ __forceinline__ void bflow_rows(uint8_t* smem, const uint8_t* w, long
 #pragma unroll
         for (int b = 0; b < 16; ++b)
           if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
-        y[(size_t)m * ldy + r0 + j] = gave_up ? __builtin_nanf("") : acc;
+        y.put((size_t)m * ldy + r0 + j, gave_up ? __builtin_nanf("") : acc);
       }
     }
     return;
@@ -268,7 +268,7 @@ template <int TYPE, int C>
 __global__ __launch_bounds__(1024) void bflow_kernel(const uint8_t* w, uint32_t pack_a,
                                                      uint32_t pack_b, int N, int row_bytes,
                                                      const int8_t* q, const int16_t* bsums,
-                                                     const float* d, float* __restrict__ y,
+                                                     const float* d, YOut y,
                                                      int ldy) {
   extern __shared__ __align__(16) uint8_t smem[];
   BfGeo geo;
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(1024) void bflow_kernel(const uint8_t* w, uint32_t 
   const int M = (pack_a >> 16) & 0x1F, nb = pack_a >> 21;
   Act act;
   act.q = q, act.d = d, act.bsums = bsums, act.x = nullptr;
-  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr;
+  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr, act.xbf16 = 0;
   bflow_rows<TYPE, C>(smem, w, row_bytes, act, y, ldy, M, N, geo, blockIdx.x);
 }
 
@@ -288,7 +288,7 @@ __host__ constexpr int bf_row_chunks(long long row_bytes) {
 }
 
 template <int TYPE, int C>
-int launch_bf(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
+int launch_bf(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
               int N, hipStream_t stream) {
   const int nb = act.nb;
   const int ncu = cu_count();
@@ -319,7 +319,7 @@ int launch_bf(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
 
 }  // namespace
 
-int launch_bflow(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_bflow(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (act.q == nullptr || m_rows < 1 || m_rows > 16 || n_rows < 1 || act.nb > 16) return -1;
   if ((((uintptr_t)w | (uintptr_t)row_bytes) & 15) != 0) return -1;

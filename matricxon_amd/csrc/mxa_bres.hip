@@ -67,7 +67,7 @@ __device__ __forceinline__ void br_add(int* p, int v) {
 
 template <int TYPE, int C>
 __device__ __forceinline__ void bres_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
-                                          const Act& act, float* __restrict__ y, long long ldy,
+                                          const Act& act, YOut y, long long ldy,
                                           int M, int N, const BrGeo& geo, int wg) {
   using Tile = typename TileOf<TYPE>::T;
   using F = typename Tile::F;
@@ -174,7 +174,7 @@ __device__ __forceinline__ void bres_rows(uint8_t* smem, const uint8_t* w, long 
           const float* src = (const float*)(tile + ((ro + wv * C * TB + 3) & ~3));
           acc = Tile::fold(acc, Ad[b * 16 + m], src[cc * 16 + m], src[C * 16 + cc]);
         }
-        y[(size_t)m * ldy + r0 + 16 * t + nl] = acc;
+        y.put((size_t)m * ldy + r0 + 16 * t + nl, acc);
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot reads are done
       if (lane == 0) br_add(&folded[t], 1);
@@ -250,7 +250,7 @@ __device__ __forceinline__ void bres_rows(uint8_t* smem, const uint8_t* w, long 
 
 template <int TYPE, int C>
 __global__ __launch_bounds__(1024) void bres_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                    float* __restrict__ y, long long ldy, int M,
+                                                    YOut y, long long ldy, int M,
                                                     int N, BrGeo geo) {
   extern __shared__ __align__(16) uint8_t smem[];
   bres_rows<TYPE, C>(smem, w, row_bytes, act, y, ldy, M, N, geo, blockIdx.x);
@@ -262,7 +262,7 @@ constexpr int kBrMaxSegs = 4;
 struct BrSeg {
   const uint8_t* w;
   long long row_bytes;
-  float* y;  // the segment's first output column
+  YOut y;  // the segment's first output column
   int n, type, wg0;
   BrGeo geo;
 };
@@ -306,7 +306,7 @@ inline bool br_geometry(BrGeo& geo, long long row_bytes, int nb, int C, int R, i
 }
 
 template <int TYPE, int C>
-int launch_br(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
+int launch_br(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
               int N, hipStream_t stream) {
   const int ncu = cu_count();
   const int R = max(16, (int)((N + (long long)ncu - 1) / ncu));
@@ -321,7 +321,7 @@ int launch_br(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
 }
 
 template <int TYPE>
-int launch_br_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_br_type(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                    int M, int N, hipStream_t stream) {
   if (act.nb <= 8) return launch_br<TYPE, 1>(w, row_bytes, act, y, ldy, M, N, stream);
   return launch_br<TYPE, 2>(w, row_bytes, act, y, ldy, M, N, stream);
@@ -358,7 +358,7 @@ int launch_br_multi(const DecodeSeg* seg, int count, const Act& act, long long l
 
 }  // namespace
 
-int launch_bres(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_bres(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                 long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (act.q == nullptr || m_rows < 1 || m_rows > 16 || n_rows < 1 || act.nb > 16) return -1;
   switch (type) {

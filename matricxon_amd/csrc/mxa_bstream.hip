@@ -83,7 +83,7 @@ __device__ __forceinline__ void wait_at_least(const int* p, int target) {
 // order, t = s / np, p = s % np.
 template <int TYPE, int C>
 __device__ __forceinline__ void bstream_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
-                                             const Act& act, float* __restrict__ y, long long ldy,
+                                             const Act& act, YOut y, long long ldy,
                                              int M, int N, const BsGeo& geo, int wg) {
   using Tile = typename TileOf<TYPE>::T;
   using F = typename Tile::F;
@@ -272,7 +272,7 @@ __device__ __forceinline__ void bstream_rows(uint8_t* smem, const uint8_t* w, lo
     const int n0 = 16 * t0, nr = min(rows, 16 * t1) - n0;
     for (int i = tid; i < nr * M; i += nct) {
       const int m = i / nr, n = n0 + (i - m * nr);
-      y[(size_t)m * ldy + r0 + n] = Yo[((n >> 4) % kOutTiles) * 256 + (n & 15) * 16 + m];
+      y.put((size_t)m * ldy + r0 + n, Yo[((n >> 4) % kOutTiles) * 256 + (n & 15) * 16 + m]);
     }
   };
 
@@ -319,7 +319,7 @@ __device__ __forceinline__ void bstream_rows(uint8_t* smem, const uint8_t* w, lo
 
 template <int TYPE, int C>
 __global__ __launch_bounds__(768) void bstream_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                      float* __restrict__ y, long long ldy, int M,
+                                                      YOut y, long long ldy, int M,
                                                       int N, BsGeo geo) {
   extern __shared__ __align__(16) uint8_t smem[];
   bstream_rows<TYPE, C>(smem, w, row_bytes, act, y, ldy, M, N, geo, blockIdx.x);
@@ -331,7 +331,7 @@ constexpr int kMaxSegs = 4;
 struct BsSeg {
   const uint8_t* w;
   long long row_bytes;
-  float* y;  // the segment's first output column
+  YOut y;  // the segment's first output column
   int n, type, wg0, rows_per_wg, rs, buf_bytes;
 };
 struct BsSegs {
@@ -390,7 +390,7 @@ inline bool bs_buffers(BsGeo& geo, int buf_bytes, int kb, int nb) {
 }
 
 template <int TYPE, int C>
-int launch_bs(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
+int launch_bs(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
               int N, hipStream_t stream) {
   const int nb = act.nb;
   const int ncu = cu_count();
@@ -411,7 +411,7 @@ int launch_bs(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
 }
 
 template <int TYPE>
-int launch_bs_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_bs_type(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                    int M, int N, hipStream_t stream) {
   const int nb = act.nb;
   // one or two blocks per compute wave and stage: at most 8 compute waves
@@ -460,7 +460,7 @@ int launch_bs_multi(const DecodeSeg* seg, int count, const Act& act, long long l
 
 }  // namespace
 
-int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (act.q == nullptr || m_rows < 1 || m_rows > 16 || n_rows < 1) return -1;
   switch (type) {

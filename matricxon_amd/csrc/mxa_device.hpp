@@ -133,6 +133,38 @@ __device__ __forceinline__ float sbyte_f(uint32_t w) {
   return (float)(int8_t)(uint8_t)(w >> (8 * K));
 }
 
+// ------------------------------------------------------------------ bfloat16 activations / outputs
+// float -> bfloat16, round to nearest even; a NaN becomes the quiet NaN 0x7FC0 (torch's cast,
+// c10::detail::round_to_nearest_even).
+__host__ __device__ __forceinline__ uint16_t bf16_rne(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+// bfloat16 (low 16 bits of h) -> float, exact.
+__device__ __forceinline__ float bf16_to_float(uint32_t h) {
+  return __builtin_bit_cast(float, (h & 0xFFFFu) << 16);
+}
+
+// The output rows of a matmul: float32, or bfloat16 (each value rounded as bf16_rne), one
+// pointer-sized kernel argument. The element type rides in bit 0 of the address (outputs are at
+// least 2-byte aligned); at() keeps it, so offsets count elements of either type.
+struct YOut {
+  uintptr_t v;
+  __host__ __device__ static YOut f32(float* p) { return YOut{(uintptr_t)p}; }
+  __host__ __device__ static YOut bf16(void* p) { return YOut{(uintptr_t)p | 1u}; }
+  __host__ __device__ bool is_bf16() const { return (v & 1u) != 0; }
+  __host__ __device__ YOut at(long long i) const {
+    return YOut{v + (uintptr_t)(i * (is_bf16() ? 2 : 4))};
+  }
+  __device__ __forceinline__ void put(long long i, float x) const {
+    if (v & 1u)
+      ((uint16_t*)(v - 1))[i] = bf16_rne(x);
+    else
+      ((float*)v)[i] = x;
+  }
+};
+
 // Q8_K activations on the device, as produced by the quantize kernel: q (M, K) int8 row-major,
 // d (M, nb) float, bsums (M, nb, 16) int16. `x` is the raw float (M, K) input (IQ4_XS reads it).
 struct Act {
@@ -143,6 +175,7 @@ struct Act {
   int k;
   int nb;
   void* xsplit;  // IQ4_XS prefill: workspace for the bf16 split of x (nullptr when not provided)
+  int xbf16;     // x holds bfloat16 values (only the kernels that quantize x themselves take it)
 };
 
 // ------------------------------------------------------------------ LDS copies and their waits

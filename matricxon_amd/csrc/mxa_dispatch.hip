@@ -55,7 +55,7 @@ void set_fused_max_rows(int n) {
                          std::memory_order_relaxed);
 }
 
-int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                   long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (type == T_IQ4_XS || act.q == nullptr) {
     // IQ4_XS up to kFusedQuantMaxRows rows; K-quants whose x the caller left unquantized (the
@@ -76,7 +76,7 @@ int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& ac
     Act a = act;
     a.q = nullptr;
     a.x = act.x + (size_t)m0 * act.k;
-    const int st = launch_gemv_lpb(type, w, row_bytes, a, y + (size_t)m0 * ldy, ldy,
+    const int st = launch_gemv_lpb(type, w, row_bytes, a, y.at((size_t)m0 * ldy), ldy,
                                    min(kFusedQuantMaxRows, m_rows - m0), n_rows, stream);
     if (st != 0) return st;
   }

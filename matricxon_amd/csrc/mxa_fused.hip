@@ -1,6 +1,7 @@
 // Fused producers of the projections' activations: RMSNorm and SwiGLU's silu(gate) * up, each
-// writing its fp32 result and the Q8_K blocks of that result in one pass, so that the projections
-// that consume it (q|k|v and gate|up after a norm, down after SwiGLU) skip the quantize launch.
+// writing its result (float32, or bfloat16 for a bfloat16 layer) and the Q8_K blocks of that
+// result in one pass, so that the projections that consume it (q|k|v and gate|up after a norm,
+// down after SwiGLU) skip the quantize launch.
 //
 // Both take four values per thread, a wave per 256-value block, so that a call is one memory round
 // trip and a short dependent chain (decode sizes are latency-bound): RMSNorm one workgroup of up
@@ -186,7 +187,109 @@ __global__ __launch_bounds__(256) void silu_mul_q8k_v4_kernel(
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Four bfloat16 values (8 bytes) as floats, exactly.
+__device__ __forceinline__ void bf16x4_to_float(uint2 h, float (&v)[4]) {
+  v[0] = bf16_to_float(h.x), v[1] = bf16_to_float(h.x >> 16);
+  v[2] = bf16_to_float(h.y), v[3] = bf16_to_float(h.y >> 16);
+}
+__device__ __forceinline__ uint2 float4_to_bf16x4(const float (&v)[4]) {
+  return uint2{(uint32_t)bf16_rne(v[0]) | (uint32_t)bf16_rne(v[1]) << 16,
+               (uint32_t)bf16_rne(v[2]) | (uint32_t)bf16_rne(v[3]) << 16};
+}
+
+// RMSNorm of a bfloat16 layer, the steps of the reference's torch forward for a bfloat16 input
+// and weight (app/architectures/layers.py:77-81): x widened to float32, variance = the mean of x^2
+// (torch's mean multiplies the sum by 1 / dim), x * rsqrt(variance + eps) rounded to bfloat16,
+// times the bfloat16 weight, rounded again. Row blockIdx.x, four values per thread (as
+// rms_norm_q8k_v4_kernel); the Q8_K blocks are those of the bfloat16 result.
+__global__ __launch_bounds__(kRmsMaxThreads) void rms_norm_q8k_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float eps,
+    uint16_t* __restrict__ out, int8_t* __restrict__ q, float* __restrict__ d,
+    int16_t* __restrict__ bsums, int k) {
+  __shared__ float part[kRmsMaxThreads / 64];
+  const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, T = blockDim.x, n4 = k / 4;
+  const int nb = k / QK;
+  const uint16_t* xr = x + (size_t)r * k;
+  float xv[kRmsMaxParts][4], wv[kRmsMaxParts][4];
+#pragma unroll
+  for (int j = 0; j < kRmsMaxParts; ++j) {
+    const int i = t + T * j;
+    if (i < n4) {
+      bf16x4_to_float(*(const uint2*)(xr + 4 * i), xv[j]);
+      bf16x4_to_float(*(const uint2*)(w + 4 * i), wv[j]);
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRmsMaxParts; ++j)
+    if (t + T * j < n4) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = s + xv[j][e] * xv[j][e];
+    }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s = s + __shfl_xor(s, o);
+  if (lane == 0) part[t >> 6] = s;
+  __syncthreads();
+  float sum = 0.0f;
+  for (int i = 0; i < T / 64; ++i) sum = sum + part[i];
+  const float scale = rsqrtf(sum * (1.0f / (float)k) + eps);
+#pragma unroll
+  for (int j = 0; j < kRmsMaxParts; ++j) {
+    const int i = t + T * j;
+    if (i < n4) {  // uniform over the wave: n4 is a multiple of 64
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = bf16_to_float(bf16_rne(bf16_to_float(bf16_rne(xv[j][e] * scale)) * wv[j][e]));
+      if (out != nullptr) *(uint2*)(out + (size_t)r * k + 4 * i) = float4_to_bf16x4(v);
+      const int b = i >> 6;
+      q8k_part4(v, lane, q + (size_t)r * k + (size_t)b * QK, bsums + ((size_t)r * nb + b) * 16,
+                d + (size_t)r * nb + b);
+    }
+  }
+}
+
+// silu(gate) * up of a bfloat16 layer, the steps of torch's `F.silu(gate) * up` on bfloat16
+// tensors (app/architectures/layers.py:53-57): g / (1 + exp(-g)) in float32 rounded to bfloat16,
+// times up, rounded again. Row blockIdx.x, four values 256 blockIdx.y + threadIdx.x of the row;
+// the Q8_K blocks are those of the bfloat16 result.
+__global__ __launch_bounds__(256) void silu_mul_q8k_bf16_kernel(
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, long long ld,
+    uint16_t* __restrict__ out, int8_t* __restrict__ q, float* __restrict__ d,
+    int16_t* __restrict__ bsums, int k) {
+  const int r = blockIdx.x, i = 256 * (int)blockIdx.y + (int)threadIdx.x, lane = threadIdx.x & 63;
+  if (i >= k / 4) return;  // uniform over the wave: k / 4 is a multiple of 64
+  float g[4], u[4], v[4];
+  bf16x4_to_float(*(const uint2*)(gate + (size_t)r * ld + 4 * i), g);
+  bf16x4_to_float(*(const uint2*)(up + (size_t)r * ld + 4 * i), u);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    v[e] = bf16_to_float(bf16_rne(bf16_to_float(bf16_rne(g[e] / (1.0f + expf(-g[e])))) * u[e]));
+  if (out != nullptr) *(uint2*)(out + (size_t)r * k + 4 * i) = float4_to_bf16x4(v);
+  const int nb = k / QK, b = i >> 6;
+  q8k_part4(v, lane, q + (size_t)r * k + (size_t)b * QK, bsums + ((size_t)r * nb + b) * 16,
+            d + (size_t)r * nb + b);
+}
+
 }  // namespace
+
+int launch_rms_norm_q8k_bf16(const uint16_t* x, const uint16_t* w, float eps, uint16_t* out,
+                             const ActBuffers& a, int m_rows, int k, hipStream_t stream) {
+  const int n4 = k / 4;
+  if (n4 > kRmsMaxThreads * kRmsMaxParts || (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 7))
+    return -1;
+  hipLaunchKernelGGL(rms_norm_q8k_bf16_kernel, dim3(m_rows), dim3(min(n4, kRmsMaxThreads)), 0,
+                     stream, x, w, eps, out, a.q, a.d, a.bsums, k);
+  return 0;
+}
+
+int launch_silu_mul_q8k_bf16(const uint16_t* gate, const uint16_t* up, long long ld, uint16_t* out,
+                             const ActBuffers& a, int m_rows, int k, hipStream_t stream) {
+  if ((((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) & 7) || ld % 4 != 0) return -1;
+  hipLaunchKernelGGL(silu_mul_q8k_bf16_kernel, dim3(m_rows, (k / 4 + 255) / 256), dim3(256), 0,
+                     stream, gate, up, ld, out, a.q, a.d, a.bsums, k);
+  return 0;
+}
 
 void launch_rms_norm_q8k(const float* x, const float* w, float eps, float* out, const ActBuffers& a,
                          int m_rows, int k, hipStream_t stream) {

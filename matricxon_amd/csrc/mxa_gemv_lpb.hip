@@ -55,7 +55,7 @@ struct Geometry {
 template <int TYPE, int MAXM, bool FUSEQ>
 __global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict__ w,
                                                        long long row_bytes, Act act,
-                                                       float* __restrict__ y, long long ldy,
+                                                       YOut y, long long ldy,
                                                        int M, int N, Geometry geo) {
   using L = Lpb<TYPE>;
   constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
@@ -205,12 +205,12 @@ __global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict
 #pragma unroll
   for (int j = 0; j < MAXM; ++j) {
     const int f = lane + 64 * j, fr = f % R, fm = f / R;
-    if (f < R * M && fr < N - n_wave0) y[(size_t)fm * ldy + n_wave0 + fr] = acc[j];
+    if (f < R * M && fr < N - n_wave0) y.put((size_t)fm * ldy + n_wave0 + fr, acc[j]);
   }
 }
 
 template <int TYPE, int MAXM, bool FUSEQ>
-int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                int M, int N, hipStream_t stream) {
   using L = Lpb<TYPE>;
   constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
@@ -397,7 +397,7 @@ __device__ __forceinline__ void stage_activations(const Act& act, int M, int aw,
 // wave) of one packed weight.
 template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG, bool LONG = false>
 __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long long row_bytes,
-                                          const Act& act, float* __restrict__ y, long long ldy,
+                                          const Act& act, YOut y, long long ldy,
                                           int M, int N, const PipeGeo& geo, int tile) {
   static_assert(!ACTREG || (MAXM == 1 && (TYPE == T_Q4_K || TYPE == T_Q8_0)),
                 "register activations: one Q8_K row, types whose compute leaves room for them");
@@ -553,7 +553,7 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
   if constexpr (LONG) {
     for (int f = lane; f < nrows * M; f += 64) {  // consecutive lanes, consecutive rows
       const int fm = f / nrows, fr = f - fm * nrows;
-      y[(size_t)fm * ldy + n0 + fr] = Ybuf[fm * R + fr];
+      y.put((size_t)fm * ldy + n0 + fr, Ybuf[fm * R + fr]);
     }
     return;
   }
@@ -580,7 +580,7 @@ __device__ __forceinline__ void pipe_rows(uint8_t* smem, const uint8_t* w, long 
     }
     for (; bb < nb; ++bb)
       acc = L::fold(acc, kFloatAct ? 0.0f : xd[bb], v[bb], L::kHasD ? dd[bb] : 0.0f);
-    y[(size_t)fm * ldy + n0 + fr] = acc;
+    y.put((size_t)fm * ldy + n0 + fr, acc);
   }
 }
 
@@ -603,7 +603,7 @@ inline bool pipe_pack(const PipeGeo& g, int nb, int grid, PipePack& p) {
 
 template <int TYPE, int MAXM, bool FUSEQ, bool ACTREG, bool LONG>
 __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, const float* x,
-                                                         float* __restrict__ y, int row_bytes,
+                                                         YOut y, int row_bytes,
                                                          int N, int M, int ldy, uint32_t pack_a,
                                                          uint32_t pack_b, const int8_t* q,
                                                          const float* d, const int16_t* bsums) {
@@ -617,7 +617,7 @@ __global__ __launch_bounds__(768) void gemv_pipe_kernel(const uint8_t* w, const 
   const int nb = pack_b & 0xFF, grid = pack_b >> 8;
   Act act;
   act.q = q, act.d = d, act.bsums = bsums, act.x = x;
-  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr;
+  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr, act.xbf16 = 0;
   pipe_rows<TYPE, MAXM, FUSEQ, ACTREG, LONG>(smem, w, row_bytes, act, y, ldy, M, N, geo,
                                              xcd_tile(blockIdx.x, grid));
 }
@@ -628,7 +628,7 @@ constexpr int kMaxSegs = 4;
 struct PipeSeg {
   const uint8_t* w;
   long long row_bytes;
-  float* y;  // the segment's first output column
+  YOut y;  // the segment's first output column
   int n, type, wg0, rows_per_wave;
 };
 struct PipeSegs {
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(768) void gemv_pipe_multi_kernel(PipeSegs segs, Act
 
 // Returns -1 when the shape does not suit the pipelined form (the caller uses gemv_lpb_kernel).
 template <int TYPE, int MAXM, bool FUSEQ>
-int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_pipe(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                 int M, int N, hipStream_t stream) {
   using L = Lpb<TYPE>;
   constexpr int kActBlk = ActTraits<TYPE>::kBlk;
@@ -797,14 +797,14 @@ int launch_pipe_multi(const DecodeSeg* seg, int count, const Act& act, long long
 }
 
 template <int TYPE, int MAXM, bool FUSEQ>
-int launch_decode(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_decode(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                   int M, int N, hipStream_t stream) {
   if (launch_pipe<TYPE, MAXM, FUSEQ>(w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   return launch_lpb<TYPE, MAXM, FUSEQ>(w, row_bytes, act, y, ldy, M, N, stream);
 }
 
 template <int TYPE>
-int launch_lpb_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_lpb_type(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                     int M, int N, hipStream_t stream) {
   constexpr bool kQ8K = !ActTraits<TYPE>::kFloat;
   const bool fuse = kQ8K && act.q == nullptr;
@@ -823,6 +823,7 @@ int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long lo
   if (m_rows < 1 || m_rows > kFusedQuantMaxRows) return -1;
   const bool fuse = act.q == nullptr;
   if (m_rows == 1 && launch_gemv_wave_multi(seg, count, act, stream) == 0) return 0;
+  if (fuse && act.xbf16) return -1;  // only the floor-shaped kernel reads bfloat16 x
   if (m_rows == 1) return fuse ? launch_pipe_multi<1, true>(seg, count, act, ldy, m_rows, stream)
                                : launch_pipe_multi<1, false>(seg, count, act, ldy, m_rows, stream);
   if (m_rows == 2) return fuse ? launch_pipe_multi<2, true>(seg, count, act, ldy, m_rows, stream)
@@ -831,7 +832,7 @@ int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long lo
               : launch_pipe_multi<4, false>(seg, count, act, ldy, m_rows, stream);
 }
 
-int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (m_rows < 1 || m_rows > 4) return -1;
   if (m_rows == 1) {
@@ -839,10 +840,12 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
     // size on MI355X: Q4_K 4096 x 4096 3.8 vs 5.3 us, 14336 x 4096 7.4 vs 8.6 us), else the
     // workgroup-resident kernel for weights up to 12 MB
     if (launch_gemv_wave(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
+    if (act.q == nullptr && act.xbf16) return -1;  // only the floor-shaped kernel reads bf16 x
     if (launch_gemv_res(type, w, row_bytes, act, y, n_rows, stream) == 0) return 0;
   }
   if (m_rows >= 2 && launch_gemv_wave_m(type, w, row_bytes, act, y, ldy, m_rows, n_rows, stream) == 0)
     return 0;
+  if (act.q == nullptr && act.xbf16) return -1;
   switch (type) {
     case T_Q4_K: return launch_lpb_type<T_Q4_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     case T_Q6_K: return launch_lpb_type<T_Q6_K>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
@@ -853,11 +856,11 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
 }
 
 int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float* x, int k,
-                    float* y, long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+                    YOut y, long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (m_rows < 1 || m_rows > 4) return -1;
   Act act;
   act.q = nullptr, act.d = nullptr, act.bsums = nullptr, act.x = x;
-  act.k = k, act.nb = k / QK, act.xsplit = nullptr;
+  act.k = k, act.nb = k / QK, act.xsplit = nullptr, act.xbf16 = 0;
   // the floor-shaped kernel where it applies (the same bits as the pipelined kernel; measured on
   // MI355X, one row: Q4_K 14336 x 4096 11.3 vs 17.2 us, 4096 x 4096 5.7 vs 11.1, Q8_0 4096 x 4096
   // 7.0 vs 11.9, Q6_K 4096 x 14336 18.7 vs 27.7, the 128256 x 4096 head 83 vs 94; four rows Q4_K

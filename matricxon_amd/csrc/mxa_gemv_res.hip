@@ -313,7 +313,7 @@ __device__ __forceinline__ int fold_slot(int j) {
 // Row r of the workgroup's rows: its groups' fold operands (left in LDS by the units) folded
 // in order 0..nb-1 with the oracle's fused steps (mx_dot_k_ssse3.c:115-154); y points at row 0's output.
 template <int GB>
-__device__ __forceinline__ void fold_row(const uint8_t* reg, int r, int nb, float* y) {
+__device__ __forceinline__ void fold_row(const uint8_t* reg, int r, int nb, YOut y) {
   float acc = 0.0f;
   const int j0 = r * nb;
   int bb = 0;
@@ -328,7 +328,7 @@ __device__ __forceinline__ void fold_row(const uint8_t* reg, int r, int nb, floa
     const float2 v = *(const float2*)(reg + fold_slot<GB>(j0 + bb));
     acc = fmaf(v.x, v.y, acc);
   }
-  y[r] = acc;
+  y.put(r, acc);
 }
 
 struct ResGeo {
@@ -411,7 +411,7 @@ __device__ __forceinline__ void copy_rows(const uint8_t* src, const uint8_t* las
 template <int TYPE, bool XQ8K, bool ACTREG>
 __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restrict__ w,
                                                           long long row_bytes, Act act,
-                                                          float* __restrict__ y, int N,
+                                                          YOut y, int N,
                                                           ResGeo geo) {
   using Q = Pair<TYPE>;
   constexpr int GB = Q::kBytes;  // bytes of one 256-value group
@@ -567,18 +567,18 @@ __global__ __launch_bounds__(1024) void gemv_res_kernel(const uint8_t* __restric
       const int per = kUnit / nb;
       for (int l = lane; l < per * ((units - cw + NW - 1) / NW); l += 64) {
         const int r = (cw + NW * (l / per)) * per + l % per;
-        if (r < nrows) fold_row<GB>(reg, r, nb, y + n0);
+        if (r < nrows) fold_row<GB>(reg, r, nb, y.at(n0));
       }
     }
   }
   if constexpr (ACTREG) return;
   lds_barrier();
   // 4. fold: one thread per row takes the row's groups in order 0..nb-1 (mx_dot_k_ssse3.c:115-154)
-  for (int r = threadIdx.x; r < nrows; r += blockDim.x) fold_row<GB>(reg, r, nb, y + n0);
+  for (int r = threadIdx.x; r < nrows; r += blockDim.x) fold_row<GB>(reg, r, nb, y.at(n0));
 }
 
 template <int TYPE, bool XQ8K>
-int launch_res_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, int N,
+int launch_res_t(const uint8_t* w, long long row_bytes, const Act& act, YOut y, int N,
                   hipStream_t stream) {
   using Q = Pair<TYPE>;
   const int nb = act.nb;
@@ -617,13 +617,13 @@ int launch_res_t(const uint8_t* w, long long row_bytes, const Act& act, float* y
 
 }  // namespace
 
-int launch_gemv_res(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_res(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                      int n_rows, hipStream_t stream) {
   // Measured on MI355X against the pipelined lane-per-block kernel: faster for weights up to
   // about 12 MB (Q4_K 4096 x 4096: 5.2 vs 5.7 us; Q6_K 1024 x 4096: 6.3 vs 6.7 us), slower above
   // (Q4_K 14336 x 4096: 10.2 vs 9.7 us; Q6_K 128256 x 4096: 117 vs 108 us).
   if ((long long)n_rows * row_bytes > kResMaxBytes) return -1;
-  if (((uintptr_t)act.x & 15) != 0) return -1;
+  if (((uintptr_t)act.x & 15) != 0 || (act.q == nullptr && act.xbf16)) return -1;
   const bool q8k = act.q != nullptr;
   switch (type) {
     case T_Q4_K: return q8k ? launch_res_t<T_Q4_K, true>(w, row_bytes, act, y, n_rows, stream)

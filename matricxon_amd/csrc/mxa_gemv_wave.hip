@@ -102,18 +102,19 @@ typedef __attribute__((address_space(3))) int lds_int;
 // counts once after a bounded amount of work); a wave that gives up writes NaN.
 constexpr int kWaveSpinLimit = 1 << 22;
 
-// pack: waves | stagers << 8 | activation rows << 16: the first `waves` waves of the workgroup
+// pack: waves | stagers << 8 | (activation rows | bf16 x << 7) << 16 | late row waves << 24: the
+// first `waves` waves of the workgroup
 // own rows, the first `stagers` also stage the activations (the workgroup has max(waves, stagers)
 // waves; one that owns no rows only stages).
 // The workgroup's work: workgroup wg of n_wg over the N rows of one weight, for M <= MAXM
 // activation rows (y row m at y + m ldy).
 template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM = 1, bool LOOP = false>
 __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                          float* __restrict__ y, int N, int row_bytes, int waves,
+                                          YOut y, int N, int row_bytes, int waves,
                                           int nq, int M, int ldy, const int8_t* __restrict__ aq,
                                           const float* __restrict__ ad,
                                           const int16_t* __restrict__ abs_, int wg, int n_wg,
-                                          int late = 0) {
+                                          int late = 0, bool xbf16 = false) {
   using L = Lpb<TYPE>;
   static_assert(!ACTREG || MAXM == 1, "activations in registers for one row only");
   // float activations, unquantized (IQ4_XS, the fp32-activation types; these also use sums of 16)
@@ -166,9 +167,16 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
     } else if constexpr (FUSEQ) {
       for (int r = wave; r < kRounds * M; r += nq) {
         const int m = r / kRounds, g0 = 4 * (r % kRounds);
-        for (int g = g0; g < g0 + 4; ++g)
-          copy16_to_lds((const void*)(x + (size_t)m * K + g * QK + 4 * lane),
-                        lds_addr(xs + m * K + g * QK));
+        if (xbf16) {  // bfloat16 x: a 1 KB copy moves two blocks
+          const uint16_t* xh = (const uint16_t*)x + (size_t)m * K;
+          for (int g = g0; g < g0 + 4; g += 2)
+            copy16_to_lds((const void*)(xh + g * QK + 8 * lane),
+                          lds_addr((uint16_t*)xs + m * K + g * QK));
+        } else {
+          for (int g = g0; g < g0 + 4; ++g)
+            copy16_to_lds((const void*)(x + (size_t)m * K + g * QK + 4 * lane),
+                          lds_addr(xs + m * K + g * QK));
+        }
       }
     } else {
       // Copy j of row m: q8 pieces (j < kQ; slot s = 64 j + lane: piece s / NB of block s % NB),
@@ -231,10 +239,21 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
       for (int r = wave; r < kRounds * M; r += nq) {
         const int m = r / kRounds, g = 4 * (r % kRounds) + (lane >> 4);
         float v[16];
+        if (xbf16) {  // the values widened exactly
+          const uint16_t* src = (const uint16_t*)xs + m * K + g * QK + 16 * p;
+          const uint4 a = *(const uint4*)src, b = *(const uint4*)(src + 8);
+          const uint32_t hv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 f = *(const float4*)(xs + m * K + g * QK + 16 * p + 4 * q);
-          v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+          for (int i = 0; i < 8; ++i) {
+            v[2 * i] = bf16_to_float(hv[i]);
+            v[2 * i + 1] = bf16_to_float(hv[i] >> 16);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 f = *(const float4*)(xs + m * K + g * QK + 16 * p + 4 * q);
+            v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+          }
         }
         // the steps of q8k_part16, piece p of block g going to 16 (p NB + g)
         float amax = 0.0f;
@@ -360,7 +379,7 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
 #pragma unroll
         for (int i = 0; i < kC; ++i) acc = L::fold(acc, xx[i], vv[i], dd[i]);
       }
-      y[(size_t)fm * ldy + n0 + fr] = gave_up ? __builtin_nanf("") : acc;
+      y.put((size_t)fm * ldy + n0 + fr, gave_up ? __builtin_nanf("") : acc);
     }
     if (!LOOP || next >= n_sets) break;
     // the next set into the stage once this one's reads have returned (issued after the fold:
@@ -375,12 +394,12 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
 // LOOP: waves may take more than one row set (a single pass compiles without the set loop)
 template <int TYPE, int NB, bool FUSEQ, bool ACTREG, int MAXM, bool LOOP>
 __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
-    const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int N,
+    const uint8_t* __restrict__ w, const float* __restrict__ x, YOut y, int N,
     int row_bytes, uint32_t pack, int ldy, const int8_t* __restrict__ aq,
     const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
   wave_rows<TYPE, NB, FUSEQ, ACTREG, MAXM, LOOP>(w, x, y, N, row_bytes, pack & 0xFF, (pack >> 8) & 0xFF,
-                                           (pack >> 16) & 0xFF, ldy, aq, ad, abs_, blockIdx.x,
-                                           gridDim.x, (int)(pack >> 24));
+                                           (pack >> 16) & 0x7F, ldy, aq, ad, abs_, blockIdx.x,
+                                           gridDim.x, (int)(pack >> 24), ((pack >> 23) & 1) != 0);
 }
 
 // Several weights that share the activation row (q|k|v, gate|up), one launch: each weight's
@@ -389,12 +408,13 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_kernel(
 constexpr int kWaveMaxSegs = 4;
 struct WaveSeg {
   const uint8_t* w;
-  float* y;
+  YOut y;
   int n, row_bytes, type, wg0, waves, n_wg;
 };
 struct WaveSegs {
   WaveSeg s[kWaveMaxSegs];
   int count;
+  int xbf16;  // x holds bfloat16 values
 };
 
 template <int NB, bool FUSEQ, bool LOOP>
@@ -409,13 +429,13 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
   const int wg = (int)blockIdx.x - g.wg0;
   if (g.type == T_Q4_K)
     wave_rows<T_Q4_K, NB, FUSEQ, true, 1, LOOP>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq,
-                                                ad, abs_, wg, g.n_wg);
+                                                ad, abs_, wg, g.n_wg, 0, segs.xbf16 != 0);
   else if (g.type == T_Q8_0)
     wave_rows<T_Q8_0, NB, FUSEQ, true, 1, LOOP>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0, aq,
-                                                ad, abs_, wg, g.n_wg);
+                                                ad, abs_, wg, g.n_wg, 0, segs.xbf16 != 0);
   else
     wave_rows<T_Q6_K, NB, FUSEQ, false, 1, LOOP>(g.w, x, g.y, g.n, g.row_bytes, g.waves, nq, 1, 0,
-                                                 aq, ad, abs_, wg, g.n_wg);
+                                                 aq, ad, abs_, wg, g.n_wg, 0, segs.xbf16 != 0);
 }
 
 // One token's routed experts (MoE decode): pair p multiplies expert ids[p] (a device array; an id
@@ -425,7 +445,7 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_multi_kernel(
 template <int TYPE, int NB, bool FUSEQ, bool ACTREG, bool LOOP>
 __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_pairs_kernel(
     const uint8_t* __restrict__ w, long long expert_stride, const int32_t* __restrict__ ids,
-    int n_experts, const float* __restrict__ x, int x_step, float* __restrict__ y, int N,
+    int n_experts, const float* __restrict__ x, int x_step, YOut y, int N,
     int row_bytes, uint32_t pack, int G, const int8_t* __restrict__ aq,
     const float* __restrict__ ad, const int16_t* __restrict__ abs_) {
   constexpr int K = NB * QK;
@@ -433,17 +453,18 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_pairs_kernel(
   const int e = min(max(ids[p], 0), n_experts - 1);
   const size_t r = (size_t)p * x_step;  // the pair's activation row
   wave_rows<TYPE, NB, FUSEQ, ACTREG, 1, LOOP>(
-      w + (size_t)e * expert_stride, FUSEQ ? x + r * K : x, y + (size_t)p * N, N, row_bytes,
+      w + (size_t)e * expert_stride, FUSEQ ? x + r * K : x, y.at((size_t)p * N), N, row_bytes,
       pack & 0xFF, (pack >> 8) & 0xFF, 1, 0, FUSEQ ? aq : aq + r * K, FUSEQ ? ad : ad + r * NB,
       FUSEQ ? abs_ : abs_ + r * NB * 16, wg, G);
 }
 
 template <int TYPE, int NB, bool FUSEQ, int MAXM>
-int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                   int M, int N, hipStream_t stream) {
   constexpr bool kXF = ActTraits<TYPE>::kFloat, kSums = ActTraits<TYPE>::kSums;
   // activation registers: not for Q6_K (its compute leaves no room for them) or float x
   constexpr bool kReg = !kXF && TYPE != T_Q6_K && MAXM == 1;
+  if (kXF && act.xbf16) return -1;  // float activations are staged as float32 only
   constexpr int R = 64 / NB;
   const int ncu = cu_count();
   const int per_cu = (int)(((long long)N + ncu - 1) / ncu);
@@ -481,14 +502,15 @@ int launch_wave_t(const uint8_t* w, long long row_bytes, const Act& act, float* 
                                               : gemv_wave_kernel<TYPE, NB, FUSEQ, kReg, MAXM, false>;
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, w, act.x, y, N, (int)row_bytes,
-                     (uint32_t)waves | (uint32_t)nq << 8 | (uint32_t)M << 16 | (uint32_t)late << 24,
+                     (uint32_t)waves | (uint32_t)nq << 8 |
+                         (uint32_t)(M | (FUSEQ && act.xbf16 ? 0x80 : 0)) << 16 | (uint32_t)late << 24,
                      (int)ldy, act.q,
                      act.d, act.bsums);
   return 0;
 }
 
 template <int TYPE, int NB, int MAXM>
-int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                   int M, int N, hipStream_t stream) {
   if constexpr (ActTraits<TYPE>::kFloat)  // float activations, staged unquantized
     return act.q == nullptr ? launch_wave_t<TYPE, NB, false, MAXM>(w, row_bytes, act, y, ldy, M, N, stream)
@@ -510,7 +532,7 @@ int launch_wave_m(const uint8_t* w, long long row_bytes, const Act& act, float* 
 // 20.4 / 28 / 40 vs 28.7 / 38.8 / 58.9, IQ4_XS 14336 x 4096 22.8 / 27.7 / 37.8 vs 31.9 / 43.3 /
 // 50.3; Q8_0 two rows only (4096 x 4096 10.8 vs 13.4; three rows 15.2 vs 14.5).
 template <int TYPE, int NB>
-int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                    int M, int N, hipStream_t stream) {
   if (M == 1) return launch_wave_m<TYPE, NB, 1>(w, row_bytes, act, y, ldy, M, N, stream);
   if constexpr (NB == 8 || NB == 16 || NB == 32) {
@@ -522,7 +544,7 @@ int launch_wave_nb(const uint8_t* w, long long row_bytes, const Act& act, float*
 }
 
 template <int TYPE>
-int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_wave_type(const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                      long long ldy, int M, int N, hipStream_t stream) {
   switch (act.nb) {
     case 4: return launch_wave_nb<TYPE, 4>(w, row_bytes, act, y, ldy, M, N, stream);
@@ -570,6 +592,7 @@ int launch_wave_multi_t(const DecodeSeg* seg, int count, const Act& act, hipStre
   }
   WaveSegs segs{};
   segs.count = count;
+  segs.xbf16 = FUSEQ && act.xbf16 ? 1 : 0;
   int grid = 0, nw = min(kWaveMaxWaves, NB / 4), lds = act_lds;
   bool loop = false;
   for (int i = 0; i < count; ++i) {
@@ -605,7 +628,7 @@ int launch_wave_multi_nb(const DecodeSeg* seg, int count, const Act& act, hipStr
 template <int TYPE, int NB, bool FUSEQ>
 int launch_pairs_t(const uint8_t* w, long long row_bytes, long long expert_stride,
                    const int32_t* ids, int n_experts, int n_pairs, int x_step, const Act& act,
-                   float* y, int N, hipStream_t stream) {
+                   YOut y, int N, hipStream_t stream) {
   constexpr bool kReg = TYPE != T_Q6_K;
   constexpr int R = 64 / NB;
   if constexpr (NB == 56 && FUSEQ && TYPE != T_Q4_K) return -1;
@@ -635,7 +658,7 @@ int launch_pairs_t(const uint8_t* w, long long row_bytes, long long expert_strid
 template <int TYPE, int NB>
 int launch_pairs_nb(const uint8_t* w, long long row_bytes, long long expert_stride,
                     const int32_t* ids, int n_experts, int n_pairs, int x_step, const Act& act,
-                    float* y, int N, hipStream_t stream) {
+                    YOut y, int N, hipStream_t stream) {
   return act.q == nullptr
              ? launch_pairs_t<TYPE, NB, true>(w, row_bytes, expert_stride, ids, n_experts, n_pairs,
                                               x_step, act, y, N, stream)
@@ -646,7 +669,7 @@ int launch_pairs_nb(const uint8_t* w, long long row_bytes, long long expert_stri
 template <int TYPE>
 int launch_pairs_type(const uint8_t* w, long long row_bytes, long long expert_stride,
                       const int32_t* ids, int n_experts, int n_pairs, int x_step, const Act& act,
-                      float* y, int N, hipStream_t stream) {
+                      YOut y, int N, hipStream_t stream) {
   switch (act.nb) {
 #define MXA_PAIRS_NB(nb) \
   case nb: return launch_pairs_nb<TYPE, nb>(w, row_bytes, expert_stride, ids, n_experts, n_pairs, x_step, act, y, N, stream);
@@ -663,7 +686,7 @@ int launch_pairs_type(const uint8_t* w, long long row_bytes, long long expert_st
 
 }  // namespace
 
-int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                        long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (n_rows < 1 || m_rows < 1 || m_rows > 4) return -1;
   if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF) return -1;
@@ -686,9 +709,10 @@ int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Ac
   }
 }
 
-int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                          long long ldy, int m_rows, int n_rows, hipStream_t stream) {
-  if (n_rows < 1 || m_rows < 1 || m_rows > 4 || act.q != nullptr || ((uintptr_t)act.x & 15) != 0)
+  if (n_rows < 1 || m_rows < 1 || m_rows > 4 || act.q != nullptr || act.xbf16 ||
+      ((uintptr_t)act.x & 15) != 0)
     return -1;
   if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF) return -1;
   switch (type) {
@@ -699,7 +723,7 @@ int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const 
   }
 }
 
-int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                      int n_rows, hipStream_t stream) {
   return launch_gemv_wave_m(type, w, row_bytes, act, y, n_rows, 1, n_rows, stream);
 }
@@ -727,8 +751,9 @@ int launch_gemv_wave_multi(const DecodeSeg* seg, int count, const Act& act, hipS
 
 int launch_gemv_wave_pairs(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
                            const int32_t* ids, int n_experts, int n_pairs, int x_step,
-                           const Act& act, float* y, int n_rows, hipStream_t stream) {
-  if (n_rows < 1 || n_pairs < 1 || n_experts < 1 || ids == nullptr || (x_step != 0 && x_step != 1))
+                           const Act& act, YOut y, int n_rows, hipStream_t stream) {
+  if (n_rows < 1 || n_pairs < 1 || n_experts < 1 || ids == nullptr || (x_step != 0 && x_step != 1) ||
+      act.xbf16)
     return -1;
   if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF ||
       expert_stride % 16 != 0 || expert_stride < (long long)n_rows * row_bytes)

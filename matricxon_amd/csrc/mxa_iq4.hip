@@ -94,7 +94,7 @@ template <int MT>
 __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t* w, long long row_bytes,
                                                                    const uint16_t* __restrict__ xh,
                                                                    const uint16_t* __restrict__ xl,
-                                                                   int K, float* __restrict__ y,
+                                                                   int K, YOut y,
                                                                    long long ldy, int M, int N) {
   constexpr int kRows = 16 * MT;
   constexpr int kBuf = 2 * kRows * kXStride;                  // hi rows, then lo rows
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = m0 + 16 * mt + 4 * g + i;
-      if (m < M && n < N) y[(size_t)m * ldy + n] = acc[mt][i];
+      if (m < M && n < N) y.put((size_t)m * ldy + n, acc[mt][i]);
     }
 }
 
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t
 size_t iq4_prefill_workspace(int m_rows, int k) { return (size_t)m_rows * k * 2 * 2; }
 
 int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, void* workspace,
-                       float* y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream) {
+                       YOut y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream) {
   uint16_t* hi = (uint16_t*)workspace;
   uint16_t* lo = hi + (size_t)m_rows * k;
   const long long n4 = (long long)m_rows * k / 4;

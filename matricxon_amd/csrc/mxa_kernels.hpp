@@ -73,6 +73,11 @@ inline ActBuffers act_layout(void* ws, int m_rows, int k) {
 
 void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
                          hipStream_t stream);
+// The same from bfloat16 x (x widened exactly first; x 16-byte aligned).
+void launch_quantize_q8k_bf16(const uint16_t* x, const ActBuffers& a, int m_rows, int k,
+                              hipStream_t stream);
+// out[i] = x[i] widened from bfloat16 to float32 (n a multiple of 4; x 8-, out 16-byte aligned).
+void launch_widen_bf16(const uint16_t* x, float* out, long long n, hipStream_t stream);
 
 // Fused producers: RMSNorm (mx_rms_norm, app/native/src/mx_fused_ops.c:6-17) and SwiGLU's
 // silu(gate) * up (mx_silu_mul, mx_fused_ops.c:36-42) over m_rows rows of k values, writing the fp32
@@ -82,6 +87,13 @@ void launch_rms_norm_q8k(const float* x, const float* w, float eps, float* out, 
 // gate and up rows are ld floats apart.
 void launch_silu_mul_q8k(const float* gate, const float* up, long long ld, float* out,
                          const ActBuffers& a, int m_rows, int k, hipStream_t stream);
+// The bfloat16 forms, with the reference's torch steps for a bfloat16 layer (each elementwise
+// result rounded to bfloat16 as torch rounds it); Q8_K of the bfloat16 result. -1 when the rows
+// are too long (RMSNorm: above 16384 values) or the operands not 8-byte aligned (ld % 4 != 0).
+int launch_rms_norm_q8k_bf16(const uint16_t* x, const uint16_t* w, float eps, uint16_t* out,
+                             const ActBuffers& a, int m_rows, int k, hipStream_t stream);
+int launch_silu_mul_q8k_bf16(const uint16_t* gate, const uint16_t* up, long long ld, uint16_t* out,
+                             const ActBuffers& a, int m_rows, int k, hipStream_t stream);
 
 // Reads bytes (a multiple of 16) at src once and discards them; may write one word to sink.
 void launch_stream_read(const void* src, long long bytes, uint32_t* sink, hipStream_t stream);
@@ -121,35 +133,35 @@ void set_fused_max_rows(int n);
 // Decode GEMV for 1 <= m_rows <= 4: y[m * ldy + n] for m < m_rows, n < n_rows (out_features) of
 // one packed weight, lane-per-block compute on weight rows staged into LDS by coalesced copies. A
 // K-quant or Q8_0 weight with act.q == nullptr quantizes act.x to Q8_K in the kernel.
-int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                     long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // The same GEMV on float activations (x is not quantized; the K-quants and Q8_0 take each block
 // as d * sc * q - dmin * m in float against x, IQ4_XS as always): y[m * ldy + n] for
 // m < m_rows <= 4, n < n_rows, from x (m_rows, k) row-major.
 int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float* x, int k,
-                    float* y, long long ldy, int m_rows, int n_rows, hipStream_t stream);
+                    YOut y, long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Decode GEMV in the read floor's shape (mxa_gemv_wave.hip): one workgroup per CU, every weight
 // byte requested at once, lane-per-block compute as each wave's rows land. y[m * ldy + n] for
 // m < m_rows <= 2, n < n_rows; quantizes act.x to Q8_K in the kernel when act.q == nullptr.
 // Q4_K / Q8_0 / Q6_K with K / 256 in {4, 8, 16, 32, 64} (56 on workspace Q8_K; {8, 16, 32} for
 // two rows), 16-byte aligned rows, and the rows per CU the type allows; -1 otherwise.
-int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_wave_m(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                        long long ldy, int m_rows, int n_rows, hipStream_t stream);
 // The same for one activation row.
-int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_wave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                      int n_rows, hipStream_t stream);
 // The fp32-activation forms of Q4_K, Q6_K, Q8_0 (d * sc * q met by unquantized x) on the
 // floor-shaped kernel, m_rows <= 4; -1 where it does not apply.
-int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_wave_f32(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                          long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Decode GEMV for one activation row on a workgroup-resident weight share (mxa_gemv_res.hip):
 // y[n] for n < n_rows. Quantizes act.x to Q8_K in the kernel when act.q == nullptr (IQ4_XS reads
 // it as floats). -1 when the weight is larger than the kernel is used for, or the shape or
 // alignment does not suit it.
-int launch_gemv_res(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_gemv_res(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                      int n_rows, hipStream_t stream);
 
 // One of several packed weights that share the activations of a multi-weight launch.
@@ -157,7 +169,7 @@ struct DecodeSeg {
   int type;
   const uint8_t* w;
   long long row_bytes;
-  float* y;  // the weight's first output column (row stride ldy)
+  YOut y;  // the weight's first output column (row stride ldy)
   int n;     // output rows of the weight
 };
 
@@ -167,7 +179,7 @@ struct DecodeSeg {
 // suit it.
 int launch_gemv_wave_pairs(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
                            const int32_t* ids, int n_experts, int n_pairs, int x_step,
-                           const Act& act, float* y, int n_rows, hipStream_t stream);
+                           const Act& act, YOut y, int n_rows, hipStream_t stream);
 
 // One-row decode over up to 4 Q4_K / Q6_K / Q8_0 weights sharing the activations, in the
 // floor-shaped kernel (mxa_gemv_wave.hip); -1 when the weights do not suit it.
@@ -182,7 +194,7 @@ int launch_decode_multi(const DecodeSeg* seg, int count, const Act& act, long lo
 // Matrix-core kernel for m_rows > 4 (batched decode and prefill) on Q8_K activations already in
 // the workspace: Q4_K, Q6_K, Q8_0.
 bool mtile_supported(int type);
-int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Grouped MoE projection (mxa_mtile.hip): expert e of n_experts multiplies rows
@@ -192,7 +204,7 @@ int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act
 // otherwise.
 int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
                    int n_experts, const Act& act, const int32_t* offsets, int total_rows,
-                   int max_rows, float* y, long long ldy, int n_rows, hipStream_t stream);
+                   int max_rows, YOut y, long long ldy, int n_rows, hipStream_t stream);
 
 // out[t] (n_tokens x n_embd fp32) = the routing-weighted sum of token t's expert outputs:
 // down row rows[t top_k + k] (rows == nullptr: row t top_k + k) of slot k, times weights[t top_k
@@ -206,20 +218,20 @@ int launch_moe_combine(const float* down, const int32_t* rows, const int32_t* id
 // Batched decode (m_rows <= 16) on the matrix cores with the weight rows streamed into LDS by
 // coalesced copies, one persistent workgroup per CU: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
 // workspace. -1 when the shape does not suit it (the caller uses launch_mtile).
-int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Batched decode (m_rows <= 16, rows of up to 16 blocks) with the workgroup's whole weight share
 // resident in LDS, streamed in by copy waves while compute waves run the matrix cores
 // (mxa_bflow.hip): Q4_K, Q6_K, Q8_0 on Q8_K activations in the workspace, 16-byte aligned weight
 // and rows. -1 when the share does not fit LDS (the caller uses launch_bres).
-int launch_bflow(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_bflow(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 // Batched decode (m_rows <= 16, rows of up to 16 blocks) with each workgroup's weight rows
 // streamed through LDS in 16-row tiles, in order: Q4_K, Q6_K, Q8_0 on Q8_K activations in the
 // workspace. -1 when the geometry does not fit (the caller uses launch_bstream).
-int launch_bres(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_bres(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
 // The same over up to 4 weights sharing the activations, in one launch.
 int launch_bres_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
@@ -235,10 +247,10 @@ int launch_bstream_multi(const DecodeSeg* seg, int count, const Act& act, long l
 constexpr int kIq4MfmaMinRows = 17;
 size_t iq4_prefill_workspace(int m_rows, int k);
 int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, void* workspace,
-                       float* y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream);
+                       YOut y, long long ldy, int m_rows, int k, int n_rows, hipStream_t stream);
 
 // The matmul for any m_rows: picks the kernel (mxa_dispatch.hip); -1 when no kernel applies.
-int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_matmul(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                   long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
 }  // namespace mxa

@@ -32,7 +32,7 @@ constexpr int kMtBuf = ((16 * MT * kQStride + 16 * MT * kBStride * 2 + kCB * 16 
 // Row-tiled kernel: MT activation tiles x NT weight tiles of 16 rows per wave, WAVES waves.
 template <int TYPE, int MT, int NT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                           float* __restrict__ y, long long ldy, int M,
+                                                           YOut y, long long ldy, int M,
                                                            int N) {
   using Tile = typename TileOf<TYPE>::T;
   using W = typename Tile::W;
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = m0 + 16 * mt + 4 * g + i;
-        if (m < M && n < N) y[(size_t)m * ldy + n] = acc[mt][nt][i];
+        if (m < M && n < N) y.put((size_t)m * ldy + n, acc[mt][nt][i]);
       }
   }
 }
@@ -211,7 +211,7 @@ constexpr int kDecBStride = kDecCh * 16 + 8;
 // rows.
 template <int TYPE, int kDecRT>
 __device__ __forceinline__ void mdec_rows(const uint8_t* w, long long row_bytes, const Act& act,
-                                          float* __restrict__ y, long long ldy, int M, int N, int wg,
+                                          YOut y, long long ldy, int M, int N, int wg,
                                           int n_wg) {
   using Tile = typename TileOf<TYPE>::T;
   using W = typename Tile::W;
@@ -311,13 +311,13 @@ __device__ __forceinline__ void mdec_rows(const uint8_t* w, long long row_bytes,
 #pragma unroll
   for (int k = 0; k < kOut; ++k) {
     const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15, n = n0 + 16 * t + (idx & 15);
-    if (m < M && n < N) y[(size_t)m * ldy + n] = acc[k];
+    if (m < M && n < N) y.put((size_t)m * ldy + n, acc[k]);
   }
 }
 
 template <int TYPE, int kDecRT>
 __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long row_bytes, Act act,
-                                                   float* __restrict__ y, long long ldy, int M, int N) {
+                                                   YOut y, long long ldy, int M, int N) {
   mdec_rows<TYPE, kDecRT>(w, row_bytes, act, y, ldy, M, N, blockIdx.x, gridDim.x);
 }
 
@@ -332,7 +332,7 @@ template <int TYPE, int kDecRT>
 __global__ __launch_bounds__(256) void moe_dec_kernel(const uint8_t* w, long long row_bytes,
                                                       long long expert_stride, Act act,
                                                       const int32_t* __restrict__ offsets,
-                                                      int total_rows, float* __restrict__ y,
+                                                      int total_rows, YOut y,
                                                       long long ldy, int N) {
   const int e = blockIdx.y;
   const int begin = min(max(offsets[e], 0), total_rows);
@@ -343,14 +343,14 @@ __global__ __launch_bounds__(256) void moe_dec_kernel(const uint8_t* w, long lon
     a.q = act.q + (size_t)p0 * act.k;
     a.d = act.d + (size_t)p0 * act.nb;
     a.bsums = act.bsums + (size_t)p0 * act.nb * 16;
-    mdec_rows<TYPE, kDecRT>(w + (size_t)e * expert_stride, row_bytes, a, y + (size_t)p0 * ldy, ldy,
+    mdec_rows<TYPE, kDecRT>(w + (size_t)e * expert_stride, row_bytes, a, y.at((size_t)p0 * ldy), ldy,
                             M, N, blockIdx.x, gridDim.x);
     __syncthreads();  // the next chunk rewrites the LDS tiles this one read
   }
 }
 
 template <int TYPE, int MT, int NT, int WAVES>
-int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy, int M,
+int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
               int N, hipStream_t stream) {
   constexpr int kLds = 2 * kMtBuf<MT>;
   allow_lds((const void*)mtile_kernel<TYPE, MT, NT, WAVES>, kLds);
@@ -362,7 +362,7 @@ int launch_mt(const uint8_t* w, long long row_bytes, const Act& act, float* y, l
 }
 
 template <int TYPE>
-int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, float* y, long long ldy,
+int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
                    int M, int N, hipStream_t stream) {
   // M <= 16: the streaming kernel, else the block-split kernel unless the 64-row tiles alone give
   // >= 512 workgroups
@@ -390,7 +390,7 @@ bool mtile_supported(int type) { return type == T_Q4_K || type == T_Q6_K || type
 
 int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
                    int n_experts, const Act& act, const int32_t* offsets, int total_rows,
-                   int max_rows, float* y, long long ldy, int n_rows, hipStream_t stream) {
+                   int max_rows, YOut y, long long ldy, int n_rows, hipStream_t stream) {
   if (act.q == nullptr || n_experts < 1 || n_experts > 65535 || max_rows < 1 || n_rows < 1 ||
       total_rows < 1)
     return -1;
@@ -410,7 +410,7 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
   }
 }
 
-int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, float* y,
+int launch_mtile(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream) {
   if (act.q == nullptr || m_rows < 1) return -1;
   switch (type) {

@@ -10,7 +10,9 @@ namespace mxa {
 
 // 16 lanes per (row m, 256-value block b), four blocks per wave; lane part p owns elements
 // 16p..16p+15 (q8k_part16 in mxa_kernels.hpp does the arithmetic).
-__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
+// x is float32, or bfloat16 (BF16; widened exactly before the same steps).
+template <bool BF16>
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const void* __restrict__ x,
                                                            int8_t* __restrict__ q,
                                                            float* __restrict__ d,
                                                            int16_t* __restrict__ bsums, int m_rows,
@@ -21,10 +23,21 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
   const int m = blk / nb, b = blk - m * nb;
   const size_t base = (size_t)m * k + (size_t)b * QK + 16 * p;
   float v[16];
+  if constexpr (BF16) {
+    const uint16_t* xh = (const uint16_t*)x + base;
+    const uint4 a = *(const uint4*)xh, c = *(const uint4*)(xh + 8);
+    const uint32_t hv[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 f = *(const float4*)(x + base + 4 * i);
-    v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = bf16_to_float(hv[i]);
+      v[2 * i + 1] = bf16_to_float(hv[i] >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 f = *((const float4*)x + base / 4 + i);
+      v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+    }
   }
   q8k_part16(v, p, q + (size_t)m * k + (size_t)b * QK, bsums + ((size_t)m * nb + b) * 16,
              d + (size_t)m * nb + b);
@@ -35,8 +48,33 @@ void launch_quantize_q8k(const float* x, const ActBuffers& a, int m_rows, int k,
   const int nb = k / QK;
   const int blocks = m_rows * nb;
   const int grid = (blocks + 15) / 16;
-  hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, stream, x, a.q, a.d, a.bsums,
-                     m_rows, k, nb);
+  hipLaunchKernelGGL(quantize_q8k_kernel<false>, dim3(grid), dim3(256), 0, stream, x, a.q, a.d,
+                     a.bsums, m_rows, k, nb);
+}
+
+void launch_quantize_q8k_bf16(const uint16_t* x, const ActBuffers& a, int m_rows, int k,
+                              hipStream_t stream) {
+  const int nb = k / QK;
+  const int blocks = m_rows * nb;
+  const int grid = (blocks + 15) / 16;
+  hipLaunchKernelGGL(quantize_q8k_kernel<true>, dim3(grid), dim3(256), 0, stream, x, a.q, a.d,
+                     a.bsums, m_rows, k, nb);
+}
+
+// bfloat16 -> float32, exactly, four values per thread (n a multiple of 4, both 8-byte aligned).
+__global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x,
+                                                         float* __restrict__ out, long long n4) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const uint2 h = ((const uint2*)x)[i];
+  ((float4*)out)[i] = float4{bf16_to_float(h.x), bf16_to_float(h.x >> 16), bf16_to_float(h.y),
+                             bf16_to_float(h.y >> 16)};
+}
+
+void launch_widen_bf16(const uint16_t* x, float* out, long long n, hipStream_t stream) {
+  const long long n4 = n / 4;
+  hipLaunchKernelGGL(widen_bf16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
+                     x, out, n4);
 }
 
 // ---------------------------------------------------------------------------------------------

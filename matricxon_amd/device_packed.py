@@ -13,8 +13,11 @@ dequantizing with torch ops and calling `F.linear`.
   n_rows rows (device_packed.py:14-19).
 * `HipDequantizer`: the `TorchDequantizer` interface (torch_dequant.py:221-236) on the kernels.
 
-A float32 input that a fused producer (`matricxon_amd.fused_ops.HipFusedOps`) just wrote comes
-with its Q8_K blocks; `DevicePackedLinear` then runs the matmul alone on them.
+A bfloat16 layer (the reference's GPU dtype) reads bfloat16 x and writes bfloat16 y straight from
+the kernels (`mxa_gemm_bf16`: each output the float32 result rounded as torch's cast), so a call is
+one library call with no cast launches. An input that a fused producer
+(`matricxon_amd.fused_ops.HipFusedOps`) just wrote comes with its Q8_K blocks;
+`DevicePackedLinear` then runs the matmul alone on them.
 
 Only Q8_0, Q4_K, Q6_K and IQ4_XS (with in_features % 256 == 0) are computed here; a loader
 asks `HipDequantizer.supports` / `HipGemm.supports` and keeps the reference module for the rest.
@@ -159,14 +162,23 @@ class DevicePackedLinear(nn.Module):
             return self.finish(self._forward_f32(x.reshape(-1, k)), lead)
         # The reference casts x to the layer dtype before its matmul (device_packed.py:54).
         x = x.to(self._dtype)
+        bf16 = self._dtype == torch.bfloat16  # the kernels read and write bfloat16 themselves
+        dev = self.packed.device
+        n, big_n = x.numel() // k, self.out_features
         ws = HANDOFF.claim(x) if self._ggml_type != _IQ4_XS else None
         if ws is not None:  # x came from a fused producer that also wrote its Q8_K blocks
-            n = x.numel() // k
-            y = torch.empty((n, self.out_features), dtype=torch.float32, device=self.packed.device)
-            self._gemm.matmul_q8k(self._ggml_type, self.packed, ws, None, y, n, self.out_features, k)
+            y = torch.empty((n, big_n), dtype=torch.bfloat16 if bf16 else torch.float32, device=dev)
+            self._gemm.matmul_q8k(self._ggml_type, self.packed, ws, None, y, n, big_n, k)
+        elif bf16 and x.device == dev and n > 0:
+            xb = x.reshape(n, k)
+            if not xb.is_contiguous() or xb.data_ptr() % 16 != 0:
+                xb = xb.clone(memory_format=torch.contiguous_format)
+            y = torch.empty((n, big_n), dtype=torch.bfloat16, device=dev)
+            self._gemm._gemm_bf16(self._ggml_type, self.packed, xb, y, n, big_n, k)
+        elif bf16:
+            y = self._gemm.matmul_bf16(self._ggml_type, self.packed, x.reshape(-1, k), big_n, k)
         else:
-            y = self._gemm.matmul(self._ggml_type, self.packed, x.reshape(-1, k),
-                                  self.out_features, k)
+            y = self._gemm.matmul(self._ggml_type, self.packed, x.reshape(-1, k), big_n, k)
         return self.finish(y, lead)
 
     def _forward_f32(self, x2: torch.Tensor) -> torch.Tensor:

@@ -3,17 +3,21 @@ weights on the GPU:
 
 * `HipFusedOps.rms_norm(x, weight, eps)` / `.silu_mul(gate, up)`: the `FusedOps` methods that
   `RMSNorm.forward` and `SwiGLUMLP.forward` call (app/native/fused_ops.py:152-158, 201-208;
-  app/architectures/layers.py:53-57, 72-76), same contract: the float32 result, or None when the
-  inputs are not handled (not float32 on a GPU, mismatched shapes, a last dimension that is not
-  a multiple of 256) so the caller runs its torch code. Each also writes the Q8_K blocks of its
-  result in the same kernel and hands them to the packed projections that read that result.
+  app/architectures/layers.py:53-57, 72-76), same contract: the result, or None when the inputs
+  are not handled (not all float32 or all bfloat16 on a GPU, mismatched shapes, a last dimension
+  that is not a multiple of 256) so the caller runs its torch code. Float32 inputs get the
+  reference C kernels' float32 steps (mx_fused_ops.c); bfloat16 inputs, the dtype of the
+  reference's GPU layers (app/runtime/compute_device.py:74-78), get the steps of the torch code the
+  reference runs for them (layers.py:53-57, 77-81), each elementwise result rounded to bfloat16
+  where torch rounds it. Each also writes the Q8_K blocks of its result in the same kernel and
+  hands them to the packed projections that read that result.
 * `project_shared(owner, names, x)`: `owner.<name>(x)` for each name, as one
   `mxa_gemm_multi` call when every module is a `DevicePackedLinear` over the same input (the
   device side of app/architectures/shared_projection.py:33-43).
 
 The hand-off keeps, per host thread, the most recent producer result and its Q8_K blocks. A
-projection takes them only when its input is that very result: the same storage and element count,
-float32, unmodified since (a tensor's version counter, shared by its views, moves on any in-place
+projection takes them only when its input is that very result: the same storage, element count
+and dtype, unmodified since (a tensor's version counter, shared by its views, moves on any in-place
 write), on the device and stream the producer ran on. Holding the result keeps its memory from
 being reused by another tensor while the blocks are offered.
 """
@@ -55,10 +59,11 @@ class _Handoff:
         """The Q8_K workspace of x if x is this thread's offered result, unchanged, on the stream
         it was produced on; else None."""
         slot = getattr(self._local, "slot", None)
-        if slot is None or x.dtype != torch.float32 or not x.is_contiguous():
+        if slot is None or not x.is_contiguous():
             return None
         out, version, workspace, device, stream = slot
-        if (x.device != device or x.data_ptr() != out.data_ptr() or x.numel() != out.numel()
+        if (x.dtype != out.dtype or x.device != device or x.data_ptr() != out.data_ptr()
+                or x.numel() != out.numel()
                 or x.shape[-1] != out.shape[-1] or x._version != version
                 or out._version != version or _stream_of(device) != stream):
             return None
@@ -68,8 +73,14 @@ class _Handoff:
 HANDOFF = _Handoff()
 
 
+_RMS_BF16_MAX = 16384  # the bfloat16 RMSNorm kernel's longest row
+
+
 def _handled(*tensors: torch.Tensor) -> bool:
-    return all(t.dtype == torch.float32 and t.device.type == "cuda" for t in tensors)
+    """All on a GPU and all float32, or all bfloat16."""
+    dt = tensors[0].dtype
+    return dt in (torch.float32, torch.bfloat16) and all(
+        t.dtype == dt and t.device.type == "cuda" for t in tensors)
 
 
 class HipFusedOps:
@@ -93,7 +104,8 @@ class HipFusedOps:
     def rms_norm(self, x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor | None:
         """x * (1 / sqrt(mean(x^2) + eps)) * weight over the last dimension (layers.py:72-81)."""
         if (not _handled(x, weight) or weight.dim() != 1 or x.shape[-1] != weight.shape[0]
-                or x.shape[-1] % 256 != 0 or x.numel() == 0):
+                or x.shape[-1] % 256 != 0 or x.numel() == 0
+                or (x.dtype == torch.bfloat16 and x.shape[-1] > _RMS_BF16_MAX)):
             return None
         out, ws = self._gemm.rms_norm_q8k(x, weight, eps)
         out = out.view(x.shape)
@@ -127,9 +139,11 @@ def project_shared(owner: nn.Module, names: tuple[str, ...], x: torch.Tensor) ->
     xd = x.to(dtype)  # each module casts x to its dtype first (device_packed.py:54)
     items = [(m.ggml_type, m.packed, m.out_features) for m in mods]
     gemm = HipGemm.get()
+    bf16 = dtype == torch.bfloat16  # bfloat16 outputs straight from the kernels
     ws = HANDOFF.claim(xd)
     if ws is not None and all(t != _IQ4_XS for t, _, _ in items):
-        ys = gemm.matmul_multi_q8k(items, ws, xd.numel() // k, k)
+        ys = gemm.matmul_multi_q8k(items, ws, xd.numel() // k, k,
+                                   dtype=torch.bfloat16 if bf16 else torch.float32)
     else:
-        ys = gemm.matmul_multi(items, xd.reshape(-1, k))
+        ys = gemm.matmul_multi(items, xd.reshape(-1, k), bf16=bf16)
     return [m.finish(y, lead) for m, y in zip(mods, ys, strict=True)]

@@ -179,6 +179,44 @@ class HipGemm:
         self._calls += 1
         return out
 
+    def matmul_bf16(self, ggml_type: int, packed: torch.Tensor, x: torch.Tensor,
+                    out_features: int, in_features: int,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+        """`matmul` for a bfloat16 layer (`mxa_gemm_bf16`): x (n_tokens, in_features) is taken as
+        bfloat16 (cast first if it is not) and the result (n_tokens, out_features) is bfloat16, each
+        value the float32 result rounded to nearest even as torch's cast rounds it. One library
+        call, no cast launches."""
+        ggml_type = int(ggml_type)
+        if not self.supports(ggml_type, in_features):
+            raise RuntimeError(f"mxa_gemm_bf16 failed with status -1 for type {ggml_type}")
+        self._check_packed(ggml_type, packed, out_features, in_features)
+        xb = x.detach().reshape(-1, in_features)
+        if xb.dtype != torch.bfloat16 or xb.device != packed.device:
+            xb = xb.to(device=packed.device, dtype=torch.bfloat16)
+        xb = _aligned16(xb.contiguous())
+        n_tokens = xb.shape[0]
+        if out is None:
+            out = torch.empty((n_tokens, out_features), dtype=torch.bfloat16, device=packed.device)
+        elif out.shape != (n_tokens, out_features) or out.dtype != torch.bfloat16 or \
+                not out.is_contiguous() or out.device != packed.device:
+            raise ValueError("out must be a contiguous bfloat16 (n_tokens, out_features) tensor")
+        if n_tokens == 0:
+            return out
+        self._gemm_bf16(ggml_type, packed, xb, out, n_tokens, out_features, in_features)
+        return out
+
+    def _gemm_bf16(self, ggml_type: int, packed: torch.Tensor, xb: torch.Tensor,
+                   out: torch.Tensor, n_tokens: int, out_features: int, in_features: int) -> None:
+        """The library call of `matmul_bf16` on checked operands: xb contiguous bfloat16 on
+        packed's device, 16-byte aligned; out contiguous bfloat16."""
+        ws_bytes = self._lib.mxa_workspace_bytes_bf16(ggml_type, n_tokens, in_features)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=packed.device)
+        status = self._lib.mxa_gemm_bf16(ggml_type, packed.data_ptr(), xb.data_ptr(),
+                                         out.data_ptr(), n_tokens, out_features, in_features,
+                                         ws.data_ptr(), ws_bytes, _stream(packed.device))
+        self._check(status, "mxa_gemm_bf16", ggml_type)
+        self._calls += 1
+
     def gemv_f32(self, ggml_type: int, packed: torch.Tensor, x: torch.Tensor, out_features: int,
                  in_features: int, out: torch.Tensor | None = None) -> torch.Tensor:
         """`matmul` with x kept in float32 (never quantized to Q8_K), the numerics of the
@@ -210,8 +248,16 @@ class HipGemm:
                    x: torch.Tensor | None, out: torch.Tensor, n_tokens: int, out_features: int,
                    in_features: int) -> torch.Tensor:
         """The matmul kernel alone on activations already quantized into `workspace` (by
-        `quantize_into`); `x` (float32, contiguous) is read only for IQ4_XS."""
+        `quantize_into`); `x` (float32, contiguous) is read only for IQ4_XS. `out` float32, or
+        bfloat16 for a K-quant / Q8_0 weight (each value rounded as torch's cast)."""
         ggml_type = int(ggml_type)
+        if out.dtype == torch.bfloat16:
+            status = self._lib.mxa_gemm_q8k_bf16(ggml_type, packed.data_ptr(), out.data_ptr(),
+                                                 n_tokens, out_features, in_features,
+                                                 workspace.data_ptr(), workspace.numel(),
+                                                 _stream(packed.device))
+            self._check(status, "mxa_gemm_q8k_bf16", ggml_type)
+            return out
         status = self._lib.mxa_gemm_q8k(ggml_type, packed.data_ptr(),
                                         None if x is None else x.data_ptr(), out.data_ptr(),
                                         n_tokens, out_features, in_features,
@@ -221,21 +267,23 @@ class HipGemm:
         return out
 
     def quantize_into(self, x: torch.Tensor, workspace: torch.Tensor) -> None:
-        """Q8_K activations of x (M, K) float32 contiguous into `workspace` (uint8, at least
-        `q8k_bytes(M, K)` bytes)."""
+        """Q8_K activations of x (M, K) float32 or bfloat16, contiguous, into `workspace` (uint8,
+        at least `q8k_bytes(M, K)` bytes)."""
         m, k = x.shape
-        status = self._lib.mxa_quantize_q8_k(x.data_ptr(), m, k, workspace.data_ptr(),
-                                             workspace.numel(), _stream(x.device))
+        fn = self._lib.mxa_quantize_q8_k_bf16 if x.dtype == torch.bfloat16 else \
+            self._lib.mxa_quantize_q8_k
+        status = fn(x.data_ptr(), m, k, workspace.data_ptr(), workspace.numel(), _stream(x.device))
         self._check(status, "mxa_quantize_q8_k", 15)
 
     def matmul_multi(self, items: list[tuple[int, torch.Tensor, int]], x: torch.Tensor,
-                     out: torch.Tensor | None = None) -> list[torch.Tensor]:
+                     out: torch.Tensor | None = None, bf16: bool = False) -> list[torch.Tensor]:
         """`items`: (ggml_type, packed, out_features) per weight sharing input `x`
         (n_tokens, in_features): one activation quantization, one float32 output per weight,
         as `MultiGemmPlan.run` (app/native/gemm_multi.py:46-61) returns them. For up to 16 tokens
         and K-quant / Q8_0 weights of up to 16 blocks per row this is a single matmul launch.
-        `out`, if given, is the float32 (n_tokens, sum of out_features) result buffer the outputs
-        are views of."""
+        `out`, if given, is the (n_tokens, sum of out_features) result buffer the outputs are
+        views of. `bf16`: x taken as bfloat16 and the outputs bfloat16 (`mxa_gemm_multi_bf16`,
+        a bfloat16 layer's projections)."""
         import ctypes
 
         if not 1 <= len(items) <= 4:
@@ -248,31 +296,34 @@ class HipGemm:
             self._check_packed(int(t), p, o, in_features)
             if p.device != device:
                 raise ValueError("all packed weights must be on one device")
-        x32 = x.detach().reshape(-1, in_features).to(device=device, dtype=torch.float32).contiguous()
-        n_tokens = x32.shape[0]
+        dtype = torch.bfloat16 if bf16 else torch.float32
+        xc = _aligned16(x.detach().reshape(-1, in_features).to(device=device, dtype=dtype)
+                        .contiguous())
+        n_tokens = xc.shape[0]
         outs = [int(o) for _, _, o in items]
         if out is None:
-            y = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
+            y = torch.empty((n_tokens, sum(outs)), dtype=dtype, device=device)
         else:
-            if (out.dtype != torch.float32 or out.device != device or not out.is_contiguous()
+            if (out.dtype != dtype or out.device != device or not out.is_contiguous()
                     or tuple(out.shape) != (n_tokens, sum(outs))):
-                raise ValueError("out must be a contiguous float32 (n_tokens, sum of out_features) "
-                                 "tensor on the weights' device")
+                raise ValueError(f"out must be a contiguous {dtype} (n_tokens, sum of "
+                                 "out_features) tensor on the weights' device")
             y = out
-        # the Q8_K part and the IQ4_XS split part are separate regions of one workspace
+        # the Q8_K part and the IQ4_XS part(s) are separate regions of one workspace
+        size_of = self._lib.mxa_workspace_bytes_bf16 if bf16 else self._lib.mxa_workspace_bytes
         need = {False: 0, True: 0}
         for t, _, _ in items:
             is_iq4 = int(t) == 23
-            need[is_iq4] = max(need[is_iq4], self.workspace_bytes(int(t), n_tokens, in_features))
+            need[is_iq4] = max(need[is_iq4], int(size_of(int(t), n_tokens, in_features)))
         ws_bytes = need[False] + need[True]
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
         n = len(items)
         types = (ctypes.c_int * n)(*[int(t) for t, _, _ in items])
         ptrs = (ctypes.c_void_p * n)(*[p.data_ptr() for _, p, _ in items])
         couts = (ctypes.c_int * n)(*outs)
-        status = self._lib.mxa_gemm_multi(n, types, ptrs, couts, x32.data_ptr(), y.data_ptr(),
-                                          n_tokens, in_features, ws.data_ptr(), ws_bytes,
-                                          _stream(device))
+        fn = self._lib.mxa_gemm_multi_bf16 if bf16 else self._lib.mxa_gemm_multi
+        status = fn(n, types, ptrs, couts, xc.data_ptr(), y.data_ptr(), n_tokens, in_features,
+                    ws.data_ptr(), ws_bytes, _stream(device))
         self._check(status, "mxa_gemm_multi", int(items[0][0]))
         self._calls += 1
         return list(torch.split(y, outs, dim=-1))
@@ -285,6 +336,8 @@ class HipGemm:
         (out float32 (M, K) or None, workspace) where the workspace holds the Q8_K blocks of out,
         ready for `matmul_multi_q8k` / `matmul_q8k`. K must be a multiple of 256."""
         _require_device_tensor("x", x)
+        if x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16:
+            return self._rms_norm_q8k_bf16(x, weight, eps, want_out)
         x32 = x.detach().to(torch.float32).reshape(-1, x.shape[-1]).contiguous()
         w32 = weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
         m, k = x32.shape
@@ -298,6 +351,25 @@ class HipGemm:
         self._check(status, "mxa_rms_norm_q8_k", 15)
         return out, ws
 
+    def _rms_norm_q8k_bf16(self, x: torch.Tensor, weight: torch.Tensor, eps: float,
+                           want_out: bool) -> tuple[torch.Tensor | None, torch.Tensor]:
+        """`rms_norm_q8k` of a bfloat16 layer (x and weight bfloat16): the reference's torch steps
+        for those dtypes (app/architectures/layers.py:77-81), out bfloat16 (M, K), and the Q8_K
+        blocks of out. K up to 16384."""
+        k = x.shape[-1]
+        xb = _aligned16(x.detach().reshape(-1, k).contiguous())
+        wb = _aligned16(weight.detach().to(x.device).contiguous())
+        m = xb.shape[0]
+        if wb.shape != (k,):
+            raise ValueError("weight must have shape (K,) for x (..., K)")
+        out = torch.empty_like(xb) if want_out else None
+        ws = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device=x.device)
+        status = self._lib.mxa_rms_norm_q8_k_bf16(xb.data_ptr(), wb.data_ptr(), float(eps), m, k,
+                                                  None if out is None else out.data_ptr(),
+                                                  ws.data_ptr(), ws.numel(), _stream(x.device))
+        self._check(status, "mxa_rms_norm_q8_k_bf16", 15)
+        return out, ws
+
     def silu_mul_q8k(self, gate: torch.Tensor, up: torch.Tensor,
                      want_out: bool = True) -> tuple[torch.Tensor | None, torch.Tensor]:
         """silu(gate) * up over (..., K) on the device, in float32: (out (M, K) or None,
@@ -309,6 +381,8 @@ class HipGemm:
             raise ValueError("gate and up must have the same shape")
         k = gate.shape[-1]
         g2, u2 = gate.detach().reshape(-1, k), up.detach().reshape(-1, k)
+        if g2.dtype == u2.dtype == torch.bfloat16:
+            return self._silu_mul_q8k_bf16(g2, u2, want_out)
         if not (g2.dtype == u2.dtype == torch.float32 and u2.device == g2.device
                 and g2.stride(-1) == u2.stride(-1) == 1 and g2.stride(0) == u2.stride(0)
                 and g2.stride(0) >= k):
@@ -321,6 +395,26 @@ class HipGemm:
                                              None if out is None else out.data_ptr(),
                                              ws.data_ptr(), ws.numel(), _stream(g2.device))
         self._check(status, "mxa_silu_mul_q8_k", 15)
+        return out, ws
+
+    def _silu_mul_q8k_bf16(self, g2: torch.Tensor, u2: torch.Tensor,
+                           want_out: bool) -> tuple[torch.Tensor | None, torch.Tensor]:
+        """`silu_mul_q8k` of bfloat16 (M, K) gate and up (read in place when they share a row
+        stride, a multiple of 4, with unit column stride and 8-byte aligned data, as the halves of a
+        gate|up output): torch's steps for bfloat16 tensors, out bfloat16."""
+        k = g2.shape[-1]
+        if not (u2.device == g2.device and g2.stride(-1) == u2.stride(-1) == 1
+                and g2.stride(0) == u2.stride(0) and g2.stride(0) >= k and g2.stride(0) % 4 == 0
+                and g2.data_ptr() % 8 == 0 and u2.data_ptr() % 8 == 0):
+            g2 = _aligned16(g2.contiguous())
+            u2 = _aligned16(u2.to(g2.device).contiguous())
+        m = g2.shape[0]
+        out = torch.empty((m, k), dtype=torch.bfloat16, device=g2.device) if want_out else None
+        ws = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device=g2.device)
+        status = self._lib.mxa_silu_mul_q8_k_bf16(g2.data_ptr(), u2.data_ptr(), g2.stride(0), m, k,
+                                                  None if out is None else out.data_ptr(),
+                                                  ws.data_ptr(), ws.numel(), _stream(g2.device))
+        self._check(status, "mxa_silu_mul_q8_k_bf16", 15)
         return out, ws
 
     def matmul_moe(self, ggml_type: int, experts: torch.Tensor, x: torch.Tensor | None,
@@ -445,10 +539,11 @@ class HipGemm:
         return out
 
     def matmul_multi_q8k(self, items: list[tuple[int, torch.Tensor, int]], workspace: torch.Tensor,
-                         n_tokens: int, in_features: int,
-                         out: torch.Tensor | None = None) -> list[torch.Tensor]:
+                         n_tokens: int, in_features: int, out: torch.Tensor | None = None,
+                         dtype: torch.dtype = torch.float32) -> list[torch.Tensor]:
         """`matmul_multi` on activations already quantized into `workspace` (by a fused producer
-        or `quantize_into`); K-quant and Q8_0 weights only."""
+        or `quantize_into`); K-quant and Q8_0 weights only. Outputs float32, or bfloat16 (`dtype`,
+        or `out`'s dtype) rounded as torch's cast."""
         import ctypes
 
         if not 1 <= len(items) <= 4:
@@ -460,18 +555,19 @@ class HipGemm:
             self._check_packed(int(t), p, o, in_features)
         outs = [int(o) for _, _, o in items]
         if out is None:
-            out = torch.empty((n_tokens, sum(outs)), dtype=torch.float32, device=device)
-        elif (out.dtype != torch.float32 or out.device != device or not out.is_contiguous()
-              or tuple(out.shape) != (n_tokens, sum(outs))):
-            raise ValueError("out must be a contiguous float32 (n_tokens, sum of out_features) "
-                             "tensor on the weights' device")
+            out = torch.empty((n_tokens, sum(outs)), dtype=dtype, device=device)
+        elif (out.dtype not in (torch.float32, torch.bfloat16) or out.device != device
+              or not out.is_contiguous() or tuple(out.shape) != (n_tokens, sum(outs))):
+            raise ValueError("out must be a contiguous float32 or bfloat16 (n_tokens, sum of "
+                             "out_features) tensor on the weights' device")
         n = len(items)
         types = (ctypes.c_int * n)(*[int(t) for t, _, _ in items])
         ptrs = (ctypes.c_void_p * n)(*[p.data_ptr() for _, p, _ in items])
         couts = (ctypes.c_int * n)(*outs)
-        status = self._lib.mxa_gemm_multi_q8k(n, types, ptrs, couts, out.data_ptr(), n_tokens,
-                                              in_features, workspace.data_ptr(), workspace.numel(),
-                                              _stream(device))
+        fn = self._lib.mxa_gemm_multi_q8k_bf16 if out.dtype == torch.bfloat16 else \
+            self._lib.mxa_gemm_multi_q8k
+        status = fn(n, types, ptrs, couts, out.data_ptr(), n_tokens, in_features,
+                    workspace.data_ptr(), workspace.numel(), _stream(device))
         self._check(status, "mxa_gemm_multi_q8k", int(items[0][0]))
         self._calls += 1
         return list(torch.split(out, outs, dim=-1))
