@@ -186,7 +186,10 @@ int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_t
  * expert with more rows is still computed whole, by looping. x == NULL:
  * `workspace` already holds the Q8_K activations of the n_rows rows (mxa_quantize_q8_k,
  * mxa_silu_mul_q8_k). workspace: mxa_quantize_q8_k's layout for n_rows rows. Each row equals
- * mxa_gemm of that row alone bit for bit. Q4_K, Q6_K, Q8_0 (IQ4_XS: -1).
+ * mxa_gemm of that row alone bit for bit. Q4_K, Q6_K, Q8_0; IQ4_XS multiplies the float rows of x
+ * (x required, no workspace) with the decode kernels' arithmetic, so each row equals mxa_gemm of
+ * that row alone, and an expert's rows equal mxa_gemm of them together while it has up to 16
+ * (from 17 rows mxa_gemm takes the matrix cores: within the bound stated there).
  * Replaces the per-expert loop of `QuantizedMoEExperts.forward`
  * (app/architectures/moe_experts.py:81-88: one `DevicePackedLinear` call per active expert and
  * projection, after a host sync on the routed expert ids). */

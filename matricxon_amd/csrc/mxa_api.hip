@@ -351,14 +351,23 @@ int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_ex
                  const float* x, const int32_t* offsets, int n_rows, int max_rows_per_expert,
                  float* y, int out_features, int in_features, void* workspace,
                  size_t workspace_bytes, void* stream) {
-  if (!mxa_supports(ggml_type, in_features) || !needs_q8k(ggml_type) || w == nullptr ||
-      offsets == nullptr || y == nullptr || n_experts < 1 || n_rows < 1 || out_features < 1 ||
+  if (!mxa_supports(ggml_type, in_features) || w == nullptr || offsets == nullptr ||
+      y == nullptr || n_experts < 1 || n_rows < 1 || out_features < 1 ||
       max_rows_per_expert < 1 || !aligned(w, 4) || !aligned(x, 16) || !aligned(workspace, 16))
     return MXA_ERR_UNSUPPORTED;
   // every expert's weight starts as aligned as mxa_gemm asks of its w
   const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
   if (expert_stride < (long long)out_features * rb || expert_stride % 4 != 0)
     return MXA_ERR_UNSUPPORTED;
+  if (!needs_q8k(ggml_type)) {  // IQ4_XS: float activations, no workspace
+    if (x == nullptr) return MXA_ERR_UNSUPPORTED;
+    const mxa::Act act = make_act(x, nullptr, in_features);
+    if (mxa::launch_moe_lpb(ggml_type, (const uint8_t*)w, rb, expert_stride, n_experts, act,
+                            offsets, n_rows, min(max_rows_per_expert, n_rows), mxa::YOut::f32(y),
+                            out_features, out_features, (hipStream_t)stream) != 0)
+      return MXA_ERR_UNSUPPORTED;
+    return check_launch();
+  }
   if (workspace == nullptr || workspace_bytes < mxa::act_bytes(n_rows, in_features))
     return MXA_ERR_WORKSPACE;
   const mxa::ActBuffers buf = mxa::act_layout(workspace, n_rows, in_features);

@@ -52,11 +52,11 @@ struct Geometry {
   int act_blocks;       // activation blocks staged per pass
 };
 
+// The rows of weight tile blockIdx.x (of gridDim.x) against M <= MAXM activation rows.
 template <int TYPE, int MAXM, bool FUSEQ>
-__global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict__ w,
-                                                       long long row_bytes, Act act,
-                                                       YOut y, long long ldy,
-                                                       int M, int N, Geometry geo) {
+__device__ __forceinline__ void lpb_rows(const uint8_t* __restrict__ w, long long row_bytes,
+                                         const Act& act, YOut y, long long ldy, int M, int N,
+                                         const Geometry& geo) {
   using L = Lpb<TYPE>;
   constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
   constexpr int kActBlk = ActTraits<TYPE>::kBlk;
@@ -210,13 +210,45 @@ __global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict
 }
 
 template <int TYPE, int MAXM, bool FUSEQ>
-int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
-               int M, int N, hipStream_t stream) {
+__global__ __launch_bounds__(512) void gemv_lpb_kernel(const uint8_t* __restrict__ w,
+                                                       long long row_bytes, Act act,
+                                                       YOut y, long long ldy,
+                                                       int M, int N, Geometry geo) {
+  lpb_rows<TYPE, MAXM, FUSEQ>(w, row_bytes, act, y, ldy, M, N, geo);
+}
+
+// Grouped MoE projection on float activations (IQ4_XS experts): expert e = blockIdx.y multiplies
+// its rows [offsets[e], offsets[e + 1]) of x by its weight (w + e * expert_stride), writing the same
+// rows of y, four rows at a time through the decode body: chunk z of the expert's rows by the
+// workgroups of blockIdx.z == z mod gridDim.z, so every row is computed whatever the grid's depth.
+// Each row takes the decode kernels' summation order, so it equals that row multiplied alone. The
+// offsets come from the device: clamped to [0, total_rows), a bad table gives wrong rows, never an
+// access outside x or y.
+template <int TYPE>
+__global__ __launch_bounds__(512) void moe_lpb_kernel(const uint8_t* __restrict__ w,
+                                                      long long row_bytes, long long expert_stride,
+                                                      Act act, const int32_t* __restrict__ offsets,
+                                                      int total_rows, YOut y, long long ldy, int N,
+                                                      Geometry geo) {
+  const int e = blockIdx.y;
+  const int begin = min(max(offsets[e], 0), total_rows);
+  const int end = min(max(offsets[e + 1], begin), total_rows);
+  for (int p0 = begin + 4 * (int)blockIdx.z; p0 < end; p0 += 4 * (int)gridDim.z) {
+    Act a = act;  // rows p0 .. p0 + 3, uniform over the workgroup
+    a.x = act.x + (size_t)p0 * act.k;
+    lpb_rows<TYPE, 4, false>(w + (size_t)e * expert_stride, row_bytes, a, y.at((long long)p0 * ldy),
+                             ldy, min(4, end - p0), N, geo);
+    __syncthreads();  // the next chunk restages the LDS this one read
+  }
+}
+
+// Rows per wave, blocks per pass and LDS of the lane-per-block kernel for MAXM activation rows;
+// false when the workgroup does not fit LDS.
+template <int TYPE, int MAXM>
+bool lpb_geometry(int nb, Geometry& geo, int& nw, int& lds) {
   using L = Lpb<TYPE>;
   constexpr bool kFloatAct = ActTraits<TYPE>::kFloat;
   constexpr int kActBlk = ActTraits<TYPE>::kBlk;
-  const int nb = act.nb;
-  Geometry geo;
   // blocks staged per pass: a wave's 64 lanes, and (float activations, 1 KB per block and row)
   // at most ~40 KB of activations
   const int cap = kFloatAct ? max(1, min(kWaveLanes, 40960 / (MAXM * kActBlk))) : kWaveLanes;
@@ -233,10 +265,17 @@ int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, YOut y, lo
   const int act_lds = MAXM * geo.act_blocks * (kActBlk + 32 + 4) + 16;
   const int wave_lds = geo.reg_bytes + MAXM * 64 * 4 * 2;
   // two workgroups per CU (<= 80 KB each), at most 8 waves
-  int nw = (80 * 1024 - act_lds) / wave_lds;
-  nw = max(1, min(8, nw));
-  const int lds = act_lds + nw * wave_lds;
-  if (lds > 160 * 1024) return -1;
+  nw = max(1, min(8, (80 * 1024 - act_lds) / wave_lds));
+  lds = act_lds + nw * wave_lds;
+  return lds <= 160 * 1024;
+}
+
+template <int TYPE, int MAXM, bool FUSEQ>
+int launch_lpb(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy,
+               int M, int N, hipStream_t stream) {
+  Geometry geo;
+  int nw = 0, lds = 0;
+  if (!lpb_geometry<TYPE, MAXM>(act.nb, geo, nw, lds)) return -1;
   const int tile_rows = geo.rows_per_wave * nw;
   const int grid = (N + tile_rows - 1) / tile_rows;
   auto kern = gemv_lpb_kernel<TYPE, MAXM, FUSEQ>;
@@ -853,6 +892,25 @@ int launch_gemv_lpb(int type, const uint8_t* w, long long row_bytes, const Act& 
     case T_IQ4_XS: return launch_lpb_type<T_IQ4_XS>(w, row_bytes, act, y, ldy, m_rows, n_rows, stream);
     default: return -1;
   }
+}
+
+int launch_moe_lpb(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                   int n_experts, const Act& act, const int32_t* offsets, int total_rows,
+                   int max_rows, YOut y, long long ldy, int n_rows, hipStream_t stream) {
+  if (type != T_IQ4_XS || act.x == nullptr || act.xbf16 || ((uintptr_t)act.x & 15) != 0 ||
+      n_experts < 1 || n_experts > 65535 || max_rows < 1 || n_rows < 1 || total_rows < 1)
+    return -1;
+  Geometry geo;
+  int nw = 0, lds = 0;
+  if (!lpb_geometry<T_IQ4_XS, 4>(act.nb, geo, nw, lds)) return -1;
+  const int chunks = min((max_rows + 3) / 4, 65535);
+  const int tile_rows = geo.rows_per_wave * nw;
+  const dim3 grid((n_rows + tile_rows - 1) / tile_rows, n_experts, chunks);
+  auto kern = moe_lpb_kernel<T_IQ4_XS>;
+  if (lds > 64 * 1024) allow_lds((const void*)kern, 160 * 1024);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * nw), lds, stream, w, row_bytes, expert_stride, act,
+                     offsets, total_rows, y, ldy, n_rows, geo);
+  return 0;
 }
 
 int launch_gemv_f32(int type, const uint8_t* w, long long row_bytes, const float* x, int k,

@@ -206,6 +206,12 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
                    int n_experts, const Act& act, const int32_t* offsets, int total_rows,
                    int max_rows, YOut y, long long ldy, int n_rows, hipStream_t stream);
 
+// The same for IQ4_XS experts on float activations act.x (the decode body, four rows at a time):
+// each row equals that row multiplied alone by mxa_gemm's decode kernels. -1 otherwise.
+int launch_moe_lpb(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                   int n_experts, const Act& act, const int32_t* offsets, int total_rows,
+                   int max_rows, YOut y, long long ldy, int n_rows, hipStream_t stream);
+
 // out[t] (n_tokens x n_embd fp32) = the routing-weighted sum of token t's expert outputs:
 // down row rows[t top_k + k] (rows == nullptr: row t top_k + k) of slot k, times weights[t top_k
 // + k], slots in ascending ids[t top_k + k] (ties in slot order), bf16 != 0: each down value

@@ -458,14 +458,15 @@ class HipGemm:
             raise ValueError("out must be a contiguous float32 (n_rows, out_features) tensor")
         if n_rows == 0:
             return out
-        ws_bytes = q8k_bytes(n_rows, in_features)
-        if workspace is None:
-            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        if workspace is None and ggml_type != 23:  # IQ4_XS multiplies the float rows: none
+            workspace = torch.empty(q8k_bytes(n_rows, in_features), dtype=torch.uint8,
+                                    device=device)
         status = self._lib.mxa_gemm_moe(
             ggml_type, experts.data_ptr(), rb * out_features, n_experts,
             None if x32 is None else x32.data_ptr(), offsets.data_ptr(), n_rows,
             max(1, min(int(max_rows_per_expert), n_rows)), out.data_ptr(), out_features,
-            in_features, workspace.data_ptr(), workspace.numel(), _stream(device))
+            in_features, None if workspace is None else workspace.data_ptr(),
+            0 if workspace is None else workspace.numel(), _stream(device))
         self._check(status, "mxa_gemm_moe", ggml_type)
         self._calls += 1
         return out

@@ -71,7 +71,7 @@ class HipPackedMoEExperts(nn.Module):
         self.types = (int(gate_type), int(up_type), int(down_type))
         self._gemm = HipGemm.get()
         for t, k in ((gate_type, n_embd), (up_type, n_embd), (down_type, ffn_len)):
-            if not self._gemm.supports(int(t), k) or int(t) == 23:
+            if not self._gemm.supports(int(t), k):
                 raise ValueError(f"no grouped HIP projection for GGUF type {int(t)}")
         for name, w in (("gate", gate), ("up", up), ("down", down)):
             if w.dim() != 3 or w.shape[0] != self.num_experts or (w.shape[1] * w.shape[2]) % 4:
@@ -79,7 +79,8 @@ class HipPackedMoEExperts(nn.Module):
                                  "expert's bytes a multiple of 4")
         # the one-token pairs launch takes K / 256 in {4, 8, 16, 32, 56, 64} and 16-byte aligned
         # rows; other shapes go straight to the grouped launch
-        self._pairs = all(k // 256 in (4, 8, 16, 32, 56, 64) and
+        # (K-quant and Q8_0 experts; IQ4_XS experts take the grouped launch)
+        self._pairs = all(int(t) != 23 and k // 256 in (4, 8, 16, 32, 56, 64) and
                           self._gemm.row_bytes(int(t), k) % 16 == 0
                           for t, k in ((gate_type, n_embd), (up_type, n_embd), (down_type, ffn_len)))
         self.register_buffer("gate_packed", gate, persistent=False)

@@ -19,6 +19,7 @@ from matricxon_amd.device_packed import DevicePackedLinear
 from matricxon_amd.gemm import q8k_bytes
 from matricxon_amd.moe import HipPackedMoEExperts, route_pairs
 from oracle import dequant as D
+from tests.test_gpu_kernels import assert_within_tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -209,10 +210,59 @@ def test_module_repeated_expert_in_a_tokens_routing(dtype) -> None:
         f"max |diff| {(got.float() - want.float()).abs().max().item()}"
 
 
-def test_module_rejects_types_without_grouped_launch() -> None:
-    z = torch.zeros((2, 256, 136), dtype=torch.uint8, device="cuda")
-    with pytest.raises(ValueError):
-        HipPackedMoEExperts(z, z, z, D.IQ4_XS, D.IQ4_XS, D.IQ4_XS, 256, 256, F.silu)
+def test_module_rejects_types_without_a_kernel() -> None:
+    z = torch.zeros((2, 256, 144), dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):  # Q5_K (13): no HIP kernel
+        HipPackedMoEExperts(z, z, z, 13, 13, 13, 256, 256, F.silu)
+
+
+@pytest.mark.parametrize("n,k", [(512, 1024), (300, 2048)])
+@pytest.mark.parametrize("ci", range(len(COUNTS)))
+def test_grouped_iq4_xs_rows_equal_single_rows(gpu, n, k, ci) -> None:
+    """IQ4_XS experts in the grouped launch (float activations): every row equals mxa_gemm of
+    that row alone bit for bit, and an expert's rows equal mxa_gemm of them together while the
+    expert has up to 16 (from 17 rows mxa_gemm takes the matrix cores: within tolerance)."""
+    counts = COUNTS[ci]
+    n_experts, n_rows = len(counts), sum(counts)
+    w = expert_weights(D.IQ4_XS, n_experts, n, k, seed=n + k + ci)
+    x = S.activations(n_rows, k, seed=ci + 11)
+    off = offsets_of(counts)
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    got = gpu.matmul_moe(D.IQ4_XS, wd, xd, torch.from_numpy(off).cuda(), max(counts), n, k)
+    got = got.cpu().numpy()
+    for e in range(n_experts):
+        for r in range(off[e], off[e + 1]):
+            alone = gpu.matmul(D.IQ4_XS, wd[e], xd[r:r + 1], n, k).cpu().numpy()
+            assert_bit_exact(got[r:r + 1], alone, f"expert {e} row {r}")
+        if counts[e]:
+            together = gpu.matmul(D.IQ4_XS, wd[e], xd[off[e]:off[e + 1]], n, k).cpu().numpy()
+            if counts[e] <= 16:
+                assert_bit_exact(got[off[e]:off[e + 1]], together, f"expert {e}")
+            else:
+                assert_within_tolerance(got[off[e]:off[e + 1]], together)
+
+
+# up to 16 tokens an expert has at most 16 rows (top-k ids are distinct): bit for bit, also in
+# bfloat16; 24 float32 tokens may give an expert 17+ rows
+@pytest.mark.parametrize("n_tokens,dtype", [(1, torch.bfloat16), (10, torch.bfloat16),
+                                            (6, torch.float32), (24, torch.float32)])
+def test_module_iq4_xs_experts_match_reference_loop(n_tokens, dtype) -> None:
+    """An IQ4_XS expert set (gate/up IQ4_XS, down Q4_K) in the grouped launch, with no host sync:
+    bit for bit the reference's loop while every expert has up to 16 rows, within tolerance of it
+    otherwise (an expert with 17+ rows in the loop runs mxa_gemm's matrix-core prefill)."""
+    types = (D.IQ4_XS, D.IQ4_XS, D.Q4_K)
+    mod, per_expert = build_experts(types, 4, 1024, 512, dtype, seed=41 + n_tokens)
+    assert not mod._pairs
+    x = torch.from_numpy(S.activations(n_tokens, 1024, seed=42)).cuda().to(dtype)
+    tw, tidx = routing(n_tokens, 4, 2, seed=43)
+    got = mod(x, tw, tidx)
+    want = reference_forward(x, tw, tidx, per_expert, F.silu)
+    assert got.dtype == want.dtype == dtype
+    rows_per_expert = torch.bincount(tidx.reshape(-1).cpu(), minlength=4)
+    if int(rows_per_expert.max()) <= 16:
+        assert torch.equal(got.float().view(torch.int32), want.float().view(torch.int32))
+    else:
+        assert_within_tolerance(got.float().cpu().numpy(), want.float().cpu().numpy())
 
 
 PAIR_CASES = [
