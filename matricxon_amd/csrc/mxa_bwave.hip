@@ -1,0 +1,320 @@
+// Batched decode (up to 16 activation rows, rows of up to 16 blocks) on the matrix cores, with every
+// wave streaming and computing its own units: no copy waves, no wave ever waits for another.
+//
+// Work split. One workgroup per CU owns R consecutive weight rows (R = ceil(N / CUs)), T =
+// ceil(R / 16) tiles of 16 rows. Its waves split the blocks of a row: wave w owns blocks w C ..
+// w C + C - 1 of every row and keeps their Q8_K activations (the MFMA A operands of all 16
+// activation rows) in registers. Its unit of a tile is those C blocks of the tile's 16 rows: 16
+// pieces of C * block bytes, one per row, which the wave gathers itself with 1 KB
+// global_load_lds_dwordx4 copies (lane -> one 16-byte chunk of one row's piece; a row's piece is
+// one contiguous run of the row) into its own LDS slot for that tile. Every slot of every tile is
+// resident (nothing is reused), so no wave waits for LDS space.
+//
+// Stream. A wave keeps D tiles of its copies in flight: it requests tiles 0 .. D - 1, and tile
+// t + D as soon as tile t has landed (its own vmcnt: copies complete in issue order). The CU's
+// queue thus holds D tiles of every wave, and a wave starts on a tile the moment its own pieces
+// of it have landed, not the whole tile.
+//
+// Compute. For each tile, the wave builds the B operands of its blocks from its slot with the
+// tile builders of mxa_tiles.hpp (the arithmetic of the other batched kernels) and writes the
+// block values over the slot's bytes. After its last tile it meets the others at one barrier, and
+// the workgroup folds every output (weight row, activation row) over blocks 0..nb-1 in order with
+// the oracle's fused steps (app/native/src/mx_dot_k_ssse3.c:115-154, 200-206; mx_dot_q8_0.c:8-18),
+// so results equal the other decode kernels and the oracle bit for bit. No output is stored before
+// that barrier: a store counts on the same vmcnt as the copies, and a wave with a store pending
+// would wait for later tiles' copies at its next copy wait. (Folding each tile after a barrier of
+// its own, its outputs parked in LDS: 12.4 vs 12.1 us at Q4_K 14336 x 4096, M = 16.)
+#include "mxa_kernels.hpp"
+#include "mxa_tiles.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mxa {
+namespace {
+
+template <int TYPE>
+constexpr int kBwBlockBytes = TYPE == T_Q4_K ? 144 : TYPE == T_Q6_K ? 210 : 272;
+constexpr int kBwMaxTiles = 8;
+constexpr int kBwMaxCopies = 8;  // 1 KB copies of one wave's unit of a tile
+constexpr int kBwLds = 160 * 1024;
+
+typedef __attribute__((address_space(3))) int lds_int;
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+// A wave's activation operands travel through LDS: C blocks of 16 activation rows, each row's 256
+// q8 bytes as 16 pieces of 16 bytes (piece p of row r at slot (p + r) mod 16: the 16 rows of one
+// MFMA operand read fall in different banks), then (Q4_K, Q6_K) the rows' 32 bytes of bsums. They
+// are gathered with 1 KB copies of whole 256-byte row runs (16 cache lines a copy; the MFMA-shaped
+// register loads touch 64 lines an instruction and read each line four times) into the wave's
+// slots of its last two tiles, requested only later, or into an area of their own.
+template <int TYPE>
+__host__ __device__ constexpr int a_stage_bytes(int C) {
+  return C * 16 * QK + (TYPE != T_Q8_0 ? C * 16 * 32 : 0);
+}
+
+// The staging copies of blocks b0 .. b0 + C - 1 (clamped to the row's blocks): copy 4 c + i moves
+// rows 4 i .. 4 i + 3 of block c; copy 4 C the bsums of both blocks (lane -> block, row, half).
+template <int TYPE, int C>
+__device__ __forceinline__ int a_stage(const Act& act, int M, int b0, int lane, uint32_t dst) {
+  const int nb = act.nb;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int b = min(b0 + c, nb - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * i + (lane >> 4), s = lane & 15, p = (s - r) & 15;
+      const int8_t* src = act.q + (size_t)min(r, M - 1) * act.k + (size_t)b * QK + 16 * p;
+      copy16_to_lds(src, dst + (uint32_t)(c * 16 * QK + 1024 * i));
+    }
+  }
+  if constexpr (TYPE == T_Q8_0) {
+    return 4 * C;
+  } else {
+    if (lane < 32 * C) {
+      const int c = lane >> 5, r = (lane & 31) >> 1, h = lane & 1;
+      const int b = min(b0 + c, nb - 1);
+      copy16_to_lds((const uint8_t*)(act.bsums + ((size_t)min(r, M - 1) * nb + b) * 16) + 16 * h,
+                    dst + (uint32_t)(C * 16 * QK));
+    }
+    return 4 * C + 1;
+  }
+}
+
+// The MFMA A operands of block c from the staging area (lane: activation row ln, k-group g).
+template <int TYPE>
+__device__ __forceinline__ typename TileOf<TYPE>::T::F a_read(const uint8_t* ast, int C, int c,
+                                                              int ln, int g) {
+  typename TileOf<TYPE>::T::F f;
+  const uint8_t* row = ast + c * 16 * QK + ln * QK;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int p = TYPE == T_Q6_K ? 8 * (g >> 1) + (g & 1) + 2 * t : 4 * g + t;
+    f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(row + 16 * ((p + ln) & 15)));
+  }
+  if constexpr (TYPE != T_Q8_0) {
+    const uint2 v = *(const uint2*)(ast + C * 16 * QK + c * 512 + 32 * ln + 8 * g);
+    f.bs = f16x4{(_Float16)(float)(int16_t)(v.x & 0xFFFFu), (_Float16)(float)(int16_t)(v.x >> 16),
+                 (_Float16)(float)(int16_t)(v.y & 0xFFFFu), (_Float16)(float)(int16_t)(v.y >> 16)};
+  }
+  return f;
+}
+
+struct BwGeo {
+  int R;     // rows per workgroup
+  int rs;    // 16-byte chunks per row piece in a slot (odd)
+  int D;     // tiles of copies in flight per wave
+  int ncw;   // waves: ceil(nb / C)
+};
+
+// pack = R | rs << 12 | D << 20 | ncw << 24 | staging in the last two tiles' slots << 29;
+// packm = M | nb << 8
+template <int TYPE, int C>
+__global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_t* __restrict__ w, uint32_t pack,
+                                                        uint32_t packm, int N, int row_bytes,
+                                                        const int8_t* q, const int16_t* bsums,
+                                                        const float* d, YOut y, int ldy) {
+  using Tile = typename TileOf<TYPE>::T;
+  using F = typename Tile::F;
+  constexpr int TB = kBwBlockBytes<TYPE>;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int R = pack & 0xFFF, rs = (pack >> 12) & 0xFF, D = (pack >> 20) & 0xF;
+  const int ncw = (pack >> 24) & 0x1F;
+  const bool stage_in_slots = ((pack >> 29) & 1) != 0;
+  const int M = packm & 0x1F, nb = (packm >> 8) & 0xFF;
+  Act act;
+  act.q = q, act.d = d, act.bsums = bsums, act.x = nullptr;
+  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr, act.xbf16 = 0;
+
+  const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r0 = (int)blockIdx.x * R;
+  const int rows = min(R, N - r0);  // >= 1: the grid is ceil(N / R)
+  const int T = (rows + 15) >> 4;
+  const int slot_bytes = 16 * rs * 16;
+  constexpr int kStage = a_stage_bytes<TYPE>(C);
+  auto slot = [&](int wv, int t) { return smem + (wv * T + t) * slot_bytes; };
+  // the wave's staging area: its slots of tiles T - 2, T - 1 (requested after the operands are
+  // read), or an area of its own after all slots
+  uint8_t* ast = stage_in_slots ? slot(wave, T - 2) : smem + ncw * T * slot_bytes + wave * kStage;
+
+  // this wave's blocks, and its piece of a row: chunks [c_lo, c_hi) of the row (16-byte aligned
+  // chunks covering bytes b0 TB .. (b0 + cb) TB; rows are 16-byte multiples, so they stay inside)
+  const int b0 = wave * C, cb = min(C, nb - b0);
+  const int c_lo = (b0 * TB) >> 4, c_hi = ((b0 + cb) * TB + 15) >> 4;
+  const int nch = c_hi - c_lo;
+  const int skew = b0 * TB - 16 * c_lo;  // byte of block b0 in the row piece
+  const int ncp = (16 * rs + 63) >> 6;   // copies per unit
+
+  // 1. the A operands into the staging area, and the activation scales of the lane's fold row
+  //    m = lane % 16 into registers (four 16-byte loads, nb % 4 == 0), issued before any weight
+  //    copy so that they land first. The scale loads are inline assembly, so the compiler's wait
+  //    insertion never waits for them (it would wait for every copy issued after them); no
+  //    branch or copy of their registers comes before the wave's own wait.
+  const int am = min(ln, M - 1);
+  const int n_stage = a_stage<TYPE, C>(act, M, b0, lane, lds_addr(ast));
+  f32x4 xq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float* p = d + (size_t)am * nb + min(4 * i, nb - 4);
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(xq[i]) : "v"(p) : "memory");
+  }
+  (void)n_stage;
+
+  // 2. the copies: lane chunk e = 64 i + lane of the unit is chunk e % rs of row e / rs
+  uint32_t off[kBwMaxCopies];
+  int crow[kBwMaxCopies];
+#pragma unroll
+  for (int i = 0; i < kBwMaxCopies; ++i) {
+    const int e = 64 * i + lane, j = e / rs, c = e - j * rs;
+    crow[i] = c < nch ? j : 16;  // 16: not copied (padding chunk or past the unit)
+    off[i] = (uint32_t)(j * row_bytes + 16 * (c_lo + c));
+  }
+  // copies issued for tile t (an instruction none of whose lanes copies is not issued)
+  auto issued = [&](int t) {
+    const int live = min(16, rows - 16 * t);
+    return min(ncp, ((live - 1) * rs + nch + 63) >> 6);
+  };
+  auto issue = [&](int t) {
+    const uint8_t* base = w + (size_t)(r0 + 16 * t) * row_bytes;
+    const int live = min(16, rows - 16 * t);
+    const uint32_t dst = lds_addr(slot(wave, t));
+#pragma unroll
+    for (int i = 0; i < kBwMaxCopies; ++i)
+      if (i < ncp && crow[i] < live) copy16_to_lds_s_nt(base, off[i], dst + 1024u * (uint32_t)i);
+  };
+
+  int in_flight = 0;  // copies issued after the A loads
+  for (int t = 0; t < min(D, T); ++t) {
+    issue(t);
+    in_flight += issued(t);
+  }
+  wait_vmcnt(min(in_flight, kMaxCopies));  // the A operands and scales have landed
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(xq[i]));
+  float xd[16];
+#pragma unroll
+  for (int b = 0; b < 16; ++b) xd[b] = xq[b >> 2][b & 3];
+  F f[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) f[c] = a_read<TYPE>(ast, C, c, ln, g);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staging area is read before tiles land in it
+
+  for (int t = 0; t < T; ++t) {
+    // tile t has landed once only the later tiles' copies are outstanding
+    int later = 0;
+    for (int u = t + 1; u < min(t + D, T); ++u) later += issued(u);
+    wait_vmcnt(later);
+    if (t + D < T) issue(t + D);
+    const int live = min(16, rows - 16 * t);
+    uint8_t* sl = slot(wave, t);
+    const int jr = min(ln, live - 1);  // lanes past the rows compute the last row, never folded
+    float v[C][4], dv[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (c < cb) {
+        const typename Tile::P pp =
+            Tile::prep(Tile::load_lds(sl, jr * rs * 16 + skew + c * TB, g), g);
+        Tile::value(pp, f[c], g, [&](int e, float val, float dd) {
+          v[c][e] = val;
+          dv[c] = dd;
+        });
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot's bytes are read
+    // block values over the slot: [c][row][m], then (Q6_K) the blocks' d [c][row]
+    float* vals = (float*)sl;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (c < cb) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vals[(c * 16 + ln) * 16 + 4 * g + e] = v[c][e];
+        if (g == 0) vals[C * 256 + c * 16 + ln] = dv[c];
+      }
+    }
+  }
+  // 3. every wave has written its block values of every tile: the workgroup folds all outputs
+  //    (tile t, weight row j, activation row m), m the thread's own row (its scales in registers)
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  for (int o = tid; o < T * 256; o += 64 * ncw) {
+    const int t = o >> 8, j = (o >> 4) & 15, m = o & 15;
+    if (j < rows - 16 * t && m < M) {
+      float vv[16], dd[16];
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
+        if (b < nb) {
+          const int wv = b / C, cc = b - wv * C;
+          const float* src = (const float*)slot(wv, t);
+          vv[b] = src[(cc * 16 + j) * 16 + m];
+          dd[b] = src[C * 256 + cc * 16 + j];
+        }
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 16; ++b)
+        if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
+      y.put((size_t)m * ldy + r0 + 16 * t + j, acc);
+    }
+  }
+}
+
+template <int TYPE, int C>
+int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
+              int N, int depth, hipStream_t stream) {
+  constexpr int TB = kBwBlockBytes<TYPE>;
+  const int nb = act.nb;
+  const int ncu = cu_count();
+  const int R = (int)((N + (long long)ncu - 1) / ncu);
+  const int T = (R + 15) / 16;
+  const int ncw = (nb + C - 1) / C;
+  // the widest row piece of any wave, in 16-byte chunks, made odd (bank spread of the 16 rows)
+  int nch = 0;
+  for (int wv = 0; wv < ncw; ++wv) {
+    const int b0 = wv * C, cb = min(C, nb - b0);
+    nch = max(nch, ((b0 + cb) * TB + 15) / 16 - (b0 * TB) / 16);
+  }
+  const int rs = nch | 1;
+  const int ncp = (16 * rs + 63) / 64;
+  const int slot_bytes = 16 * rs * 16;
+  const int D = max(1, min(depth, min(T, 15)));
+  // the operands' staging area: the last two tiles' slots when those are requested only after
+  // the operands are read (T - 2 >= D), else an area of its own
+  const bool in_slots = T - 2 >= D && 2 * slot_bytes >= a_stage_bytes<TYPE>(C);
+  const int lds = ncw * T * slot_bytes + (in_slots ? 0 : ncw * a_stage_bytes<TYPE>(C));
+  // values [C][16][16] and d [C][16] fit a slot; every slot resident; the scales of a row in four
+  // 16-byte loads
+  if (T > kBwMaxTiles || ncp > kBwMaxCopies || ncw > 16 || lds > kBwLds || nb % 4 != 0 ||
+      (C * 256 + C * 16) * 4 > slot_bytes || R > 0xFFF || rs > 0xFF || ldy > 0x7FFFFFFF ||
+      row_bytes > 0x7FFFFFFF)
+    return -1;
+  const uint32_t pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24 |
+                        (uint32_t)in_slots << 29;
+  const uint32_t packm = (uint32_t)M | (uint32_t)nb << 8;
+  allow_lds((const void*)bwave_kernel<TYPE, C>, kBwLds);
+  const int grid = (int)((N + (long long)R - 1) / R);
+  hipLaunchKernelGGL((bwave_kernel<TYPE, C>), dim3(grid), dim3(64 * ncw), lds, stream, w, pack,
+                     packm, N, (int)row_bytes, act.q, act.bsums, act.d, y, (int)ldy);
+  return 0;
+}
+
+}  // namespace
+
+int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
+                 long long ldy, int m_rows, int n_rows, hipStream_t stream) {
+  if (act.q == nullptr || m_rows < 1 || m_rows > 16 || n_rows < 1 || act.nb > 16) return -1;
+  if ((((uintptr_t)w | (uintptr_t)row_bytes) & 15) != 0) return -1;
+  // Two tiles of copies in flight (three measured no faster where the slots allow it); two
+  // blocks per wave, one for Q8_0 (its 272-byte groups: 16 waves, 7.1 vs 8.4 us at 4096 x 4096,
+  // M = 16; Q4_K 4096 x 4096 6.1 vs 5.7 us with one)
+  constexpr int kDepth = 2;
+  switch (type) {
+    case T_Q4_K: return launch_bw<T_Q4_K, 2>(w, row_bytes, act, y, ldy, m_rows, n_rows, kDepth, stream);
+    case T_Q6_K: return launch_bw<T_Q6_K, 2>(w, row_bytes, act, y, ldy, m_rows, n_rows, kDepth, stream);
+    case T_Q8_0: return launch_bw<T_Q8_0, 1>(w, row_bytes, act, y, ldy, m_rows, n_rows, kDepth, stream);
+    default: return -1;
+  }
+}
+
+}  // namespace mxa

@@ -157,11 +157,13 @@ struct YOut {
   __host__ __device__ YOut at(long long i) const {
     return YOut{v + (uintptr_t)(i * (is_bf16() ? 2 : 4))};
   }
+  // Global-memory stores (an address that went through an integer would otherwise become a flat
+  // store, which also counts on lgkmcnt: every later LDS wait would then wait for the store).
   __device__ __forceinline__ void put(long long i, float x) const {
     if (v & 1u)
-      ((uint16_t*)(v - 1))[i] = bf16_rne(x);
+      ((__attribute__((address_space(1))) uint16_t*)(v - 1))[i] = bf16_rne(x);
     else
-      ((float*)v)[i] = x;
+      ((__attribute__((address_space(1))) float*)v)[i] = x;
   }
 };
 

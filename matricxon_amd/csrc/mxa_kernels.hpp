@@ -227,6 +227,13 @@ int launch_moe_combine(const float* down, const int32_t* rows, const int32_t* id
 int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                    long long ldy, int m_rows, int n_rows, hipStream_t stream);
 
+// Batched decode (m_rows <= 16, rows of up to 16 blocks) in which every wave gathers, computes
+// and (the last of each tile) folds its own block columns (mxa_bwave.hip): Q4_K, Q6_K, Q8_0 on
+// Q8_K activations in the workspace, 16-byte aligned weight and rows. -1 when the workgroup's
+// slots do not fit LDS.
+int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
+                 long long ldy, int m_rows, int n_rows, hipStream_t stream);
+
 // Batched decode (m_rows <= 16, rows of up to 16 blocks) with the workgroup's whole weight share
 // resident in LDS, streamed in by copy waves while compute waves run the matrix cores
 // (mxa_bflow.hip): Q4_K, Q6_K, Q8_0 on Q8_K activations in the workspace, 16-byte aligned weight

@@ -366,6 +366,10 @@ int launch_mt_type(const uint8_t* w, long long row_bytes, const Act& act, YOut y
                    int M, int N, hipStream_t stream) {
   // M <= 16: the streaming kernel, else the block-split kernel unless the 64-row tiles alone give
   // >= 512 workgroups
+  // M <= 16: the per-wave streaming kernel where its slots fit LDS (measured on MI355X at M = 16,
+  // the same bits: Q4_K 4096 x 4096 5.7 vs 7.1 us, 1024 x 4096 5.4 vs 6.3, Q8_0 4096 x 4096 7.1 vs
+  // 8.4; Q4_K 14336 x 4096 12.1 vs 12.0-12.3), then the copy-wave kernels
+  if (M <= 16 && launch_bwave(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && launch_bflow(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && launch_bres(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
   if (M <= 16 && launch_bstream(TYPE, w, row_bytes, act, y, ldy, M, N, stream) == 0) return 0;
