@@ -4,11 +4,10 @@
 // Work split. One workgroup per CU owns R consecutive weight rows (R = ceil(N / CUs)), T =
 // ceil(R / 16) tiles of 16 rows. Its waves split the blocks of a row: wave w owns blocks w C ..
 // w C + C - 1 of every row and keeps their Q8_K activations (the MFMA A operands of all 16
-// activation rows) in registers. Its unit of a tile is those C blocks of the tile's 16 rows: 16
-// pieces of C * block bytes, one per row, which the wave gathers itself with 1 KB
-// global_load_lds_dwordx4 copies (lane -> one 16-byte chunk of one row's piece; a row's piece is
-// one contiguous run of the row) into its own LDS slot for that tile. Every slot of every tile is
-// resident (nothing is reused), so no wave waits for LDS space.
+// activation rows), staged through LDS with whole-row copies, in registers. Its unit of a tile is
+// those C blocks of the tile's 16 rows: 16 pieces of C * block bytes, one per row, which the wave
+// gathers itself with 1 KB global_load_lds_dwordx4 copies (lane -> one 16-byte chunk of one row's
+// piece; a row's piece is one contiguous run of the row) into its own LDS slot for that tile.
 //
 // Stream. A wave keeps D tiles of its copies in flight: it requests tiles 0 .. D - 1, and tile
 // t + D as soon as tile t has landed (its own vmcnt: copies complete in issue order). The CU's
@@ -16,14 +15,19 @@
 // of it have landed, not the whole tile.
 //
 // Compute. For each tile, the wave builds the B operands of its blocks from its slot with the
-// tile builders of mxa_tiles.hpp (the arithmetic of the other batched kernels) and writes the
-// block values over the slot's bytes. After its last tile it meets the others at one barrier, and
-// the workgroup folds every output (weight row, activation row) over blocks 0..nb-1 in order with
-// the oracle's fused steps (app/native/src/mx_dot_k_ssse3.c:115-154, 200-206; mx_dot_q8_0.c:8-18),
-// so results equal the other decode kernels and the oracle bit for bit. No output is stored before
-// that barrier: a store counts on the same vmcnt as the copies, and a wave with a store pending
-// would wait for later tiles' copies at its next copy wait. (Folding each tile after a barrier of
-// its own, its outputs parked in LDS: 12.4 vs 12.1 us at Q4_K 14336 x 4096, M = 16.)
+// tile builders of mxa_tiles.hpp (the arithmetic of the other batched kernels) and keeps the
+// block values. Every output (weight row, activation row) is then folded over blocks 0..nb-1 in
+// order with the oracle's fused steps (app/native/src/mx_dot_k_ssse3.c:115-154, 200-206;
+// mx_dot_q8_0.c:8-18), so results equal the other decode kernels and the oracle bit for bit.
+//
+// Two forms. Resident (up to 8 tiles whose slots all fit LDS): nothing is reused, so no wave ever
+// waits for another; block values go over the slot's own bytes, and after its last tile every
+// wave meets the others at one barrier and the workgroup folds all outputs. No output is stored
+// before that barrier: a store counts on the same vmcnt as the copies, and a wave with a store
+// pending would wait for later tiles' copies at its next copy wait. (Folding each tile after a
+// barrier of its own, its outputs parked in LDS: 12.4 vs 12.1 us at Q4_K 14336 x 4096, M = 16.)
+// Ring (more tiles, e.g. a vocabulary head): D + 1 slots per wave cycle, and each tile's values
+// go to a two-entry value ring folded after a per-tile barrier (below).
 #include "mxa_kernels.hpp"
 #include "mxa_tiles.hpp"
 
@@ -106,9 +110,19 @@ struct BwGeo {
   int ncw;   // waves: ceil(nb / C)
 };
 
+// Values of one tile in the RING form: [block][row][m] floats, then the blocks' d [block][row].
+constexpr int kBwValBytes = (16 * 256 + 16 * 16) * 4;
+
 // pack = R | rs << 12 | D << 20 | ncw << 24 | staging in the last two tiles' slots << 29;
-// packm = M | nb << 8
-template <int TYPE, int C>
+// packm = M | nb << 8.
+// RING: more tiles than stay resident. A wave keeps S = D + 1 slots and requests tile t + D into
+// the slot of tile t - 1, which it has finished reading itself (no other wave reads a slot). The
+// block values go to a two-entry value ring, the waves meet at a barrier after every tile and the
+// first 256 threads fold that tile's outputs and store them; the barrier of tile t + 1 also keeps
+// any wave from writing tile t + 2's values before tile t's fold has read the entry. The operands'
+// staging area is the region from the slots of index D through the value ring (first used after
+// a barrier that follows every wave's reads of its operands).
+template <int TYPE, int C, bool RING>
 __global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_t* __restrict__ w, uint32_t pack,
                                                         uint32_t packm, int N, int row_bytes,
                                                         const int8_t* q, const int16_t* bsums,
@@ -133,10 +147,16 @@ __global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_
   const int T = (rows + 15) >> 4;
   const int slot_bytes = 16 * rs * 16;
   constexpr int kStage = a_stage_bytes<TYPE>(C);
-  auto slot = [&](int wv, int t) { return smem + (wv * T + t) * slot_bytes; };
-  // the wave's staging area: its slots of tiles T - 2, T - 1 (requested after the operands are
-  // read), or an area of its own after all slots
-  uint8_t* ast = stage_in_slots ? slot(wave, T - 2) : smem + ncw * T * slot_bytes + wave * kStage;
+  const int S = D + 1;  // RING: slots per wave
+  // resident: tile t of wave wv; RING: slot t mod S of every wave, slot index major
+  auto slot = [&](int wv, int t) {
+    return RING ? smem + ((t % S) * ncw + wv) * slot_bytes : smem + (wv * T + t) * slot_bytes;
+  };
+  uint8_t* vring = smem + S * ncw * slot_bytes;  // RING: two entries of kBwValBytes
+  // the wave's staging area: resident, its slots of tiles T - 2, T - 1 (requested after the
+  // operands are read) or an area of its own after all slots; RING, from slot index D on
+  uint8_t* ast = RING ? smem + D * ncw * slot_bytes + wave * kStage
+               : stage_in_slots ? slot(wave, T - 2) : smem + ncw * T * slot_bytes + wave * kStage;
 
   // this wave's blocks, and its piece of a row: chunks [c_lo, c_hi) of the row (16-byte aligned
   // chunks covering bytes b0 TB .. (b0 + cb) TB; rows are 16-byte multiples, so they stay inside)
@@ -199,13 +219,30 @@ __global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_
 #pragma unroll
   for (int c = 0; c < C; ++c) f[c] = a_read<TYPE>(ast, C, c, ln, g);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staging area is read before tiles land in it
+  // RING: a wave's staging area spans other waves' slots of index D and the value ring, so every
+  // wave has read its operands before any wave requests tile D or writes values
+  if constexpr (RING) {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
 
+  // RING: the output a fold thread computed for the previous tile, stored only after the next
+  // tile's wait and request, so that its store is not pending at that wait (with D = 1 the wait
+  // is for every outstanding operation)
+  float pend = 0.0f;
+  size_t pend_at = 0;
+  bool pend_ok = false;
   for (int t = 0; t < T; ++t) {
-    // tile t has landed once only the later tiles' copies are outstanding
+    // tile t has landed once only the later tiles' copies are outstanding (a store of an earlier
+    // fold issued since can only make this wait longer, never shorter: loads complete in order)
     int later = 0;
     for (int u = t + 1; u < min(t + D, T); ++u) later += issued(u);
     wait_vmcnt(later);
     if (t + D < T) issue(t + D);
+    if constexpr (RING) {
+      if (pend_ok) y.put(pend_at, pend);
+      pend_ok = false;
+    }
     const int live = min(16, rows - 16 * t);
     uint8_t* sl = slot(wave, t);
     const int jr = min(ln, live - 1);  // lanes past the rows compute the last row, never folded
@@ -215,23 +252,63 @@ __global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_
       if (c < cb) {
         const typename Tile::P pp =
             Tile::prep(Tile::load_lds(sl, jr * rs * 16 + skew + c * TB, g), g);
-        Tile::value(pp, f[c], g, [&](int e, float val, float dd) {
+        Tile::value_wide(pp, f[c], g, [&](int e, float val, float dd) {
           v[c][e] = val;
           dv[c] = dd;
         });
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot's bytes are read
-    // block values over the slot: [c][row][m], then (Q6_K) the blocks' d [c][row]
-    float* vals = (float*)sl;
+    if constexpr (RING) {
+      // block values into the value ring: [block][row][m], then d [block][row]
+      float* vals = (float*)(vring + (t & 1) * kBwValBytes);
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      if (c < cb) {
+      for (int c = 0; c < C; ++c) {
+        if (c < cb) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) vals[(c * 16 + ln) * 16 + 4 * g + e] = v[c][e];
-        if (g == 0) vals[C * 256 + c * 16 + ln] = dv[c];
+          for (int e = 0; e < 4; ++e) vals[((b0 + c) * 16 + ln) * 16 + 4 * g + e] = v[c][e];
+          if (g == 0) vals[16 * 256 + (b0 + c) * 16 + ln] = dv[c];
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (tid < 256) {  // fold tile t: output (row j, activation row m = the thread's own)
+        const int j = tid >> 4, m = tid & 15;
+        if (j < live && m < M) {
+          float vv[16], dd[16];
+#pragma unroll
+          for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
+            if (b < nb) {
+              vv[b] = vals[(b * 16 + j) * 16 + m];
+              dd[b] = vals[16 * 256 + b * 16 + j];
+            }
+          }
+          float acc = 0.0f;
+#pragma unroll
+          for (int b = 0; b < 16; ++b)
+            if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
+          pend = acc;
+          pend_at = (size_t)m * ldy + r0 + 16 * t + j;
+          pend_ok = true;
+        }
+      }
+    } else {
+      // block values over the slot: [c][row][m], then (Q6_K) the blocks' d [c][row]
+      float* vals = (float*)sl;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c < cb) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vals[(c * 16 + ln) * 16 + 4 * g + e] = v[c][e];
+          if (g == 0) vals[C * 256 + c * 16 + ln] = dv[c];
+        }
       }
     }
+  }
+  if constexpr (RING) {
+    if (pend_ok) y.put(pend_at, pend);
+    return;
   }
   // 3. every wave has written its block values of every tile: the workgroup folds all outputs
   //    (tile t, weight row j, activation row m), m the thread's own row (its scales in registers)
@@ -264,6 +341,7 @@ template <int TYPE, int C>
 int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
               int N, int depth, hipStream_t stream) {
   constexpr int TB = kBwBlockBytes<TYPE>;
+  constexpr int kStage = a_stage_bytes<TYPE>(C);
   const int nb = act.nb;
   const int ncu = cu_count();
   const int R = (int)((N + (long long)ncu - 1) / ncu);
@@ -278,24 +356,34 @@ int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, lon
   const int rs = nch | 1;
   const int ncp = (16 * rs + 63) / 64;
   const int slot_bytes = 16 * rs * 16;
-  const int D = max(1, min(depth, min(T, 15)));
-  // the operands' staging area: the last two tiles' slots when those are requested only after
-  // the operands are read (T - 2 >= D), else an area of its own
-  const bool in_slots = T - 2 >= D && 2 * slot_bytes >= a_stage_bytes<TYPE>(C);
-  const int lds = ncw * T * slot_bytes + (in_slots ? 0 : ncw * a_stage_bytes<TYPE>(C));
-  // values [C][16][16] and d [C][16] fit a slot; every slot resident; the scales of a row in four
-  // 16-byte loads
-  if (T > kBwMaxTiles || ncp > kBwMaxCopies || ncw > 16 || lds > kBwLds || nb % 4 != 0 ||
-      (C * 256 + C * 16) * 4 > slot_bytes || R > 0xFFF || rs > 0xFF || ldy > 0x7FFFFFFF ||
-      row_bytes > 0x7FFFFFFF)
+  // values [C][16][16] and d [C][16] fit a slot; the scales of a row in four 16-byte loads
+  if (ncp > kBwMaxCopies || ncw > 16 || nb % 4 != 0 || (C * 256 + C * 16) * 4 > slot_bytes ||
+      R > 0xFFF || rs > 0xFF || ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF)
     return -1;
+  // Resident: every tile's slot stays in LDS, the operands' staging area in the last two tiles'
+  // slots when those are requested only after the operands are read (T - 2 >= D), else an area
+  // of its own.
+  int D = max(1, min(depth, min(T, 15)));
+  const bool in_slots = T - 2 >= D && 2 * slot_bytes >= kStage;
+  const int lds_res = ncw * T * slot_bytes + (in_slots ? 0 : ncw * kStage);
+  bool ring = T > kBwMaxTiles || lds_res > kBwLds;
+  int lds = lds_res;
+  if (ring) {
+    // S = D + 1 slots per wave and the value ring; the staging area from slot index D on
+    for (D = min(depth, 15); D >= 1; --D) {
+      lds = (D + 1) * ncw * slot_bytes + 2 * kBwValBytes;
+      if (lds <= kBwLds && ncw * kStage <= ncw * slot_bytes + 2 * kBwValBytes) break;
+    }
+    if (D < 1) return -1;
+  }
   const uint32_t pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24 |
-                        (uint32_t)in_slots << 29;
+                        (uint32_t)(!ring && in_slots) << 29;
   const uint32_t packm = (uint32_t)M | (uint32_t)nb << 8;
-  allow_lds((const void*)bwave_kernel<TYPE, C>, kBwLds);
+  auto kern = ring ? bwave_kernel<TYPE, C, true> : bwave_kernel<TYPE, C, false>;
+  allow_lds((const void*)kern, kBwLds);
   const int grid = (int)((N + (long long)R - 1) / R);
-  hipLaunchKernelGGL((bwave_kernel<TYPE, C>), dim3(grid), dim3(64 * ncw), lds, stream, w, pack,
-                     packm, N, (int)row_bytes, act.q, act.bsums, act.d, y, (int)ldy);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * ncw), lds, stream, w, pack, packm, N,
+                     (int)row_bytes, act.q, act.bsums, act.d, y, (int)ldy);
   return 0;
 }
 

@@ -161,6 +161,11 @@ struct TileQ4 {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sink(i, fmaf(p.d, (float)sum[i], -(p.dmin * summ[i])), 0.0f);
   }
+  // value() already issues its MFMAs in two independent chains
+  template <class S>
+  __device__ static void value_wide(const P& p, const F& f, int g, S&& sink) {
+    value(p, f, g, static_cast<S&&>(sink));
+  }
 };
 
 // ---------------------------------------------------------------------------------------- Q6_K
@@ -285,6 +290,29 @@ struct TileQ6 {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sink(i, (float)(sumi[i] - 32 * (int)C[i]), p.d);
   }
+  // value() with the 16 sub-block MFMAs issued into results of their own before any is scaled, so
+  // that they overlap instead of each waiting out its predecessor's latency (64 more VGPRs live:
+  // for kernels with one activation tile); the same exact integer sum
+  template <class S>
+  __device__ static void value_wide(const P& p, const F& f, int g, S&& sink) {
+    i32x4 D[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int g2 = 0; g2 < 4; ++g2)
+        D[t][g2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[t], masked_b<false>(p.bu[t], g == g2),
+                                                          i32x4{0, 0, 0, 0}, 0, 0, 0);
+    const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bsc, f32x4{0, 0, 0, 0}, 0, 0, 0);
+    int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int g2 = 0; g2 < 4; ++g2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sumi[i] += __mul24(p.scv[t][g2], D[t][g2][i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sink(i, (float)(sumi[i] - 32 * (int)C[i]), p.d);
+  }
 };
 
 // ---------------------------------------------------------------------------------------- Q8_0
@@ -377,6 +405,28 @@ struct TileQ8 {
 #pragma unroll
       for (int i = 0; i < 4; ++i) bs[i] = fmaf(p.dk[k], (float)D[i], bs[i]);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sink(i, bs[i], 0.0f);
+  }
+  // value() with the eight blocks' MFMA pairs issued before any is scaled; the same fp32 steps
+  template <class S>
+  __device__ static void value_wide(const P& p, const F& f, int g, S&& sink) {
+    i32x4 D[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int g2 = k >> 1, h = k & 1;
+      const bool on = g == g2;
+      D[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        D[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[2 * h + tt], masked_b<false>(p.qb[2 * h + tt], on),
+                                                     D[k], 0, 0, 0);
+    }
+    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bs[i] = fmaf(p.dk[k], (float)D[k][i], bs[i]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) sink(i, bs[i], 0.0f);
   }

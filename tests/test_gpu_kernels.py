@@ -319,23 +319,24 @@ def test_one_row_decode_weight_off_16_byte_boundary(gpu, oracle, ggml_type) -> N
         assert np.array_equal(bits(y), bits(want))
 
 
-# Shapes for the batched-decode streaming kernel (5..16 tokens): rows per workgroup = max(16,
-# N / CUs), so N = 4100 leaves a one-row tile and a three-row last workgroup, N = 5000 a four-row
-# tile; K = 2304 gives an odd block count (the last wave owns one block), K = 768 three waves;
-# rows of more than 16 blocks stream in parts of 8 (K = 5120: a short last part; 14336: the down
-# projection's 56 blocks; 4352: Q6_K parts that start on 2-byte boundaries); Q6_K rows of 210 x
-# odd bytes start on 2-byte boundaries. Rows of up to 16 blocks whose workgroup share fits LDS run
-# resident (N = 14336: 56 rows, a half last tile; Q6_K / Q8_0 at N = 8192: two tiles; 3000 x
-# 2304: 12 rows per workgroup, odd block count; 14000 x 512: 55 rows of 2 blocks); more tiles than
-# LDS slots cycle through them (30000 x 4096: 8 tiles; 40000 x 2048: 10 tiles, Q4_K in 8 slots;
-# 50000 x 4096: 13 tiles); rows of more than 16 blocks stream, several tiles per workgroup with
+# Shapes for the batched-decode kernels (2..16 tokens). Rows of up to 16 blocks (a multiple of
+# four) go to the per-wave gather kernel: a workgroup owns ceil(N / CUs) rows in tiles of 16, its
+# waves two blocks each (one for Q8_0). N = 4100 leaves a one-row tile and a short last workgroup,
+# 5000 a four-row tile; the tiles stay resident in LDS up to 8 tiles that fit (14336 x 4096: 56
+# rows, a half last tile; Q6_K / Q8_0 at 8192: two tiles; 14000 x 512: one wave, 55 rows); more
+# tiles cycle through slots with a barrier-paced fold per tile (20000 x 4096: 5 tiles that do not
+# fit, Q6_K with one tile in flight; 30000 x 4096: 8 tiles, a six-row last tile; 40000 x 2048: 10
+# tiles of four waves; 50000 x 4096: 13 tiles). Other rows take the streaming kernel (rows per
+# workgroup max(16, N / CUs)): K = 2304 gives an odd block count, 768 three blocks; rows of more
+# than 16 blocks stream in parts of 8 (K = 5120: a short last part; 14336: the down projection's
+# 56 blocks; 4352: Q6_K parts that start on 2-byte boundaries), several tiles per workgroup with
 # their sums carried across parts (9000 x 5120: three tiles, the last of four rows; 40000 x 4608:
 # ten tiles of three parts, past the eight-tile output ring).
 BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
                 (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6),
                 (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10),
-                (30000, 4096, 9), (40000, 2048, 5), (50000, 4096, 16), (9000, 5120, 12),
-                (40000, 4608, 4)]
+                (20000, 4096, 3), (30000, 4096, 13), (40000, 2048, 5), (50000, 4096, 16),
+                (9000, 5120, 12), (40000, 4608, 4), (700, 4096, 2)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
