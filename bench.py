@@ -587,16 +587,16 @@ TRAFFIC_KERNELS = [
     ("gemv_wave_q4k_14336x4096_m1", r"gemv_wave_kernel<12, 16, true, ", algorithmic_bytes(1),
      "Q4_K 14336x4096, M=1, x quantized in the kernel (weight + fp32 x + fp32 y)",
      ("mxa_gemv_wave.hip",)),
-    ("bflow_q4k_14336x4096_m16", r"bflow_kernel<12, ",
+    ("bwave_q4k_14336x4096_m16", r"bwave_kernel<12, ",
      weight_bytes() + q8k_act_bytes(16, K) + 16 * N * 4,
      "Q4_K 14336x4096, M=16, on Q8_K activations (weight + Q8_K x + fp32 y)",
-     ("mxa_bflow.hip",)),
+     ("mxa_bwave.hip",)),
     ("q6k_head_128256x4096_m1", r"gemv_wave_kernel<14, 16, true, ", HEAD_N * 3360 + K * 4 + HEAD_N * 4,
      "Q6_K 128256x4096 (config 3 head), M=1 (weight + fp32 x + fp32 y)", ("mxa_gemv_wave.hip",)),
-    ("q6k_head_128256x4096_m16", r"(bflow|bres|bstream)_kernel<14, ",
+    ("q6k_head_128256x4096_m16", r"bwave_kernel<14, ",
      HEAD_N * 3360 + q8k_act_bytes(16, K) + 16 * HEAD_N * 4,
      "Q6_K 128256x4096 (config 3 head), M=16, on Q8_K activations",
-     ("mxa_bflow.hip", "mxa_bres.hip", "mxa_bstream.hip")),
+     ("mxa_bwave.hip",)),
 ]
 
 
@@ -872,7 +872,7 @@ def main() -> int:
         cpu = cpu_baseline(w_np, args.cpu_seconds)
 
     traffic1 = traffic_of("gemv_wave_q4k_14336x4096_m1")
-    traffic16 = traffic_of("bflow_q4k_14336x4096_m16")
+    traffic16 = traffic_of("bwave_q4k_14336x4096_m16")
 
     r1, r16 = results[1], results[16]
     line = {
@@ -914,7 +914,7 @@ def main() -> int:
             "kernel_us": round(r1["kernel_us"], 3),
             "bytes_per_launch": algorithmic_bytes(1),
             "m16_traffic": traffic16,
-            "m16_kernel": "bflow_kernel<Q4_K> (after quantize_q8k_kernel)",
+            "m16_kernel": "bwave_kernel<Q4_K> (after quantize_q8k_kernel)",
             # one launch that only reads the weight bytes (mxa_stream_read), timed the same way
             "read_floor_us": round(floor_us, 3),
             "read_floor_weight_gbs": round(weight_bytes() / floor_us / 1e3, 1),

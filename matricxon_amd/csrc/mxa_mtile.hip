@@ -328,8 +328,11 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
 // bound it knows without a sync; an expert with more rows loops). A workgroup whose expert has no
 // row in its chunks exits. The offsets come from the device, so they are clamped to
 // [0, total_rows): a bad table gives wrong rows, never an access outside the activations or y.
+// Two waves per SIMD asked of the compiler: the chunk loop left to itself took Q6_K to 272 VGPRs
+// (one workgroup per CU instead of two; the down projection ran 1.5x longer), with the bound it
+// fits 206 VGPRs with no scratch (Q8_0 227, Q4_K 202).
 template <int TYPE, int kDecRT>
-__global__ __launch_bounds__(256) void moe_dec_kernel(const uint8_t* w, long long row_bytes,
+__global__ __launch_bounds__(256, 2) void moe_dec_kernel(const uint8_t* w, long long row_bytes,
                                                       long long expert_stride, Act act,
                                                       const int32_t* __restrict__ offsets,
                                                       int total_rows, YOut y,
