@@ -123,6 +123,12 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
   static_assert(!kXF || (!FUSEQ && !ACTREG), "float activations are staged, not quantized");
   constexpr int kStage = wave_stage_bytes<TYPE, NB>(), kCopies = kStage / 1024;
   constexpr int R = 64 / NB, kRounds = NB / 4, kRowAct = wave_row_act(NB), K = NB * QK;
+  // bytes of a set in its last copy: the lanes past them are masked off, so a set whose bytes
+  // end inside a copy (Q6_K 4 x 3360 = 13440: 896 bytes over) does not read the next set's rows,
+  // which that set's own copies read again (lane 0 always copies: the instruction count that the
+  // waits rely on is unchanged)
+  constexpr int kTail = R * NB * Lpb<TYPE>::kBytes - (kCopies - 1) * 1024;
+  static_assert(kTail > 0 && kTail <= 1024, "the last copy holds part of the set");
   if constexpr (MAXM == 1) M = 1;  // constant LDS offsets for the one-row kernel
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -221,12 +227,14 @@ __device__ __forceinline__ void wave_rows(const uint8_t* __restrict__ w, const f
       const uint32_t lim = span > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)span;
 #pragma unroll
       for (int c = 0; c < kCopies; ++c)
-        copy16_to_lds_s_nt((const void*)src, min(lane16 + (uint32_t)(c * 1024), lim), lds_w + c * 1024);
+        if (c + 1 < kCopies || kTail == 1024 || lane16 < (uint32_t)kTail)
+          copy16_to_lds_s_nt((const void*)src, min(lane16 + (uint32_t)(c * 1024), lim), lds_w + c * 1024);
     } else {
 #pragma unroll
       for (int c = 0; c < kCopies; ++c)
-        copy16_to_lds_nt((const void*)min(src + (uintptr_t)c * 1024 + (uintptr_t)lane16, last),
-                         lds_w + c * 1024);
+        if (c + 1 < kCopies || kTail == 1024 || lane16 < (uint32_t)kTail)
+          copy16_to_lds_nt((const void*)min(src + (uintptr_t)c * 1024 + (uintptr_t)lane16, last),
+                           lds_w + c * 1024);
     }
   };
   if (has_rows && !late_wave) issue(set);
