@@ -432,6 +432,36 @@ def prefill_eager(gemm, dev, steps: int) -> None:
                 f"{2.0 * m * n * 4096 / us / 1e6:.1f} TFLOP/s-equivalent")
 
 
+def long_rows_eager(gemm, dev, steps: int) -> None:
+    """Eager launches of the long-row batched decode against the 16-block one, on Q8_K blocks
+    quantized once: the config 4 down projection (4096x14336, 56 blocks per row) in Q6_K and
+    Q4_K at M=16 (`bstream_kernel`), its one-row decode, and Q4_K 14336x4096 at M=16
+    (`bwave_kernel`); each call's mean time printed on stderr. The workload of the counter runs
+    that compare the two batched kernels' memory behaviour."""
+    import torch
+
+    from matricxon_amd import synthetic as S
+    from matricxon_amd.gemm import q8k_bytes
+
+    cases = ((14, "Q6_K 4096x14336", 4096, 14336, 16), (12, "Q4_K 4096x14336", 4096, 14336, 16),
+             (14, "Q6_K 4096x14336", 4096, 14336, 1), (12, "Q4_K 14336x4096", 14336, 4096, 16))
+    for t, name, n, k, m in cases:
+        ws = [torch.from_numpy(S.packed_weight(t, n, k, seed=80 + t + c)).to(dev) for c in range(8)]
+        x = torch.from_numpy(S.activations(m, k, seed=90 + m)).to(dev)
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        wsq = torch.empty(q8k_bytes(m, k), dtype=torch.uint8, device=dev)
+        gemm.quantize_into(x, wsq)
+        gemm.matmul_q8k(t, ws[0], wsq, None, y, m, n, k)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            gemm.matmul_q8k(t, ws[i % len(ws)], wsq, None, y, m, n, k)
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / steps * 1e6
+        log(f"long rows {name} M={m}: {us:.1f} us per call (eager, {steps} calls, 8 weight copies)")
+        del ws
+
+
 def bench_load(dev) -> None:
     """Host -> HBM upload of the config 3 packed weight (128256 x 4096 Q6_K, 431 MB) from
     pageable host memory already in the page cache: the reference's `upload_packed`
@@ -704,6 +734,10 @@ def main() -> int:
     ap.add_argument("--prefill-only", action="store_true",
                     help="only eager launches of the config 5 prefill calls (Q4_K 14336x4096 and "
                          "IQ4_XS 4096x4096 at M=512 and 2048; for rocprofv3 --pmc runs)")
+    ap.add_argument("--long-only", action="store_true",
+                    help="only eager launches of the config 4 down projection (56-block rows) at "
+                         "M=16 and M=1 beside Q4_K 14336x4096 at M=16, on Q8_K blocks (for "
+                         "rocprofv3 --pmc runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (scale for HBM counters)")
     ap.add_argument("--load", action="store_true",
@@ -744,6 +778,9 @@ def main() -> int:
 
     if args.prefill_only:
         prefill_eager(gemm, dev, args.steps)
+        return 0
+    if args.long_only:
+        long_rows_eager(gemm, dev, args.steps)
         return 0
     if args.moe:
         bench_moe(dev, min(args.steps, 50))

@@ -27,7 +27,9 @@
 // pending would wait for later tiles' copies at its next copy wait. (Folding each tile after a
 // barrier of its own, its outputs parked in LDS: 12.4 vs 12.1 us at Q4_K 14336 x 4096, M = 16.)
 // Ring (more tiles, e.g. a vocabulary head): D + 1 slots per wave cycle, and each tile's values
-// go to a two-entry value ring folded after a per-tile barrier (below).
+// go to a two-entry value ring folded after a per-tile barrier (below). Long rows (more than 16
+// blocks, `bwlong_kernel`): the unit is a tile x a part of eight blocks with its own staged
+// activations, the fold carried across a tile's parts (below).
 #include "mxa_kernels.hpp"
 #include "mxa_tiles.hpp"
 
@@ -387,12 +389,231 @@ int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, lon
   return 0;
 }
 
+// Long rows (more than 16 blocks, e.g. the FFN down projection's 56): the rows are cut into parts
+// of PB = ncw * C blocks and the stream's unit is (tile t, part p), tile-major. The A operands of
+// a part differ from the next part's, and at 16 activation rows a CU's share of them outgrows its
+// share of the weight (56 blocks: 229 KB of Q8_K against 188 KB of Q6_K), so every unit stages its
+// own: a wave's slot holds the part's A operands (the whole-row-run copies above), the 16 rows'
+// activation scales of its blocks (one 16-byte copy per row), and its weight pieces. A wave reads
+// its landed unit into registers and only then requests unit u + D into the same slot, so D slots
+// per wave keep D units in flight while one is computed. The waves put block values, block d and
+// activation
+// scales of a unit into a two-entry value ring; after a per-unit barrier the first 256 threads
+// fold that unit's blocks into their output's running sum, which carries from part to part of a
+// tile (blocks in order), and store it after the tile's last part, so the results equal the
+// oracle and the other decode kernels bit for bit. Every part starts on a 16-byte boundary of the
+// row (PB * block bytes a multiple of 16), so a wave's per-lane copy offsets serve every unit.
+template <int TYPE, int C>
+__global__ __launch_bounds__(512) void bwlong_kernel(const uint8_t* __restrict__ w, uint32_t pack,
+                                                     uint32_t packm, int N, int row_bytes,
+                                                     const int8_t* q, const int16_t* bsums,
+                                                     const float* d, YOut y, int ldy) {
+  using Tile = typename TileOf<TYPE>::T;
+  using F = typename Tile::F;
+  constexpr int TB = kBwBlockBytes<TYPE>;
+  constexpr int kStageA = a_stage_bytes<TYPE>(C);
+  constexpr int kStage = kStageA + 256;  // then the scales: row r's 16 bytes at 16 r
+  constexpr int kNA = 4 * C + (TYPE != T_Q8_0 ? 1 : 0) + 1;  // staging copies of a unit
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int R = pack & 0xFFF, rs = (pack >> 12) & 0xFF, D = (pack >> 20) & 0xF;
+  const int ncw = (pack >> 24) & 0x1F;
+  const int M = packm & 0x1F, nb = (packm >> 8) & 0xFF;
+  Act act;
+  act.q = q, act.d = d, act.bsums = bsums, act.x = nullptr;
+  act.k = nb * QK, act.nb = nb, act.xsplit = nullptr, act.xbf16 = 0;
+
+  const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r0 = (int)blockIdx.x * R;
+  const int rows = min(R, N - r0);  // >= 1: the grid is ceil(N / R)
+  const int T = (rows + 15) >> 4;
+  const int PB = ncw * C, P = (nb + PB - 1) / PB, U = T * P;
+  const int slot_bytes = kStage + 16 * rs * 16;
+  auto slot = [&](int u) { return smem + ((u % D) * ncw + wave) * slot_bytes; };
+  // value ring entry: values [PB][row][m], block d [PB][row], activation scales [PB][m]
+  const int val_bytes = PB * (256 + 16 + 16) * 4;
+  uint8_t* vring = smem + D * ncw * slot_bytes;
+
+  // this wave's blocks of a part: bw .. bw + C - 1 (relative); its row piece: chunks c_lo0 ..
+  const int bw = wave * C;
+  const int c_lo0 = (bw * TB) >> 4;
+  const int skew = bw * TB - 16 * c_lo0;
+  const int ncp = (16 * rs + 63) >> 6;
+  auto cb_of = [&](int p) { return min(C, nb - (p * PB + bw)); };  // <= 0: no block in part p
+  auto nch_of = [&](int p) {
+    const int cb = cb_of(p);
+    return cb <= 0 ? 0 : ((bw + cb) * TB + 15) / 16 - c_lo0;
+  };
+
+  // the copies: lane chunk e = 64 i + lane of the unit is chunk e % rs of row e / rs
+  uint32_t off[kBwMaxCopies];
+  int crow[kBwMaxCopies], cch[kBwMaxCopies];
+#pragma unroll
+  for (int i = 0; i < kBwMaxCopies; ++i) {
+    const int e = 64 * i + lane, j = e / rs, c = e - j * rs;
+    crow[i] = j;
+    cch[i] = c;
+    off[i] = (uint32_t)(j * row_bytes + 16 * (c_lo0 + c));
+  }
+  auto issued = [&](int u) {
+    const int t = u / P, p = u - t * P;
+    const int live = min(16, rows - 16 * t), nch = nch_of(p);
+    return nch == 0 ? 0 : kNA + min(ncp, ((live - 1) * rs + nch + 63) >> 6);
+  };
+  auto issue = [&](int u) {
+    const int t = u / P, p = u - t * P;
+    const int nch = nch_of(p);
+    if (nch == 0) return;
+    const int live = min(16, rows - 16 * t), b0 = p * PB + bw;
+    const uint32_t dst = lds_addr(slot(u));
+    a_stage<TYPE, C>(act, M, b0, lane, dst);
+    if (lane < 16)  // row lane's scales of blocks (b0 & ~3) .. + 3 (nb % 4 == 0: in the row)
+      copy16_to_lds(d + (size_t)min(lane, M - 1) * nb + (b0 & ~3), dst + kStageA);
+    const uint8_t* base = w + (size_t)(r0 + 16 * t) * row_bytes + (size_t)p * PB * TB;
+#pragma unroll
+    for (int i = 0; i < kBwMaxCopies; ++i)
+      if (i < ncp && crow[i] < live && cch[i] < nch)
+        copy16_to_lds_s_nt(base, off[i], dst + kStage + 1024u * (uint32_t)i);
+  };
+
+  for (int u = 0; u < min(D, U); ++u) issue(u);
+
+  float acc = 0.0f, pend = 0.0f;
+  size_t pend_at = 0;
+  bool pend_ok = false;
+  for (int u = 0; u < U; ++u) {
+    // unit u has landed once only the later units' copies are outstanding
+    int later = 0;
+    for (int v = u + 1; v < min(u + D, U); ++v) later += issued(v);
+    wait_vmcnt(later);
+    const int t = u / P, p = u - t * P;
+    const int live = min(16, rows - 16 * t), cb = cb_of(p), b0 = p * PB + bw;
+    // the unit's operands, scales and weight bytes into registers; then its slot takes unit u + D
+    F f[C];
+    float xs[C];
+    typename Tile::W wl[C];
+    if (cb > 0) {
+      const uint8_t* sl = slot(u);
+      const int jr = min(ln, live - 1);  // lanes past the rows compute the last row, never folded
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c < cb) {
+          f[c] = a_read<TYPE>(sl, C, c, ln, g);
+          xs[c] = *(const float*)(sl + kStageA + 16 * ln + 4 * ((b0 + c) & 3));
+          wl[c] = Tile::load_lds(sl + kStage, jr * rs * 16 + skew + c * TB, g);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot is read
+    // unit u + D into the slot just read: with one unit in flight the CU's copy queue is empty
+    // now, so the request goes ahead of this unit's compute; with more, only after it (the CU
+    // takes ~64 KB of copies in flight, and a request made while unit u + 1 is still landing
+    // stalls the wave at the copy instruction until that unit drains)
+    if (D == 1 && u + 1 < U) issue(u + 1);
+    if (pend_ok) y.put(pend_at, pend);  // the previous tile's output, stored after the wait
+    pend_ok = false;
+    float* vals = (float*)(vring + (u & 1) * val_bytes);
+    if (cb > 0) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c < cb) {
+          float v[4], dv = 0.0f;
+          const typename Tile::P pp = Tile::prep(wl[c], g);
+          Tile::value_wide(pp, f[c], g, [&](int e, float val, float dd) {
+            v[e] = val;
+            dv = dd;
+          });
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vals[((bw + c) * 16 + ln) * 16 + 4 * g + e] = v[e];
+          if (g == 0) {
+            vals[PB * 256 + (bw + c) * 16 + ln] = dv;
+            vals[PB * 272 + (bw + c) * 16 + ln] = xs[c];  // scale of activation row m = ln
+          }
+        }
+      }
+    }
+    if (D > 1 && u + D < U) issue(u + D);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): values written
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (tid < 256) {  // fold unit u into output (row j, activation row m = the thread's own)
+      const int j = tid >> 4, m = tid & 15;
+      const int nbp = min(PB, nb - p * PB);
+      if (p == 0) acc = 0.0f;
+      float vv[16], dd[16], xd[16];
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
+        if (b < nbp) {
+          vv[b] = vals[(b * 16 + j) * 16 + m];
+          dd[b] = vals[PB * 256 + b * 16 + j];
+          xd[b] = vals[PB * 272 + b * 16 + m];
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < 16; ++b)
+        if (b < nbp) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
+      if (p == P - 1 && j < live && m < M) {
+        pend = acc;
+        pend_at = (size_t)m * ldy + r0 + 16 * t + j;
+        pend_ok = true;
+      }
+    }
+  }
+  if (pend_ok) y.put(pend_at, pend);
+}
+
+template <int TYPE, int C>
+int launch_bwl(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
+               int N, int ncw, int depth, hipStream_t stream) {
+  constexpr int TB = kBwBlockBytes<TYPE>;
+  constexpr int kStage = a_stage_bytes<TYPE>(C) + 256;
+  const int nb = act.nb, PB = ncw * C;
+  const int ncu = cu_count();
+  const int R = (int)((N + (long long)ncu - 1) / ncu);
+  int nch = 0;  // the widest row piece of a wave within a part, in 16-byte chunks, made odd
+  for (int wv = 0; wv < ncw; ++wv) nch = max(nch, ((wv + 1) * C * TB + 15) / 16 - (wv * C * TB) / 16);
+  const int rs = nch | 1;
+  const int ncp = (16 * rs + 63) / 64;
+  const int slot_bytes = kStage + 16 * rs * 16;
+  const int val_bytes = PB * (256 + 16 + 16) * 4;
+  if (nb <= 16 || nb > 255 || nb % 4 != 0 || (PB * TB) % 16 != 0 || PB > 16 || ncp > kBwMaxCopies ||
+      R > 0xFFF || rs > 0xFF || ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF)
+    return -1;
+  int D = min(depth, 15), lds = 0;
+  for (; D >= 1; --D) {
+    lds = D * ncw * slot_bytes + 2 * val_bytes;
+    if (lds <= kBwLds) break;
+  }
+  if (D < 1) return -1;
+  const uint32_t pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24;
+  const uint32_t packm = (uint32_t)M | (uint32_t)nb << 8;
+  auto kern = bwlong_kernel<TYPE, C>;
+  allow_lds((const void*)kern, kBwLds);
+  const int grid = (int)((N + (long long)R - 1) / R);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * ncw), lds, stream, w, pack, packm, N,
+                     (int)row_bytes, act.q, act.bsums, act.d, y, (int)ldy);
+  return 0;
+}
+
 }  // namespace
 
 int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream) {
-  if (act.q == nullptr || m_rows < 1 || m_rows > 16 || n_rows < 1 || act.nb > 16) return -1;
+  if (act.q == nullptr || m_rows < 1 || m_rows > 16 || n_rows < 1) return -1;
   if ((((uintptr_t)w | (uintptr_t)row_bytes) & 15) != 0) return -1;
+  if (act.nb > 16) {
+    // long rows: parts of eight blocks, one per wave; one unit in flight (two measured slower,
+    // Q6_K 4096 x 14336 M = 16 25.4 vs 23.4 us: each unit's compute, ~1.6-2.4 us per block and
+    // wave at two waves per SIMD, is the limit, and the deeper queue stalls its issue)
+    constexpr int kLongDepth = 1;
+    switch (type) {
+      case T_Q4_K: return launch_bwl<T_Q4_K, 1>(w, row_bytes, act, y, ldy, m_rows, n_rows, 8, kLongDepth, stream);
+      case T_Q6_K: return launch_bwl<T_Q6_K, 1>(w, row_bytes, act, y, ldy, m_rows, n_rows, 8, kLongDepth, stream);
+      case T_Q8_0: return launch_bwl<T_Q8_0, 1>(w, row_bytes, act, y, ldy, m_rows, n_rows, 8, kLongDepth, stream);
+      default: return -1;
+    }
+  }
   // Two tiles of copies in flight (three measured no faster where the slots allow it); two
   // blocks per wave, one for Q8_0 (its 272-byte groups: 16 waves, 7.1 vs 8.4 us at 4096 x 4096,
   // M = 16; Q4_K 4096 x 4096 6.1 vs 5.7 us with one)

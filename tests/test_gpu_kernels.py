@@ -326,17 +326,20 @@ def test_one_row_decode_weight_off_16_byte_boundary(gpu, oracle, ggml_type) -> N
 # rows, a half last tile; Q6_K / Q8_0 at 8192: two tiles; 14000 x 512: one wave, 55 rows); more
 # tiles cycle through slots with a barrier-paced fold per tile (20000 x 4096: 5 tiles that do not
 # fit, Q6_K with one tile in flight; 30000 x 4096: 8 tiles, a six-row last tile; 40000 x 2048: 10
-# tiles of four waves; 50000 x 4096: 13 tiles). Other rows take the streaming kernel (rows per
-# workgroup max(16, N / CUs)): K = 2304 gives an odd block count, 768 three blocks; rows of more
-# than 16 blocks stream in parts of 8 (K = 5120: a short last part; 14336: the down projection's
-# 56 blocks; 4352: Q6_K parts that start on 2-byte boundaries), several tiles per workgroup with
-# their sums carried across parts (9000 x 5120: three tiles, the last of four rows; 40000 x 4608:
-# ten tiles of three parts, past the eight-tile output ring).
+# tiles of four waves; 50000 x 4096: 13 tiles). Longer rows whose block count is a multiple of
+# four take its long form: units of one tile x a part of eight blocks, each with its own staged
+# activations, the fold carried from part to part (K = 5120: 20 blocks, a four-block last part;
+# 8192: 32; 14336: the down projection's 56, at 1000 rows one tile per workgroup, at 5000 two, so
+# a tile's last part hands over to the next tile's first). Other rows take the streaming kernel
+# (rows per workgroup max(16, N / CUs)): K = 2304 gives an odd block count, 768 three blocks; 4352
+# and 4608 (17 and 18 blocks) stream in parts of 8, Q6_K parts starting on 2-byte boundaries, with
+# their sums carried across parts (40000 x 4608: ten tiles of three parts, past the eight-tile
+# output ring).
 BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5), (40, 768, 16),
                 (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6),
                 (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10),
                 (20000, 4096, 6), (30000, 4096, 13), (40000, 2048, 5), (50000, 4096, 16),
-                (9000, 5120, 12), (40000, 4608, 4)]
+                (9000, 5120, 12), (40000, 4608, 4), (300, 8192, 16), (5000, 14336, 5)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
