@@ -148,7 +148,8 @@ int gemm_multi_core(int n, const int* types, const void* const* ws, const int* o
     if (n_tokens <= fmax) {
       st = mxa::launch_decode_multi(seg, n, act, total, n_tokens, s);
     } else {
-      st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+      st = mxa::launch_bwave_multi(seg, n, act, total, n_tokens, s);
+      if (st != 0) st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
       if (st != 0) st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
     }
     if (st == 0) return check_launch();
@@ -214,7 +215,8 @@ int gemm_multi_q8k_core(int n, const int* types, const void* const* ws, const in
   if (n > 1 && n_tokens <= 16) {  // one launch for the group
     const int fmax = mxa::fused_max_rows();
     int st = n_tokens <= fmax ? mxa::launch_decode_multi(seg, n, act, total, n_tokens, s)
-                              : mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
+                              : mxa::launch_bwave_multi(seg, n, act, total, n_tokens, s);
+    if (st != 0 && n_tokens > fmax) st = mxa::launch_bres_multi(seg, n, act, total, n_tokens, s);
     if (st != 0 && n_tokens > fmax)
       st = mxa::launch_bstream_multi(seg, n, act, total, n_tokens, s);
     if (st == 0) return check_launch();

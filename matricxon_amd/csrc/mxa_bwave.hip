@@ -124,15 +124,16 @@ constexpr int kBwValBytes = (16 * 256 + 16 * 16) * 4;
 // any wave from writing tile t + 2's values before tile t's fold has read the entry. The operands'
 // staging area is the region from the slots of index D through the value ring (first used after
 // a barrier that follows every wave's reads of its operands).
+// The body of one workgroup: rows wg * R .. of the weight at w (bwave_kernel, and one weight of
+// a shared-input group in bwave_multi_kernel).
 template <int TYPE, int C, bool RING>
-__global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_t* __restrict__ w, uint32_t pack,
-                                                        uint32_t packm, int N, int row_bytes,
-                                                        const int8_t* q, const int16_t* bsums,
-                                                        const float* d, YOut y, int ldy) {
+__device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restrict__ w,
+                                           uint32_t pack, uint32_t packm, int N, int row_bytes,
+                                           const int8_t* q, const int16_t* bsums, const float* d,
+                                           YOut y, int ldy, int wg) {
   using Tile = typename TileOf<TYPE>::T;
   using F = typename Tile::F;
   constexpr int TB = kBwBlockBytes<TYPE>;
-  extern __shared__ __align__(16) uint8_t smem[];
 
   const int R = pack & 0xFFF, rs = (pack >> 12) & 0xFF, D = (pack >> 20) & 0xF;
   const int ncw = (pack >> 24) & 0x1F;
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_
 
   const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r0 = (int)blockIdx.x * R;
+  const int r0 = wg * R;
   const int rows = min(R, N - r0);  // >= 1: the grid is ceil(N / R)
   const int T = (rows + 15) >> 4;
   const int slot_bytes = 16 * rs * 16;
@@ -337,6 +338,75 @@ __global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_
       y.put((size_t)m * ldy + r0 + 16 * t + j, acc);
     }
   }
+}
+
+template <int TYPE, int C, bool RING>
+__global__ __launch_bounds__(C == 1 ? 1024 : 512) void bwave_kernel(const uint8_t* __restrict__ w, uint32_t pack,
+                                                        uint32_t packm, int N, int row_bytes,
+                                                        const int8_t* q, const int16_t* bsums,
+                                                        const float* d, YOut y, int ldy) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  bwave_rows<TYPE, C, RING>(smem, w, pack, packm, N, row_bytes, q, bsums, d, y, ldy, (int)blockIdx.x);
+}
+
+// Shared-input weights (q|k|v): up to four K-quant weights of the same input in one launch, each
+// in the resident form with workgroups in proportion to its bytes (its own rows per workgroup,
+// slot shape and depth in its pack word); a workgroup runs the body of its weight's type.
+constexpr int kBwMaxSegs = 4;
+struct BwSeg {
+  const uint8_t* w;
+  YOut y;  // the weight's first output column (row stride ldy)
+  uint32_t pack;
+  int n, row_bytes, type, wg0;
+};
+struct BwSegs {
+  BwSeg s[kBwMaxSegs];
+  int count;
+};
+
+__global__ __launch_bounds__(512) void bwave_multi_kernel(BwSegs segs, uint32_t packm,
+                                                          const int8_t* q, const int16_t* bsums,
+                                                          const float* d, int ldy) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int wg = blockIdx.x;
+  int i = 0;
+  while (i + 1 < segs.count && wg >= segs.s[i + 1].wg0) ++i;
+  const BwSeg& sg = segs.s[i];
+  if (sg.type == T_Q6_K)
+    bwave_rows<T_Q6_K, 2, false>(smem, sg.w, sg.pack, packm, sg.n, sg.row_bytes, q, bsums, d, sg.y,
+                                 ldy, wg - sg.wg0);
+  else
+    bwave_rows<T_Q4_K, 2, false>(smem, sg.w, sg.pack, packm, sg.n, sg.row_bytes, q, bsums, d, sg.y,
+                                 ldy, wg - sg.wg0);
+}
+
+// The resident geometry of R rows per workgroup of nb-block rows: the pack word and its LDS bytes;
+// false when the rows need the ring form or do not fit.
+template <int TYPE, int C>
+bool bw_resident(int nb, int R, int depth, uint32_t* pack, int* lds) {
+  constexpr int TB = kBwBlockBytes<TYPE>;
+  constexpr int kStage = a_stage_bytes<TYPE>(C);
+  const int T = (R + 15) / 16;
+  const int ncw = (nb + C - 1) / C;
+  int nch = 0;
+  for (int wv = 0; wv < ncw; ++wv) {
+    const int b0 = wv * C, cb = min(C, nb - b0);
+    nch = max(nch, ((b0 + cb) * TB + 15) / 16 - (b0 * TB) / 16);
+  }
+  const int rs = nch | 1;
+  const int ncp = (16 * rs + 63) / 64;
+  const int slot_bytes = 16 * rs * 16;
+  if (ncp > kBwMaxCopies || ncw > 16 || nb % 4 != 0 || (C * 256 + C * 16) * 4 > slot_bytes ||
+      R > 0xFFF || rs > 0xFF || T > kBwMaxTiles)
+    return false;
+  const int D = max(1, min(depth, min(T, 15)));
+  const bool in_slots = T - 2 >= D && 2 * slot_bytes >= kStage;
+  const int l = ncw * T * slot_bytes + (in_slots ? 0 : ncw * kStage);
+  if (l > kBwLds) return false;
+  *pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24 |
+          (uint32_t)in_slots << 29;
+  *lds = l;
+  return true;
 }
 
 template <int TYPE, int C>
@@ -597,6 +667,59 @@ int launch_bwl(const uint8_t* w, long long row_bytes, const Act& act, YOut y, lo
 }
 
 }  // namespace
+
+int launch_bwave_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
+                       hipStream_t stream) {
+  if (act.q == nullptr || m_rows < 1 || m_rows > 16 || count < 2 || count > kBwMaxSegs ||
+      act.nb > 16 || ldy > 0x7FFFFFFF)
+    return -1;
+  const int ncu = cu_count();
+  double total = 0.0;
+  for (int i = 0; i < count; ++i) {
+    if ((seg[i].type != T_Q4_K && seg[i].type != T_Q6_K) || seg[i].n < 1 ||
+        (((uintptr_t)seg[i].w | (uintptr_t)seg[i].row_bytes) & 15) != 0 || seg[i].row_bytes > 0x7FFFFFFF)
+      return -1;
+    total += (double)seg[i].n * (double)seg[i].row_bytes;
+  }
+  BwSegs segs;
+  segs.count = count;
+  int wg0 = 0, lds = 0;
+  constexpr int kDepth = 2;
+  // Workgroups in proportion to the bytes of each weight; a weight whose share of tiles does not
+  // fit LDS gets fewer tiles per workgroup (Q6_K 1024 x 4096 at 18 rows: two tiles and a separate
+  // staging area, 184 KB). A workgroup takes most of a CU's LDS, so the group must fit one round
+  // of the CUs: the shares shrink until it does, and a group that cannot (gate|up: seven tiles
+  // per CU) is left to the other kernels.
+  double budget = ncu;
+  for (int attempt = 0; attempt < 6; ++attempt) {
+    wg0 = 0, lds = 0;
+    for (int i = 0; i < count; ++i) {
+      const int share = max(1, (int)(budget * seg[i].n * seg[i].row_bytes / total));
+      int R = (seg[i].n + share - 1) / share;
+      uint32_t pack = 0;
+      int l = 0;
+      for (;;) {
+        const bool ok = seg[i].type == T_Q6_K ? bw_resident<T_Q6_K, 2>(act.nb, R, kDepth, &pack, &l)
+                                              : bw_resident<T_Q4_K, 2>(act.nb, R, kDepth, &pack, &l);
+        if (ok) break;
+        if (R <= 16) return -1;
+        R = 16 * ((R - 1) / 16);
+      }
+      segs.s[i] = BwSeg{seg[i].w, seg[i].y, pack, seg[i].n, (int)seg[i].row_bytes, seg[i].type, wg0};
+      lds = max(lds, l);
+      wg0 += (seg[i].n + R - 1) / R;
+    }
+    if (wg0 <= ncu) break;
+    budget *= (double)ncu / wg0;
+  }
+  if (wg0 > ncu) return -1;
+  const uint32_t packm = (uint32_t)m_rows | (uint32_t)act.nb << 8;
+  allow_lds((const void*)bwave_multi_kernel, kBwLds);
+  const int ncw = (act.nb + 1) / 2;
+  hipLaunchKernelGGL(bwave_multi_kernel, dim3(wg0), dim3(64 * ncw), lds, stream, segs, packm, act.q,
+                     act.bsums, act.d, (int)ldy);
+  return 0;
+}
 
 int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream) {

@@ -233,6 +233,11 @@ int launch_bstream(int type, const uint8_t* w, long long row_bytes, const Act& a
 // slots do not fit LDS.
 int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act, YOut y,
                  long long ldy, int m_rows, int n_rows, hipStream_t stream);
+// Shared-input K-quant weights (2..4, Q4_K / Q6_K, rows of up to 16 blocks, each resident) at
+// 1..16 activation rows on Q8_K blocks in one launch of the gather kernel; -1 when it does not
+// take the group.
+int launch_bwave_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
+                       hipStream_t stream);
 
 // Batched decode (m_rows <= 16, rows of up to 16 blocks) with the workgroup's whole weight share
 // resident in LDS, streamed in by copy waves while compute waves run the matrix cores

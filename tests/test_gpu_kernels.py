@@ -217,6 +217,8 @@ MULTI_CASES = [
     ([(D.Q4_K, 14336), (D.Q4_K, 14336)], 4096, 16),
     # q|k|v shape: segments of different types and tile counts
     ([(D.Q4_K, 4096), (D.Q4_K, 1024), (D.Q6_K, 1024)], 4096, 9),
+    # one-row and partial-tile segments among larger ones (rows per workgroup by byte share)
+    ([(D.Q4_K, 2000), (D.Q6_K, 1), (D.Q4_K, 37)], 4096, 13),
     # one token (the floor-shaped multi-weight kernel): q|k|v and gate|up at full size (gate|up
     # with two row sets per wave), four segments of 8-block rows, 4-block rows, groups past one
     # pass for every type (row sets), mixed types past one pass, and a segment of one workgroup
