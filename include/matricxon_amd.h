@@ -213,6 +213,16 @@ int mxa_gemm_moe_pairs(int ggml_type, const void *w, long long expert_stride, in
                        int out_features, int in_features, void *workspace,
                        size_t workspace_bytes, void *stream);
 
+/* mxa_gemm_moe_pairs on bfloat16 x (16-byte aligned; NULL: the workspace holds the Q8_K blocks
+ * of the x_rows rows, as a producer such as mxa_silu_mul_q8_k_bf16 writes them), writing bfloat16
+ * y (2-byte aligned): each output the float32 result rounded to nearest even as torch's cast
+ * rounds it. No counterpart in the reference's C library: its MoE experts on the GPU run in the
+ * layer's bfloat16 (app/architectures/moe_experts.py:81-88 through device_packed.py:53-63). */
+int mxa_gemm_moe_pairs_bf16(int ggml_type, const void *w, long long expert_stride, int n_experts,
+                            const int32_t *ids, int n_pairs, const void *x, int x_rows, void *y,
+                            int out_features, int in_features, void *workspace,
+                            size_t workspace_bytes, void *stream);
+
 /* Routing-weighted combine of MoE expert outputs, one launch: out (n_tokens, n_embd) fp32, row t =
  * the sum over token t's top_k slots k, in ascending expert id ids[t * top_k + k] (a DEVICE int32
  * array; equal ids in slot order), of down[r] * weights[t * top_k + k] with r = rows[t * top_k +

@@ -415,6 +415,38 @@ int mxa_gemm_moe_pairs(int ggml_type, const void* w, long long expert_stride, in
   return check_launch();
 }
 
+int mxa_gemm_moe_pairs_bf16(int ggml_type, const void* w, long long expert_stride, int n_experts,
+                            const int32_t* ids, int n_pairs, const void* x, int x_rows, void* y,
+                            int out_features, int in_features, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (!mxa_supports(ggml_type, in_features) || !needs_q8k(ggml_type) || w == nullptr ||
+      ids == nullptr || y == nullptr || n_experts < 1 || n_pairs < 1 || out_features < 1 ||
+      (x_rows != 1 && x_rows != n_pairs) || !aligned(x, 16) || !aligned(y, 2) ||
+      !aligned(workspace, 16))
+    return MXA_ERR_UNSUPPORTED;
+  const long long rb = (long long)mxa_row_bytes(ggml_type, in_features);
+  if (expert_stride < (long long)out_features * rb) return MXA_ERR_UNSUPPORTED;
+  const hipStream_t s = (hipStream_t)stream;
+  const int x_step = x_rows == 1 ? 0 : 1;
+  const mxa::YOut yo = mxa::YOut::bf16(y);
+  if (x != nullptr) {  // bfloat16 x read and quantized in the kernel where it can be
+    mxa::Act act = make_act((const float*)x, nullptr, in_features);
+    act.xbf16 = 1;
+    if (mxa::launch_gemv_wave_pairs(ggml_type, (const uint8_t*)w, rb, expert_stride, ids,
+                                    n_experts, n_pairs, x_step, act, yo, out_features, s) == 0)
+      return check_launch();
+  }
+  if (workspace == nullptr || workspace_bytes < mxa::act_bytes(x_rows, in_features))
+    return x == nullptr ? MXA_ERR_WORKSPACE : MXA_ERR_UNSUPPORTED;
+  const mxa::ActBuffers buf = mxa::act_layout(workspace, x_rows, in_features);
+  const mxa::Act act = make_act(nullptr, &buf, in_features);
+  if (x != nullptr) mxa::launch_quantize_q8k_bf16((const uint16_t*)x, buf, x_rows, in_features, s);
+  if (mxa::launch_gemv_wave_pairs(ggml_type, (const uint8_t*)w, rb, expert_stride, ids, n_experts,
+                                  n_pairs, x_step, act, yo, out_features, s) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
 int mxa_moe_combine(const float* down, const int32_t* rows, const int32_t* ids,
                     const float* weights, int n_tokens, int top_k, int n_embd, int round_bf16,
                     float* out, void* stream) {

@@ -460,10 +460,12 @@ __global__ __launch_bounds__(64 * kWaveMaxWaves) void gemv_wave_pairs_kernel(
   const int p = (int)blockIdx.x / G, wg = (int)blockIdx.x - p * G;
   const int e = min(max(ids[p], 0), n_experts - 1);
   const size_t r = (size_t)p * x_step;  // the pair's activation row
+  const bool xbf16 = FUSEQ && ((pack >> 23) & 1) != 0;  // x holds bfloat16 values
+  const float* xr = xbf16 ? (const float*)((const uint16_t*)x + r * K) : x + r * K;
   wave_rows<TYPE, NB, FUSEQ, ACTREG, 1, LOOP>(
-      w + (size_t)e * expert_stride, FUSEQ ? x + r * K : x, y.at((size_t)p * N), N, row_bytes,
+      w + (size_t)e * expert_stride, FUSEQ ? xr : x, y.at((size_t)p * N), N, row_bytes,
       pack & 0xFF, (pack >> 8) & 0xFF, 1, 0, FUSEQ ? aq : aq + r * K, FUSEQ ? ad : ad + r * NB,
-      FUSEQ ? abs_ : abs_ + r * NB * 16, wg, G);
+      FUSEQ ? abs_ : abs_ + r * NB * 16, wg, G, 0, xbf16);
 }
 
 template <int TYPE, int NB, bool FUSEQ, int MAXM>
@@ -659,7 +661,8 @@ int launch_pairs_t(const uint8_t* w, long long row_bytes, long long expert_strid
   allow_lds((const void*)kern, kWaveLds);
   hipLaunchKernelGGL(kern, dim3(G * n_pairs), dim3(64 * nw), lds, stream, w, expert_stride, ids,
                      n_experts, act.x, x_step, y, N, (int)row_bytes,
-                     (uint32_t)waves | (uint32_t)nq << 8 | 1u << 16, G, act.q, act.d, act.bsums);
+                     (uint32_t)waves | (uint32_t)nq << 8 | 1u << 16 | (FUSEQ && act.xbf16 ? 1u << 23 : 0u),
+                     G, act.q, act.d, act.bsums);
   return 0;
 }
 
@@ -761,7 +764,7 @@ int launch_gemv_wave_pairs(int type, const uint8_t* w, long long row_bytes, long
                            const int32_t* ids, int n_experts, int n_pairs, int x_step,
                            const Act& act, YOut y, int n_rows, hipStream_t stream) {
   if (n_rows < 1 || n_pairs < 1 || n_experts < 1 || ids == nullptr || (x_step != 0 && x_step != 1) ||
-      act.xbf16)
+      (act.xbf16 && act.q != nullptr))
     return -1;
   if (((uintptr_t)w & 15) != 0 || row_bytes % 16 != 0 || row_bytes > 0x7FFFFFFF ||
       expert_stride % 16 != 0 || expert_stride < (long long)n_rows * row_bytes)

@@ -472,13 +472,17 @@ class HipGemm:
         return out
 
     def matmul_moe_pairs(self, ggml_type: int, experts: torch.Tensor, ids: torch.Tensor,
-                         x: torch.Tensor, out_features: int, in_features: int,
-                         workspace: torch.Tensor | None = None) -> torch.Tensor | None:
+                         x: torch.Tensor | None, out_features: int, in_features: int,
+                         workspace: torch.Tensor | None = None, x_rows: int | None = None,
+                         out_dtype: torch.dtype = torch.float32) -> torch.Tensor | None:
         """One token's routed experts in one launch (`mxa_gemm_moe_pairs`): row p of the result
-        (n_pairs, out_features) float32 is expert ids[p] of `experts` (n_experts, out_features,
+        (n_pairs, out_features) is expert ids[p] of `experts` (n_experts, out_features,
         row_bytes) times row p of `x` (n_pairs rows) or the single row of `x` (one row shared by
-        all pairs). `ids`: int32 on the device, so no host sync. None when the shape does not
-        suit the launch (the caller takes `matmul_moe`). Replaces the per-expert calls of
+        all pairs). `ids`: int32 on the device, so no host sync. `out_dtype` bfloat16: x is read
+        as bfloat16 and the result written as bfloat16, each value the float32 result rounded as
+        torch's cast rounds it (`mxa_gemm_moe_pairs_bf16`). x None: `workspace` already holds the
+        Q8_K blocks of `x_rows` rows (a producer's output). None when the shape does not suit the
+        launch (the caller takes `matmul_moe`). Replaces the per-expert calls of
         QuantizedMoEExperts.forward for one token (app/architectures/moe_experts.py:81-88)."""
         ggml_type = int(ggml_type)
         _require_device_tensor("experts", experts)
@@ -490,21 +494,30 @@ class HipGemm:
         n_pairs = ids.numel()
         if ids.dtype != torch.int32 or ids.device != device or not ids.is_contiguous():
             raise ValueError(f"ids must be contiguous int32 on {device}")
-        x32 = _aligned16(x.detach().reshape(-1, in_features).to(device=device,
-                                                                dtype=torch.float32).contiguous())
-        x_rows = x32.shape[0]
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"out_dtype must be float32 or bfloat16, not {out_dtype}")
+        bf16 = out_dtype == torch.bfloat16
+        if x is None:
+            if workspace is None or x_rows is None:
+                raise ValueError("x None needs the workspace holding the Q8_K blocks and x_rows")
+            xx = None
+        else:
+            xx = _aligned16(x.detach().reshape(-1, in_features).to(
+                device=device, dtype=torch.bfloat16 if bf16 else torch.float32).contiguous())
+            x_rows = xx.shape[0]
         if x_rows not in (1, n_pairs):
             raise ValueError(f"x must have 1 or {n_pairs} rows, not {x_rows}")
         if workspace is None:
             workspace = torch.empty(q8k_bytes(x_rows, in_features), dtype=torch.uint8, device=device)
-        out = torch.empty((n_pairs, out_features), dtype=torch.float32, device=device)
-        status = self._lib.mxa_gemm_moe_pairs(
+        out = torch.empty((n_pairs, out_features), dtype=out_dtype, device=device)
+        name = "mxa_gemm_moe_pairs_bf16" if bf16 else "mxa_gemm_moe_pairs"
+        status = getattr(self._lib, name)(
             ggml_type, experts.data_ptr(), rb * out_features, experts.shape[0], ids.data_ptr(),
-            n_pairs, x32.data_ptr(), x_rows, out.data_ptr(), out_features, in_features,
-            workspace.data_ptr(), workspace.numel(), _stream(device))
+            n_pairs, None if xx is None else xx.data_ptr(), x_rows, out.data_ptr(), out_features,
+            in_features, workspace.data_ptr(), workspace.numel(), _stream(device))
         if status == -1:
             return None
-        self._check(status, "mxa_gemm_moe_pairs", ggml_type)
+        self._check(status, name, ggml_type)
         self._calls += 1
         return out
 

@@ -54,6 +54,11 @@ def combine_in_expert_order(contrib: torch.Tensor, order: torch.Tensor, top_k_id
     return out
 
 
+def _is_silu(fn) -> bool:
+    """Whether the experts' activation is SiLU (the fused producer computes exactly its steps)."""
+    return fn is torch.nn.functional.silu or isinstance(fn, torch.nn.SiLU)
+
+
 class HipPackedMoEExperts(nn.Module):
     """Packed expert FFN: gate/up/down as (num_experts, out_features, row_bytes) packed bytes on
     the device (`matricxon_amd.loading.PackedUploader.upload_experts`), all of one GGUF type each.
@@ -144,6 +149,10 @@ class HipPackedMoEExperts(nn.Module):
         g = self._gemm
         gt, ut, dt = self.types
         ids = top_k_idx.to(torch.int32).contiguous()
+        if self.dtype == torch.bfloat16 and _is_silu(self.activation):
+            out = self._one_token_bf16(x, top_k_weights, ids)
+            if out is not None:
+                return out
         # the reference casts x to the layer dtype before each matmul (device_packed.py:54); the
         # kernels take float32, so the cast values are widened once for both projections
         xs = x.to(self.dtype).to(torch.float32)
@@ -163,6 +172,36 @@ class HipPackedMoEExperts(nn.Module):
         contrib = (down.to(self.dtype) * w).to(torch.float32)  # slot order
         slot = torch.arange(ids.numel(), device=x.device)
         return combine_in_expert_order(contrib, slot, top_k_idx).to(x.dtype)
+
+    def _one_token_bf16(self, x: torch.Tensor, top_k_weights: torch.Tensor,
+                        ids: torch.Tensor) -> torch.Tensor | None:
+        """The one-token forward of a bfloat16 layer with a SiLU activation in four library
+        launches and no casts: gate and up read the bfloat16 x and write bfloat16 (the reference's
+        `gate.to(dtype)`, `up.to(dtype)`), the fused producer computes `F.silu(gate) * up` with
+        torch's bfloat16 steps and writes the down projection's Q8_K blocks of exactly that tensor,
+        and the down projection runs on them; then the combine. The same bits as the unfused steps
+        (moe_experts.py:81-88 through device_packed.py:53-63). None when a launch does not take
+        the shapes (the caller runs the float32 steps)."""
+        g = self._gemm
+        gt, ut, dt = self.types
+        idv = ids.view(-1)
+        if not self._fused_combine(top_k_weights):
+            return None
+        xb = x.to(torch.bfloat16)
+        gate = g.matmul_moe_pairs(gt, self.gate_packed, idv, xb, self.ffn_len, self.n_embd,
+                                  out_dtype=torch.bfloat16)
+        if gate is None:
+            return None
+        up = g.matmul_moe_pairs(ut, self.up_packed, idv, xb, self.ffn_len, self.n_embd,
+                                out_dtype=torch.bfloat16)
+        if up is None:
+            return None
+        _, ws = g.silu_mul_q8k(gate, up, want_out=False)
+        down = g.matmul_moe_pairs(dt, self.down_packed, idv, None, self.n_embd, self.ffn_len,
+                                  workspace=ws, x_rows=idv.numel())
+        if down is None:
+            return None
+        return self._combine(down, None, ids, top_k_weights).to(x.dtype)
 
     @classmethod
     def from_packed_bytes(cls, gate_raw, up_raw, down_raw, types: tuple[int, int, int],

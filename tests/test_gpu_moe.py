@@ -165,6 +165,8 @@ MODULE_CASES = [
     ((D.Q8_0, D.Q8_0, D.Q8_0), 4, 512, 768, 7, 2, torch.float32),
     ((D.Q4_K, D.Q4_K, D.Q4_K), 16, 512, 256, 40, 4, torch.bfloat16),
     ((D.Q6_K, D.Q6_K, D.Q4_K), 8, 256, 512, 1, 2, torch.float32),
+    # one bfloat16 token through the fused steps, the down projection on 56-block rows
+    ((D.Q4_K, D.Q4_K, D.Q6_K), 4, 1024, 14336, 1, 2, torch.bfloat16),
 ]
 
 
@@ -290,6 +292,26 @@ def test_pairs_rows_match_oracle(gpu, oracle, case) -> None:
     for p in range(n_pairs):
         xr = x[:1] if shared else x[p:p + 1]
         assert_bit_exact(got[p:p + 1], oracle.gemm(t, w[ids[p]], xr, n, k), f"pair {p}")
+
+
+@pytest.mark.parametrize("case", range(len(PAIR_CASES)))
+def test_pairs_bf16_equal_the_float32_result_cast(gpu, case) -> None:
+    """The bfloat16 pairs launch (bfloat16 x read in the kernel, bfloat16 y) equals the float32
+    launch on the bfloat16 values of x, cast by torch; on Q8_K blocks (x None) it equals it too."""
+    t, n_experts, n, k, n_pairs, shared = PAIR_CASES[case]
+    w = torch.from_numpy(expert_weights(t, n_experts, n, k, seed=case * 13)).cuda()
+    ids = torch.from_numpy(np.random.default_rng(case + 50).permutation(n_experts)[:n_pairs]
+                           .astype(np.int32)).cuda()
+    xb = torch.from_numpy(S.activations(1 if shared else n_pairs, k, seed=case + 9)).cuda().to(torch.bfloat16)
+    want = gpu.matmul_moe_pairs(t, w, ids, xb.float(), n, k)
+    got = gpu.matmul_moe_pairs(t, w, ids, xb, n, k, out_dtype=torch.bfloat16)
+    assert got is not None and got.dtype == torch.bfloat16
+    assert torch.equal(got.view(torch.int16), want.to(torch.bfloat16).view(torch.int16))
+    ws = torch.empty(q8k_bytes(xb.shape[0], k), dtype=torch.uint8, device="cuda")
+    gpu.quantize_into(xb.float(), ws)
+    pre = gpu.matmul_moe_pairs(t, w, ids, None, n, k, workspace=ws, x_rows=xb.shape[0],
+                               out_dtype=torch.bfloat16)
+    assert torch.equal(pre.view(torch.int16), got.view(torch.int16))
 
 
 def test_pairs_decline_shapes_they_do_not_take(gpu) -> None:
