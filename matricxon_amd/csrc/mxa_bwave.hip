@@ -86,16 +86,35 @@ __device__ __forceinline__ int a_stage(const Act& act, int M, int b0, int lane, 
   }
 }
 
+// The tile builders of these kernels: Q6_K on the 32-deep MFMA (TileQ6s: half the B masking
+// and MFMA cycles of TileQ6, whose 64-deep form the prefill kernels keep), the others as shared.
+template <int TYPE>
+struct BwTileOf {
+  using T = typename TileOf<TYPE>::T;
+};
+template <>
+struct BwTileOf<T_Q6_K> {
+  using T = TileQ6s;
+};
+
 // The MFMA A operands of block c from the staging area (lane: activation row ln, k-group g).
 template <int TYPE>
-__device__ __forceinline__ typename TileOf<TYPE>::T::F a_read(const uint8_t* ast, int C, int c,
-                                                              int ln, int g) {
-  typename TileOf<TYPE>::T::F f;
+__device__ __forceinline__ typename BwTileOf<TYPE>::T::F a_read(const uint8_t* ast, int C, int c,
+                                                                int ln, int g) {
+  typename BwTileOf<TYPE>::T::F f;
   const uint8_t* row = ast + c * 16 * QK + ln * QK;
+  if constexpr (TYPE == T_Q6_K) {  // chunk cc: bytes 32 cc + 8 g .. + 7 (piece 2 cc + g / 2)
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int p = TYPE == T_Q6_K ? 8 * (g >> 1) + (g & 1) + 2 * t : 4 * g + t;
-    f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(row + 16 * ((p + ln) & 15)));
+    for (int cc = 0; cc < 8; ++cc) {
+      const int p = 2 * cc + (g >> 1);
+      f.a[cc] = *(const long*)(row + 16 * ((p + ln) & 15) + 8 * (g & 1));
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int p = 4 * g + t;
+      f.a[t] = __builtin_bit_cast(i32x4, *(const u32x4*)(row + 16 * ((p + ln) & 15)));
+    }
   }
   if constexpr (TYPE != T_Q8_0) {
     const uint2 v = *(const uint2*)(ast + C * 16 * QK + c * 512 + 32 * ln + 8 * g);
@@ -131,7 +150,7 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
                                            uint32_t pack, uint32_t packm, int N, int row_bytes,
                                            const int8_t* q, const int16_t* bsums, const float* d,
                                            YOut y, int ldy, int wg) {
-  using Tile = typename TileOf<TYPE>::T;
+  using Tile = typename BwTileOf<TYPE>::T;
   using F = typename Tile::F;
   constexpr int TB = kBwBlockBytes<TYPE>;
 
@@ -478,7 +497,7 @@ __global__ __launch_bounds__(512) void bwlong_kernel(const uint8_t* __restrict__
                                                      uint32_t packm, int N, int row_bytes,
                                                      const int8_t* q, const int16_t* bsums,
                                                      const float* d, YOut y, int ldy) {
-  using Tile = typename TileOf<TYPE>::T;
+  using Tile = typename BwTileOf<TYPE>::T;
   using F = typename Tile::F;
   constexpr int TB = kBwBlockBytes<TYPE>;
   constexpr int kStageA = a_stage_bytes<TYPE>(C);

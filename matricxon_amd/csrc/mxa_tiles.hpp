@@ -315,6 +315,99 @@ struct TileQ6 {
   }
 };
 
+// ------------------------------------------------------------------------- Q6_K, 32-deep MFMAs
+// Q6_K on v_mfma_i32_16x16x32_i8 (A 16 x 32, B 32 x 16, a lane holding 8 k-values) with the block's
+// elements in natural order: chunk c (MFMA k = 32 c .. 32 c + 31) gives lane group g elements
+// 32 c + 8 g + (0..7), so lane groups {0, 1} hold sub-block 2 c and {2, 3} sub-block 2 c + 1.
+// Masking B to one pair of lane groups gives a sub-block's integer dot from half-masked operands
+// (8-byte B: two selects per MFMA instead of four), in 16 MFMAs of half the depth. Element
+// 32 c + 8 g + j (half h = c / 4, quarter r = c % 4, l = 8 g + j) is ql[64 h + l + 32 (r & 1)]'s
+// low (r < 2) or high nibble with qh[32 h + l]'s bits 2 r .. 2 r + 1 above (kquants.py:138-159),
+// so a lane reads four 8-byte runs of ql and two of qh. The integer block sum equals TileQ6's.
+struct TileQ6s {
+  struct W {
+    u32x2a4 ql[2][2];  // ql[64 h + 32 q + 8 g ..] for half h, q = r & 1
+    u32x2a4 qh[2];     // qh[32 h + 8 g ..]
+    u32x4a4 sc;        // the row's 16 scales
+    uint32_t d;
+  };
+  struct P {
+    u32x2a4 bu[8];  // codes u of chunk c
+    uint32_t scw[4];
+    f16x4 bsc;  // scales 4 g .. 4 g + 3 (the bsums term)
+    float d;
+  };
+  struct F {
+    long a[8];  // activations 32 c + 8 g .. + 7 of row ln
+    f16x4 bs;
+  };
+  // 8 bytes at buf + off in LDS, off even (2-byte-aligned blocks): dword reads + v_alignbyte.
+  __device__ __forceinline__ static u32x2a4 lds8_a2(const uint8_t* buf, int off) {
+    const int base = off & ~3;
+    const uint32_t sh = (uint32_t)(off & 3);
+    const u32x2a4 v = *(const u32x2a4*)(buf + base);
+    const uint32_t e = sh ? *(const uint32_t*)(buf + base + 8) : 0u;
+    return u32x2a4{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(e, v.y, sh)};
+  }
+  __device__ __forceinline__ static W load_lds(const uint8_t* buf, int off, int g) {
+    W L;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) L.ql[h][q] = lds8_a2(buf, off + 64 * h + 32 * q + 8 * g);
+      L.qh[h] = lds8_a2(buf, off + 128 + 32 * h + 8 * g);
+    }
+    L.sc = TileQ6::lds16_a2(buf, off + 192);
+    L.d = (uint32_t)*(const uint16_t*)(buf + off + 208);
+    return L;
+  }
+  __device__ static float fold(float acc, float xd, float v, float d) { return fmaf(xd * d, v, acc); }
+  __device__ static P prep(const W& L, int g) {
+    P p;
+    p.d = half_to_float(L.d);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int h = c >> 2, r = c & 3;
+      const u32x2a4 lo = L.ql[h][r & 1], hi = L.qh[h];
+      const uint32_t ls = 4 * (r >> 1), hs = 2 * r;
+      p.bu[c] = u32x2a4{((lo.x >> ls) & 0x0F0F0F0Fu) | (((hi.x >> hs) & 0x03030303u) << 4),
+                        ((lo.y >> ls) & 0x0F0F0F0Fu) | (((hi.y >> hs) & 0x03030303u) << 4)};
+    }
+    p.scw[0] = L.sc.x, p.scw[1] = L.sc.y, p.scw[2] = L.sc.z, p.scw[3] = L.sc.w;
+    const uint32_t sw = g == 0 ? L.sc.x : g == 1 ? L.sc.y : g == 2 ? L.sc.z : L.sc.w;  // no indexing
+    p.bsc = f16x4{(_Float16)(float)(int8_t)(sw & 0xFF), (_Float16)(float)(int8_t)((sw >> 8) & 0xFF),
+                  (_Float16)(float)(int8_t)((sw >> 16) & 0xFF), (_Float16)(float)(int8_t)(sw >> 24)};
+    return p;
+  }
+  // the 16 sub-block dots (chunk c, lane-group pair u: sub-block 2 c + u) issued before any is
+  // scaled; C = sum over the sub-blocks of bsums(m) * sc(n), exact
+  template <class S>
+  __device__ static void value_wide(const P& p, const F& f, int g, S&& sink) {
+    i32x4 D[8][2];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bool on = (g >> 1) == u;
+        const long b = (long)(((uint64_t)(on ? p.bu[c].y : 0u) << 32) | (on ? p.bu[c].x : 0u));
+        D[c][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(f.a[c], b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+      }
+    const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bsc, f32x4{0, 0, 0, 0}, 0, 0, 0);
+    int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int s = 2 * c + u;
+        const int sc = (int)(int8_t)(uint8_t)(p.scw[s >> 2] >> (8 * (s & 3)));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sumi[i] += __mul24(sc, D[c][u][i]);
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sink(i, (float)(sumi[i] - 32 * (int)C[i]), p.d);
+  }
+};
+
 // ---------------------------------------------------------------------------------------- Q8_0
 struct TileQ8 {
   struct W {
