@@ -8,6 +8,7 @@ reference's loader, app/native/library.py:70-91).
 """
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -35,6 +36,28 @@ HIPCC_FLAGS = [
     # memory requests need no kernel-argument load (measured: -0.25 us per 33 MB launch)
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
+
+
+# Sources whose kernels must use no scratch memory. mxa_bwave.hip issues loads into registers
+# from inline assembly and waits for them itself; the compiler treats those registers as written
+# at issue, so a spill (or any reuse of them) before the wait would read or clobber registers a
+# load still writes. Such a build is refused rather than shipped.
+NO_SCRATCH = {"mxa_bwave.hip"}
+_RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+
+
+def scratch_users(stderr: str) -> list[str]:
+    """Kernels with a nonzero 'ScratchSize' in hipcc's kernel-resource-usage remarks."""
+    bad, name = [], None
+    for line in stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name is not None and int(m.group(1)) > 0:
+            bad.append(f"{name} ({m.group(1)} bytes/lane)")
+    return bad
 
 
 def hipcc() -> str:
@@ -67,16 +90,23 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(src: Path) -> tuple[Path, subprocess.CompletedProcess]:
         obj = obj_dir / (src.stem + ".o")
-        cmd = [hipcc(), *compile_flags, "-c", "-o", str(obj), str(src)]
+        extra = [_RESOURCE_REMARKS] if src.name in NO_SCRATCH else []
+        cmd = [hipcc(), *compile_flags, *extra, "-c", "-o", str(obj), str(src)]
         if verbose:
             print(" ".join(cmd), flush=True)
         return obj, subprocess.run(cmd, capture_output=True, text=True)
 
+    srcs = sources()
     with ThreadPoolExecutor(_jobs()) as pool:
-        results = list(pool.map(compile_one, sources()))
+        results = list(pool.map(compile_one, srcs))
     errors = [r.stderr for _, r in results if r.returncode != 0]
     if errors:
         raise RuntimeError("hipcc failed:\n" + "\n".join(e[-8000:] for e in errors))
+    for src, (_, r) in zip(srcs, results):
+        if src.name in NO_SCRATCH:
+            bad = scratch_users(r.stderr)
+            if bad:
+                raise RuntimeError(f"{src.name}: kernels that must not use scratch do: " + ", ".join(bad))
     fd, tmp = tempfile.mkstemp(dir=PKG_DIR, suffix=".so.tmp")
     os.close(fd)
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,

@@ -192,7 +192,10 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
   //    m = lane % 16 into registers (four 16-byte loads, nb % 4 == 0), issued before any weight
   //    copy so that they land first. The scale loads are inline assembly, so the compiler's wait
   //    insertion never waits for them (it would wait for every copy issued after them); no
-  //    branch or copy of their registers comes before the wave's own wait.
+  //    branch or copy of their registers comes before the wave's own wait. The compiler takes
+  //    these registers as written at issue: a spill or reuse of them before the wait would read
+  //    or clobber registers the loads still write (a variant that spilled here faulted), so the
+  //    build refuses any kernel of this file that uses scratch memory.
   const int am = min(ln, M - 1);
   const int n_stage = a_stage<TYPE, C>(act, M, b0, lane, lds_addr(ast));
   f32x4 xq[4];
@@ -337,18 +340,21 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  // The 16 reads of an output are unconditional and their slot offsets scalar (a runtime branch
+  // and a vector multiply per read made this loop ~1.3 us of a 12 us kernel); blocks past nb read
+  // the last wave's slot and are never folded.
+  const int wstride = T * slot_bytes / 4;  // floats between one wave's slots and the next's
   for (int o = tid; o < T * 256; o += 64 * ncw) {
     const int t = o >> 8, j = (o >> 4) & 15, m = o & 15;
     if (j < rows - 16 * t && m < M) {
+      const float* tb = (const float*)slot(0, t);
       float vv[16], dd[16];
 #pragma unroll
       for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
-        if (b < nb) {
-          const int wv = b / C, cc = b - wv * C;
-          const float* src = (const float*)slot(wv, t);
-          vv[b] = src[(cc * 16 + j) * 16 + m];
-          dd[b] = src[C * 256 + cc * 16 + j];
-        }
+        const int wv = min(b / C, ncw - 1), cc = b % C;
+        const float* src = tb + wv * wstride;
+        vv[b] = src[(cc * 16 + j) * 16 + m];
+        dd[b] = src[C * 256 + cc * 16 + j];
       }
       float acc = 0.0f;
 #pragma unroll

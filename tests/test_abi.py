@@ -162,3 +162,21 @@ def test_fp32_gemv_registry_and_backend_setting(monkeypatch) -> None:
     g = DP.HipGemm.get()
     with pytest.raises(ValueError, match="HIP device"):
         g.gemv_f32(14, torch.zeros((1, 210), dtype=torch.uint8), torch.zeros(1, 256), 1, 256)
+
+
+def test_build_refuses_scratch_in_register_load_kernels() -> None:
+    """mxa_bwave.hip's kernels load into registers from inline assembly and wait themselves, so
+    the build must refuse any of them that spills: the parser of hipcc's resource remarks names
+    exactly the kernels with a nonzero scratch size."""
+    from matricxon_amd import build
+
+    assert "mxa_bwave.hip" in build.NO_SCRATCH
+    remarks = "\n".join([
+        "x.hip:9:1: remark: Function Name: _Zkeep [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: _Zspill [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     VGPRs: 128 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 228 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build.scratch_users(remarks) == ["_Zspill (228 bytes/lane)"]
+    assert build.scratch_users("") == []
