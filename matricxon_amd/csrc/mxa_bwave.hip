@@ -343,25 +343,49 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
   // The 16 reads of an output are unconditional and their slot offsets scalar (a runtime branch
   // and a vector multiply per read made this loop ~1.3 us of a 12 us kernel); blocks past nb read
   // the last wave's slot and are never folded.
+  // A thread folds two outputs (o, o + step) at a time, their chains interleaved, and the chains
+  // of full 16-block rows carry no per-block select. Output o is (tile t, weight row j,
+  // activation row m = o % 16 = the lane's own row, whose scales xd holds).
   const int wstride = T * slot_bytes / 4;  // floats between one wave's slots and the next's
-  for (int o = tid; o < T * 256; o += 64 * ncw) {
+  const int nout = T * 256, step = 64 * ncw;
+  auto read_vals = [&](int o, float* vv, float* dd) {
     const int t = o >> 8, j = (o >> 4) & 15, m = o & 15;
-    if (j < rows - 16 * t && m < M) {
-      const float* tb = (const float*)slot(0, t);
-      float vv[16], dd[16];
+    const float* tb = (const float*)slot(0, t);
 #pragma unroll
-      for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
-        const int wv = min(b / C, ncw - 1), cc = b % C;
-        const float* src = tb + wv * wstride;
-        vv[b] = src[(cc * 16 + j) * 16 + m];
-        dd[b] = src[C * 256 + cc * 16 + j];
-      }
-      float acc = 0.0f;
-#pragma unroll
-      for (int b = 0; b < 16; ++b)
-        if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
-      y.put((size_t)m * ldy + r0 + 16 * t + j, acc);
+    for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
+      const int wv = min(b / C, ncw - 1), cc = b % C;
+      const float* src = tb + wv * wstride;
+      vv[b] = src[(cc * 16 + j) * 16 + m];
+      dd[b] = src[C * 256 + cc * 16 + j];
     }
+  };
+  auto store = [&](int o, float acc) {
+    const int t = o >> 8, j = (o >> 4) & 15, m = o & 15;
+    if (o < nout && j < rows - 16 * t && m < M) y.put((size_t)m * ldy + r0 + 16 * t + j, acc);
+  };
+  for (int o = tid; o < nout; o += 2 * step) {
+    const int o2 = o + step;
+    float v0[16], d0[16], v1[16], d1[16];
+    read_vals(o, v0, d0);
+    read_vals(o2 < nout ? o2 : o, v1, d1);  // past the end: o's operands again, never stored
+    float a0 = 0.0f, a1 = 0.0f;
+    if (nb == 16) {
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        a0 = Tile::fold(a0, xd[b], v0[b], d0[b]);
+        a1 = Tile::fold(a1, xd[b], v1[b], d1[b]);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        if (b < nb) {
+          a0 = Tile::fold(a0, xd[b], v0[b], d0[b]);
+          a1 = Tile::fold(a1, xd[b], v1[b], d1[b]);
+        }
+      }
+    }
+    store(o, a0);
+    store(o2, a1);
   }
 }
 
