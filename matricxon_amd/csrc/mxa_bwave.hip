@@ -251,12 +251,12 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
     asm volatile("" ::: "memory");
   }
 
-  // RING: the output a fold thread computed for the previous tile, stored only after the next
-  // tile's wait and request, so that its store is not pending at that wait (with D = 1 the wait
-  // is for every outstanding operation)
-  float pend = 0.0f;
-  size_t pend_at = 0;
-  bool pend_ok = false;
+  // RING: the outputs a fold thread computed for the previous tile (two when the workgroup has
+  // fewer than 256 threads), stored only after the next tile's wait and request, so that their
+  // stores are not pending at that wait (with D = 1 the wait is for every outstanding operation)
+  float pend[2] = {0.0f, 0.0f};
+  size_t pend_at[2] = {0, 0};
+  bool pend_ok[2] = {false, false};
   for (int t = 0; t < T; ++t) {
     // tile t has landed once only the later tiles' copies are outstanding (a store of an earlier
     // fold issued since can only make this wait longer, never shorter: loads complete in order)
@@ -265,8 +265,11 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
     wait_vmcnt(later);
     if (t + D < T) issue(t + D);
     if constexpr (RING) {
-      if (pend_ok) y.put(pend_at, pend);
-      pend_ok = false;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        if (pend_ok[k]) y.put(pend_at[k], pend[k]);
+        pend_ok[k] = false;
+      }
     }
     const int live = min(16, rows - 16 * t);
     uint8_t* sl = slot(wave, t);
@@ -298,24 +301,34 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
       __builtin_amdgcn_s_waitcnt(0xC07F);
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (tid < 256) {  // fold tile t: output (row j, activation row m = the thread's own)
-        const int j = tid >> 4, m = tid & 15;
-        if (j < live && m < M) {
-          float vv[16], dd[16];
+      // fold tile t: output o = (row j, activation row m = o % 16, the thread's own), by the
+      // first 256 threads, or by all of them, two outputs each, in a workgroup of two waves (rows
+      // of four blocks). Blocks past nb hold stale values and are never folded.
+      const int nf = min(64 * ncw, 256);
+      if (tid < nf) {
 #pragma unroll
-          for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
-            if (b < nb) {
+        for (int k = 0; k < 2; ++k) {
+          const int o = tid + k * nf, j = o >> 4, m = o & 15;
+          if (o < 256 && j < live && m < M) {
+            float vv[16], dd[16];
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {  // operands read ahead of the dependent chain
               vv[b] = vals[(b * 16 + j) * 16 + m];
               dd[b] = vals[16 * 256 + b * 16 + j];
             }
-          }
-          float acc = 0.0f;
+            float acc = 0.0f;
+            if (nb == 16) {
 #pragma unroll
-          for (int b = 0; b < 16; ++b)
-            if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
-          pend = acc;
-          pend_at = (size_t)m * ldy + r0 + 16 * t + j;
-          pend_ok = true;
+              for (int b = 0; b < 16; ++b) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
+            } else {
+#pragma unroll
+              for (int b = 0; b < 16; ++b)
+                if (b < nb) acc = Tile::fold(acc, xd[b], vv[b], dd[b]);
+            }
+            pend[k] = acc;
+            pend_at[k] = (size_t)m * ldy + r0 + 16 * t + j;
+            pend_ok[k] = true;
+          }
         }
       }
     } else {
@@ -332,7 +345,9 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
     }
   }
   if constexpr (RING) {
-    if (pend_ok) y.put(pend_at, pend);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (pend_ok[k]) y.put(pend_at[k], pend[k]);
     return;
   }
   // 3. every wave has written its block values of every tile: the workgroup folds all outputs

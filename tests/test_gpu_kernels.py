@@ -341,7 +341,10 @@ BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5
                 (5000, 1024, 16), (23, 768, 7), (260, 5120, 9), (1000, 14336, 16), (50, 4352, 6),
                 (14336, 4096, 16), (8192, 4096, 12), (3000, 2304, 13), (14000, 512, 10),
                 (20000, 4096, 6), (30000, 4096, 13), (40000, 2048, 5), (50000, 4096, 16),
-                (9000, 5120, 12), (40000, 4608, 4), (300, 8192, 16), (5000, 14336, 5)]
+                (9000, 5120, 12), (40000, 4608, 4), (300, 8192, 16), (5000, 14336, 5),
+                # 4-block rows past eight tiles per CU: the gather kernel's ring form with two
+                # waves (128 threads, each folding two outputs of a tile)
+                (40000, 1024, 11)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
