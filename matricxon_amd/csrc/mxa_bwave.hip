@@ -166,19 +166,22 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r0 = wg * R;
   const int rows = min(R, N - r0);  // >= 1: the grid is ceil(N / R)
-  const int T = (rows + 15) >> 4;
+  const int T = (rows + 15) >> 4;   // tiles this workgroup computes
+  const int TG = (R + 15) >> 4;     // tiles of the layout the host sized (the last workgroup
+                                    // may have fewer rows; its slots keep the same places)
   const int slot_bytes = 16 * rs * 16;
   constexpr int kStage = a_stage_bytes<TYPE>(C);
   const int S = D + 1;  // RING: slots per wave
   // resident: tile t of wave wv; RING: slot t mod S of every wave, slot index major
   auto slot = [&](int wv, int t) {
-    return RING ? smem + ((t % S) * ncw + wv) * slot_bytes : smem + (wv * T + t) * slot_bytes;
+    return RING ? smem + ((t % S) * ncw + wv) * slot_bytes : smem + (wv * TG + t) * slot_bytes;
   };
   uint8_t* vring = smem + S * ncw * slot_bytes;  // RING: two entries of kBwValBytes
-  // the wave's staging area: resident, its slots of tiles T - 2, T - 1 (requested after the
+  // the wave's staging area: resident, its slots of tiles TG - 2, TG - 1 (the host puts it there
+  // only when TG - 2 >= D, so those tiles, if this workgroup has them, are requested after the
   // operands are read) or an area of its own after all slots; RING, from slot index D on
   uint8_t* ast = RING ? smem + D * ncw * slot_bytes + wave * kStage
-               : stage_in_slots ? slot(wave, T - 2) : smem + ncw * T * slot_bytes + wave * kStage;
+               : stage_in_slots ? slot(wave, TG - 2) : smem + ncw * TG * slot_bytes + wave * kStage;
 
   // this wave's blocks, and its piece of a row: chunks [c_lo, c_hi) of the row (16-byte aligned
   // chunks covering bytes b0 TB .. (b0 + cb) TB; rows are 16-byte multiples, so they stay inside)
@@ -361,7 +364,7 @@ __device__ __forceinline__ void bwave_rows(uint8_t* smem, const uint8_t* __restr
   // A thread folds two outputs (o, o + step) at a time, their chains interleaved, and the chains
   // of full 16-block rows carry no per-block select. Output o is (tile t, weight row j,
   // activation row m = o % 16 = the lane's own row, whose scales xd holds).
-  const int wstride = T * slot_bytes / 4;  // floats between one wave's slots and the next's
+  const int wstride = TG * slot_bytes / 4;  // floats between one wave's slots and the next's
   const int nout = T * 256, step = 64 * ncw;
   auto read_vals = [&](int o, float* vv, float* dd) {
     const int t = o >> 8, j = (o >> 4) & 15, m = o & 15;

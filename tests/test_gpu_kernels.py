@@ -344,7 +344,10 @@ BATCH_SHAPES = [(4100, 4096, 16), (1000, 4096, 8), (300, 8192, 12), (77, 2304, 5
                 (9000, 5120, 12), (40000, 4608, 4), (300, 8192, 16), (5000, 14336, 5),
                 # 4-block rows past eight tiles per CU: the gather kernel's ring form with two
                 # waves (128 threads, each folding two outputs of a tile)
-                (40000, 1024, 11)]
+                (40000, 1024, 11),
+                # resident gather form whose last workgroup has 13 rows (one tile of the five the
+                # layout holds): its slots and operand staging keep the layout's places
+                (20000, 2048, 8)]
 
 
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
