@@ -236,9 +236,10 @@ int gemm_multi_q8k_core(int n, const int* types, const void* const* ws, const in
 extern "C" {
 
 const char* mxa_build_info(void) {
-  return "matricxon_amd gfx950: bit-exact dequant (Q8_0/Q4_K/Q6_K/IQ4_XS); decode (M<=4): "
-         "pipelined LDS-DMA GEMV with in-kernel Q8_K quantization; M>4: int8 MFMA tiles "
-         "(Q4_K/Q6_K/Q8_0), bf16 split MFMA prefill (IQ4_XS)";
+  return "matricxon_amd gfx950: bit-exact dequant (Q8_0/Q4_K/Q6_K/IQ4_XS); decode M<=3: "
+         "LDS-DMA wave GEMV with in-kernel Q8_K quantization; M 4..16: int8 MFMA gather kernel, "
+         "each wave streaming its own block columns; prefill: int8 MFMA tiles (Q4_K/Q6_K/Q8_0), "
+         "bf16 split MFMA (IQ4_XS)";
 }
 
 int mxa_supports(int ggml_type, int in_features) {
