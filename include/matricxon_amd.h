@@ -100,7 +100,11 @@ int mxa_gemm(int ggml_type, const void *w, const float *x, float *y, int n_token
  * of the largest of each kind. Host-only. */
 size_t mxa_workspace_bytes_bf16(int ggml_type, int n_tokens, int in_features);
 
-/* mxa_gemm on bfloat16 x, writing bfloat16 y. */
+/* mxa_gemm on bfloat16 x, writing bfloat16 y. A call that the decode kernel reading bfloat16 x
+ * takes (K-quant or Q8_0 weights, n_tokens <= mxa_fused_max_tokens, a supported geometry) uses no
+ * workspace, so `workspace` may be NULL there; any other call with a workspace short of
+ * mxa_workspace_bytes_bf16 returns MXA_ERR_WORKSPACE having launched nothing. The same holds for
+ * mxa_gemm_multi_bf16 at one token. */
 int mxa_gemm_bf16(int ggml_type, const void *w, const void *x, void *y, int n_tokens,
                   int out_features, int in_features, void *workspace, size_t workspace_bytes,
                   void *stream);

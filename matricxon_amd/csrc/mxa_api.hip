@@ -105,7 +105,6 @@ int gemm_multi_core(int n, const int* types, const void* const* ws, const int* o
   const size_t widen_bytes = xbf16 ? widen_part(any_iq4, n_tokens, in_features) : 0;
   const size_t split_bytes = split_part(any_iq4, n_tokens, in_features);
   const size_t need = q8k_bytes + widen_bytes + split_bytes;
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MXA_ERR_WORKSPACE;
   mxa::DecodeSeg seg[4];
   long long c0 = 0;
   for (int i = 0; i < n; ++i) {
@@ -114,7 +113,8 @@ int gemm_multi_core(int n, const int* types, const void* const* ws, const int* o
     c0 += outs[i];
   }
   if (xbf16 && !any_iq4 && n_tokens <= fmax) {
-    // the floor-shaped decode kernel reads bfloat16 x and quantizes it itself (one launch)
+    // the floor-shaped decode kernel reads bfloat16 x and quantizes it itself (one launch, no
+    // workspace); a launcher that declines has launched nothing
     mxa::Act a = make_act((const float*)x, nullptr, in_features);
     a.xbf16 = 1;
     const int st = n == 1 ? mxa::launch_gemv_wave_m(types[0], seg[0].w, seg[0].row_bytes, a, y,
@@ -123,6 +123,7 @@ int gemm_multi_core(int n, const int* types, const void* const* ws, const int* o
                                  : -1;
     if (st == 0) return check_launch();
   }
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MXA_ERR_WORKSPACE;
   const float* xf = xbf16 ? nullptr : (const float*)x;
   if (widen_bytes > 0) {
     float* wide = (float*)((uint8_t*)workspace + q8k_bytes);

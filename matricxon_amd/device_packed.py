@@ -161,7 +161,8 @@ class DevicePackedLinear(nn.Module):
         if self.backend == "numba":
             return self.finish(self._forward_f32(x.reshape(-1, k)), lead)
         # The reference casts x to the layer dtype before its matmul (device_packed.py:54).
-        x = x.to(self._dtype)
+        if x.dtype != self._dtype:
+            x = x.to(self._dtype)
         bf16 = self._dtype == torch.bfloat16  # the kernels read and write bfloat16 themselves
         dev = self.packed.device
         n, big_n = x.numel() // k, self.out_features
@@ -195,8 +196,11 @@ class DevicePackedLinear(nn.Module):
         return y
 
     def finish(self, y: torch.Tensor, lead: tuple[int, ...]) -> torch.Tensor:
-        """Float32 result rows (M, N) -> the layer's output (..., N) in its dtype, plus bias."""
-        y = y.to(self._dtype).reshape(*lead, self.out_features)
+        """Result rows (M, N), float32 or already the layer's dtype -> the layer's output (..., N)
+        in its dtype, plus bias."""
+        if y.dtype != self._dtype:
+            y = y.to(self._dtype)
+        y = y.reshape(*lead, self.out_features)
         return y if self.bias is None else y + self.bias
 
 

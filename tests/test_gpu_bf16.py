@@ -217,3 +217,47 @@ def test_bf16_module_without_handoff_is_one_call(gpu) -> None:
     # a view that does not start on a 16-byte boundary is copied first
     xs = x_bf16(2, k + 8, seed=13)[:, 8:]
     assert torch.equal(bf16_bits(mod(xs)), bf16_bits(mod32(xs.float()).to(BF)))
+
+
+# (type, N, K, M, taken by the kernel that reads bfloat16 x): its one- and three-row forms, a
+# block count it has no form for, IQ4_XS (float activations), batched decode
+NO_WS_CASES = [
+    (D.Q4_K, 4096, 4096, 1, True), (D.Q6_K, 1024, 4096, 3, True), (D.Q8_0, 512, 2048, 2, True),
+    (D.Q4_K, 700, 768, 1, False), (D.IQ4_XS, 1024, 4096, 1, False), (D.Q4_K, 4096, 4096, 16, False),
+]
+
+
+@pytest.mark.parametrize("t,n,k,m,taken", NO_WS_CASES)
+def test_gemm_bf16_without_workspace(gpu, t, n, k, m, taken) -> None:
+    """mxa_gemm_bf16 with a NULL workspace: a call the one-launch decode kernel takes gives the
+    bits of the call with a workspace; any other returns MXA_ERR_WORKSPACE and launches nothing
+    (y keeps its sentinel)."""
+    from matricxon_amd.gemm import _stream
+
+    assert gpu.fused_max_tokens == 3
+    w = dev(S.packed_weight(t, n, k, seed=21 + m))
+    xb = x_bf16(m, k, seed=22 + m)
+    y = torch.full((m, n), 7.0, dtype=BF, device=w.device)
+    status = gpu._lib.mxa_gemm_bf16(t, w.data_ptr(), xb.data_ptr(), y.data_ptr(), m, n, k, None, 0,
+                                    _stream(w.device))
+    torch.cuda.synchronize()
+    if taken:
+        assert status == 0
+        assert torch.equal(bf16_bits(y), bf16_bits(gpu.matmul(t, w, xb.float(), n, k).to(BF)))
+    else:
+        assert status == -2
+        assert bool((y == 7.0).all())
+
+
+def test_raw_stream_handle_is_torchs_current_stream() -> None:
+    """The launch stream the library is given is torch's current stream: the default one, one
+    entered with `torch.cuda.stream`, for a device named with and without its index."""
+    from matricxon_amd.gemm import _stream
+
+    d = torch.device("cuda:0")
+    assert _stream(d) == torch.cuda.current_stream(d).cuda_stream
+    side = torch.cuda.Stream(d)
+    with torch.cuda.stream(side):
+        assert _stream(d) == side.cuda_stream
+        assert _stream(torch.device("cuda")) == side.cuda_stream
+    assert _stream(d) == torch.cuda.current_stream(d).cuda_stream != side.cuda_stream
