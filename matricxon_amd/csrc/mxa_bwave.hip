@@ -107,7 +107,9 @@ __device__ __forceinline__ typename BwTileOf<TYPE>::T::F a_read(const uint8_t* a
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) {
       const int p = 2 * cc + (g >> 1);
-      f.a[cc] = *(const long*)(row + 16 * ((p + ln) & 15) + 8 * (g & 1));
+      const long v = *(const long*)(row + 16 * ((p + ln) & 15) + 8 * (g & 1));
+      f.a[0][cc] = (g >> 1) == 0 ? v : 0;  // the copy for sub-block 2 cc (lane groups 0, 1)
+      f.a[1][cc] = (g >> 1) == 1 ? v : 0;  // and for sub-block 2 cc + 1 (lane groups 2, 3)
     }
   } else {
 #pragma unroll

@@ -319,8 +319,11 @@ struct TileQ6 {
 // Q6_K on v_mfma_i32_16x16x32_i8 (A 16 x 32, B 32 x 16, a lane holding 8 k-values) with the block's
 // elements in natural order: chunk c (MFMA k = 32 c .. 32 c + 31) gives lane group g elements
 // 32 c + 8 g + (0..7), so lane groups {0, 1} hold sub-block 2 c and {2, 3} sub-block 2 c + 1.
-// Masking B to one pair of lane groups gives a sub-block's integer dot from half-masked operands
-// (8-byte B: two selects per MFMA instead of four), in 16 MFMAs of half the depth. Element
+// Zeroing one operand outside one pair of lane groups gives a sub-block's integer dot, in 16 MFMAs
+// of half the depth. The zeroing sits in the A operands: F holds a lane's activation bytes twice,
+// once per lane-group pair, the copy of the other pair zero, so a kernel whose waves keep their A
+// operands across weight tiles builds the masks once per operand instead of selecting 32 B dwords
+// per block and tile (the B codes go to the MFMAs unmasked). Element
 // 32 c + 8 g + j (half h = c / 4, quarter r = c % 4, l = 8 g + j) is ql[64 h + l + 32 (r & 1)]'s
 // low (r < 2) or high nibble with qh[32 h + l]'s bits 2 r .. 2 r + 1 above (kquants.py:138-159),
 // so a lane reads four 8-byte runs of ql and two of qh. The integer block sum equals TileQ6's.
@@ -338,7 +341,7 @@ struct TileQ6s {
     float d;
   };
   struct F {
-    long a[8];  // activations 32 c + 8 g .. + 7 of row ln
+    long a[2][8];  // activations 32 c + 8 g .. + 7 of row ln in a[g / 2][c]; a[1 - g / 2][c] = 0
     f16x4 bs;
   };
   // 8 bytes at buf + off in LDS, off even (2-byte-aligned blocks): dword reads + v_alignbyte.
@@ -385,13 +388,12 @@ struct TileQ6s {
   __device__ static void value_wide(const P& p, const F& f, int g, S&& sink) {
     i32x4 D[8][2];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < 8; ++c) {
+      const long b = (long)(((uint64_t)p.bu[c].y << 32) | p.bu[c].x);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const bool on = (g >> 1) == u;
-        const long b = (long)(((uint64_t)(on ? p.bu[c].y : 0u) << 32) | (on ? p.bu[c].x : 0u));
-        D[c][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(f.a[c], b, i32x4{0, 0, 0, 0}, 0, 0, 0);
-      }
+      for (int u = 0; u < 2; ++u)
+        D[c][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(f.a[u][c], b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    }
     const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x16f16(f.bs, p.bsc, f32x4{0, 0, 0, 0}, 0, 0, 0);
     int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
