@@ -80,35 +80,40 @@ __device__ __forceinline__ IQ4W load_iq4(const uint8_t* row, int b, int g) {
   return L;
 }
 
-// A workgroup takes 128 weight rows (8 waves of 16) x 16 MT activation rows. The activations of a
-// block (bf16 hi and lo, 2 x 512 B per row) go to one of two LDS buffers: the next block's are
-// loaded into registers while the current block is computed and written to the other buffer
+// A workgroup takes 16 NT weight rows per wave (8 waves) x 16 MT activation rows. The activations
+// of a block (bf16 hi and lo, 2 x 512 B per row) go to one of two LDS buffers: the next block's
+// are loaded into registers while the current block is computed and written to the other buffer
 // afterwards, so one barrier per block suffices (a buffer is rewritten only after every wave has
 // passed the barrier that ends its last use). Per sub-block t the B operand is the grid values of
 // elements 32 t + 8 g .. of row n; one MFMA pair (hi, then lo) gives sum(K * x), scaled by dl in
-// fp32, sub-blocks and blocks in order.
+// fp32, sub-blocks and blocks in order. Every wave reads the workgroup's activation tiles from LDS,
+// so the NT weight tiles of a wave share each A-operand read (LDS bytes per MFMA / NT).
 constexpr int kIq4Waves = 8;
-constexpr int kIq4WgRows = 16 * kIq4Waves;
 
-template <int MT>
+template <int MT, int NT>
 __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t* w, long long row_bytes,
                                                                    const uint16_t* __restrict__ xh,
                                                                    const uint16_t* __restrict__ xl,
                                                                    int K, YOut y,
                                                                    long long ldy, int M, int N) {
   constexpr int kRows = 16 * MT;
+  constexpr int kWgRows = 16 * NT * kIq4Waves;
   constexpr int kBuf = 2 * kRows * kXStride;                  // hi rows, then lo rows
   constexpr int kPieces = kRows * 64 / (64 * kIq4Waves);      // 16-byte pieces per thread
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ln = lane & 15, g = lane >> 4;
-  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * kIq4WgRows + 16 * wave;
+  const int n0 = xcd_tile(blockIdx.x, gridDim.x) * kWgRows + 16 * NT * wave;
   const int m0 = blockIdx.y * kRows;
-  const uint8_t* row = w + (size_t)min(n0 + ln, N - 1) * row_bytes;
-  const int nb = K / QK;
-  f32x4 acc[MT];
+  const uint8_t* row[NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int nt = 0; nt < NT; ++nt) row[nt] = w + (size_t)min(n0 + 16 * nt + ln, N - 1) * row_bytes;
+  const int nb = K / QK;
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // thread tid stages pieces p = tid + 512 i: row p / 64, hi (p % 64 < 32) or lo, piece p % 32;
   // rows >= M repeat row M - 1
@@ -128,52 +133,78 @@ __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t
       *(u32x4a4*)(buf + part * kRows * kXStride + r * kXStride + 16 * q) = stage[i];
     }
   };
-  IQ4W cur = load_iq4(row, 0, g), nxt;
+  IQ4W cur[NT], nxt[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) cur[nt] = load_iq4(row[nt], 0, g);
   load_x(0);
   store_x(smem);
   __syncthreads();
   for (int b = 0; b < nb; ++b) {
     if (b + 1 < nb) {
       load_x(b + 1);
-      nxt = load_iq4(row, b + 1, g);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) nxt[nt] = load_iq4(row[nt], b + 1, g);
     }
     const uint8_t* Xh = smem + (b & 1) * kBuf;
     const uint8_t* Xl = Xh + kRows * kXStride;
-    const float d = half_to_float(cur.hdr[0]);
-    const uint32_t sh = cur.hdr[0] >> 16, sl = cur.hdr[1];
+    // sub-block t's scale bits and index words move to the front as t advances (no indexing by
+    // t: with two weight tiles the loop stays rolled, else the unrolled form needs more than the
+    // 256 VGPRs of two waves per SIMD; one tile is unrolled, where the moves vanish)
+    float dh[NT];
+    uint32_t shs[NT], sls[NT];
 #pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      dh[nt] = half_to_float(cur[nt].hdr[0]);
+      shs[nt] = cur[nt].hdr[0] >> 16, sls[nt] = cur[nt].hdr[1];
+    }
+#pragma unroll(NT == 1 ? 8 : 1)
     for (int t = 0; t < 8; ++t) {
-      const int ls = (int)(((sl >> (4 * t)) & 15u) | (((sh >> (2 * t)) & 3u) << 4));
-      const float dl = d * (float)(ls - 32);
-      const uint32_t q0 = cur.qs[2 * t], q1 = cur.qs[2 * t + 1];
-      const uint32_t i0 = (g >= 2 ? q0 >> 4 : q0) & 0x0F0F0F0Fu, i1 = (g >= 2 ? q1 >> 4 : q1) & 0x0F0F0F0Fu;
-      const bf16x8 bk = __builtin_bit_cast(bf16x8, grid_bf16x8(i0, i1));
+      float dl[NT];
+      bf16x8 bk[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int ls = (int)((sls[nt] & 15u) | ((shs[nt] & 3u) << 4));
+        sls[nt] >>= 4, shs[nt] >>= 2;
+        dl[nt] = dh[nt] * (float)(ls - 32);
+        const uint32_t q0 = cur[nt].qs[0], q1 = cur[nt].qs[1];
+#pragma unroll
+        for (int j = 0; j < 14; ++j) cur[nt].qs[j] = cur[nt].qs[j + 2];
+        const uint32_t i0 = (g >= 2 ? q0 >> 4 : q0) & 0x0F0F0F0Fu, i1 = (g >= 2 ? q1 >> 4 : q1) & 0x0F0F0F0Fu;
+        bk[nt] = __builtin_bit_cast(bf16x8, grid_bf16x8(i0, i1));
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int off = (16 * mt + ln) * kXStride + 2 * (32 * t + 8 * g);
         const bf16x8 ah = __builtin_bit_cast(bf16x8, *(const u32x4*)(Xh + off));
         const bf16x8 al = __builtin_bit_cast(bf16x8, *(const u32x4*)(Xl + off));
-        f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bk, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bk, D, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(dl, D[i], acc[mt][i]);
+        for (int nt = 0; nt < NT; ++nt) {
+          f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bk[nt], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bk[nt], D, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mt][nt][i] = fmaf(dl[nt], D[i], acc[mt][nt][i]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);  // one sub-block's operands live at a time
     }
     if (b + 1 < nb) {
       store_x(smem + ((b + 1) & 1) * kBuf);
-      cur = nxt;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) cur[nt] = nxt[nt];
     }
     __syncthreads();
   }
-  const int n = n0 + ln;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = n0 + 16 * nt + ln;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + 16 * mt + 4 * g + i;
-      if (m < M && n < N) y.put((size_t)m * ldy + n, acc[mt][i]);
-    }
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mt + 4 * g + i;
+        if (m < M && n < N) y.put((size_t)m * ldy + n, acc[mt][nt][i]);
+      }
+  }
 }
 
 }  // namespace
@@ -189,11 +220,21 @@ int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, vo
                      lo, n4);
   constexpr int MT = 4;
   constexpr int kLds = 2 * 2 * 16 * MT * kXStride;
-  allow_lds((const void*)iq4_mtile_kernel<MT>, kLds);
-  const dim3 grid((n_rows + kIq4WgRows - 1) / kIq4WgRows, (m_rows + 16 * MT - 1) / (16 * MT));
-  hipLaunchKernelGGL(iq4_mtile_kernel<MT>, grid, dim3(64 * kIq4Waves), kLds, stream, w, row_bytes, hi,
-                     lo, k, y, ldy, m_rows, n_rows);
-  return 0;
+  const int mblocks = (m_rows + 16 * MT - 1) / (16 * MT);
+  auto go = [&](auto kern, int wg_rows) {
+    allow_lds((const void*)kern, kLds);
+    const dim3 grid((n_rows + wg_rows - 1) / wg_rows, mblocks);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kIq4Waves), kLds, stream, w, row_bytes, hi, lo, k, y,
+                       ldy, m_rows, n_rows);
+    return 0;
+  };
+  // two weight tiles per wave where that still gives at least two rounds of workgroups (measured
+  // on MI355X, the same bits: 4096 x 4096 M = 2048 311 vs 345 us, 14336 x 4096 M = 2048 999 vs
+  // 1105; at M = 512 the halved grid left CUs idle, 153 vs 96 us)
+  constexpr int kRows2 = 16 * 2 * kIq4Waves;
+  if ((long long)((n_rows + kRows2 - 1) / kRows2) * mblocks >= 2LL * cu_count())
+    return go(iq4_mtile_kernel<MT, 2>, kRows2);
+  return go(iq4_mtile_kernel<MT, 1>, 16 * kIq4Waves);
 }
 
 }  // namespace mxa

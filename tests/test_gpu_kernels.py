@@ -391,6 +391,20 @@ def test_prefill_geometry_matches_oracle(gpu, oracle, ggml_type, n, k, m) -> Non
     check_gemm(gpu, oracle, ggml_type, w, x, n, k)
 
 
+# IQ4_XS prefill: one 16-row weight tile per wave, or two where the grid still gives at least two
+# rounds of workgroups (N past whole 256-row tiles, M past whole 64-row tiles, one and two blocks)
+IQ4_PREFILL_SHAPES = [(4100, 256, 2000), (2048, 512, 4100), (300, 2048, 130), (4100, 256, 1100)]
+
+
+@pytest.mark.parametrize("n,k,m", IQ4_PREFILL_SHAPES)
+def test_iq4_xs_prefill_geometry_within_tolerance(gpu, oracle, n, k, m) -> None:
+    w = S.packed_weight(D.IQ4_XS, n, k, seed=n + 3 * k + m)
+    x = S.activations(m, k, seed=m + 11)
+    y = host(gpu.matmul(D.IQ4_XS, dev(w), dev(x), n, k))
+    rows = np.unique(np.concatenate([np.arange(0, n, max(1, n // 200)), np.arange(n - 20, n)]))
+    assert_within_tolerance(y[:, rows], oracle.gemm(D.IQ4_XS, w[rows], x, len(rows), k))
+
+
 @pytest.mark.parametrize("ggml_type", [D.Q8_0, D.Q4_K, D.Q6_K])
 @pytest.mark.parametrize("n,k,m", [(130, 256, 4), (5, 16640, 3), (70, 4096, 1), (70, 512, 130)])
 def test_decode_on_prequantized_activations(gpu, oracle, ggml_type, n, k, m) -> None:
