@@ -148,8 +148,9 @@ __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t
     const uint8_t* Xh = smem + (b & 1) * kBuf;
     const uint8_t* Xl = Xh + kRows * kXStride;
     // sub-block t's scale bits and index words move to the front as t advances (no indexing by
-    // t: with two weight tiles the loop stays rolled, else the unrolled form needs more than the
-    // 256 VGPRs of two waves per SIMD; one tile is unrolled, where the moves vanish)
+    // t). Two weight tiles unroll the loop by four (fully unrolled they need more than the 256
+    // VGPRs of two waves per SIMD; rolled, the moves cost 5% more time), one tile fully, where
+    // the moves vanish.
     float dh[NT];
     uint32_t shs[NT], sls[NT];
 #pragma unroll
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(64 * kIq4Waves) void iq4_mtile_kernel(const uint8_t
       dh[nt] = half_to_float(cur[nt].hdr[0]);
       shs[nt] = cur[nt].hdr[0] >> 16, sls[nt] = cur[nt].hdr[1];
     }
-#pragma unroll(NT == 1 ? 8 : 1)
+#pragma unroll(NT == 1 ? 8 : 4)
     for (int t = 0; t < 8; ++t) {
       float dl[NT];
       bf16x8 bk[NT];
