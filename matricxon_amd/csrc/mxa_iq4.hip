@@ -230,8 +230,8 @@ int launch_iq4_prefill(const uint8_t* w, long long row_bytes, const float* x, vo
     return 0;
   };
   // two weight tiles per wave where that still gives at least two rounds of workgroups (measured
-  // on MI355X, the same bits: 4096 x 4096 M = 2048 311 vs 345 us, 14336 x 4096 M = 2048 999 vs
-  // 1105; at M = 512 the halved grid left CUs idle, 153 vs 96 us)
+  // on MI355X per call, the same bits: 4096 x 4096 M = 2048 302 vs 340-347 us, 14336 x 4096
+  // M = 2048 947 vs 1105; at M = 512 the halved grid left CUs idle, 153 vs 96 us)
   constexpr int kRows2 = 16 * 2 * kIq4Waves;
   if ((long long)((n_rows + kRows2 - 1) / kRows2) * mblocks >= 2LL * cu_count())
     return go(iq4_mtile_kernel<MT, 2>, kRows2);
