@@ -205,11 +205,13 @@ constexpr int kDecCh = 8;                     // blocks per chunk
 constexpr int kDecQStride = kDecCh * QK + 16;
 constexpr int kDecBStride = kDecCh * 16 + 8;
 
-// kDecRT 16-row weight tiles per workgroup: 2, or 1 for Q6_K (its per-lane block bytes need twice
-// the registers; one tile keeps two waves per SIMD).
-// The body of one workgroup: weight tile `wg` of n_wg (16 kDecRT rows) against M <= 16 activation
-// rows.
-template <int TYPE, int kDecRT>
+// kDecRT 16-row weight tiles per group: 2, or 1 for Q6_K (its per-lane block bytes need twice
+// the registers; one tile keeps two waves per SIMD). The body of one workgroup: groups
+// wg * kGroups .. + kGroups - 1 of n_wg * kGroups (16 kDecRT rows each) against M <= 16
+// activation rows. A chunk's activations are staged once for all of the workgroup's groups (at
+// 16 activation rows they weigh as much as 32 weight rows of the chunk), and each (chunk, group)
+// step loads the next step's weights while it computes.
+template <int TYPE, int kDecRT, int kGroups = 1>
 __device__ __forceinline__ void mdec_rows(const uint8_t* w, long long row_bytes, const Act& act,
                                           YOut y, long long ldy, int M, int N, int wg,
                                           int n_wg) {
@@ -223,24 +225,29 @@ __device__ __forceinline__ void mdec_rows(const uint8_t* w, long long row_bytes,
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ln = lane & 15, g = lane >> 4;
-  const int n0 = xcd_tile(wg, n_wg) * 16 * kDecRT;
-  const uint8_t* rows[kDecRT];
-#pragma unroll
-  for (int t = 0; t < kDecRT; ++t) rows[t] = w + (size_t)min(n0 + 16 * t + ln, N - 1) * row_bytes;
+  const int n0 = xcd_tile(wg, n_wg) * 16 * kDecRT * kGroups;
+  auto row_of = [&](int grp, int t) {
+    return w + (size_t)min(n0 + 16 * (kDecRT * grp + t) + ln, N - 1) * row_bytes;
+  };
   const int nb = act.nb;
-  constexpr int kOut = kDecRT * 256 / 256;  // outputs per thread: kDecRT tiles x 16 x 16 / 256
-  float acc[kOut];
+  constexpr int kOut = kDecRT * 256 / 256;  // outputs per thread and group: kDecRT x 16 x 16 / 256
+  float acc[kGroups][kOut];
 #pragma unroll
-  for (int k = 0; k < kOut; ++k) acc[k] = 0.0f;
+  for (int grp = 0; grp < kGroups; ++grp)
+#pragma unroll
+    for (int k = 0; k < kOut; ++k) acc[grp][k] = 0.0f;
 
-  W cur[2][kDecRT], nxt[2][kDecRT];
-  {
-    const int cn = min(kDecCh, nb);
+  // this wave's blocks wave and wave + 4 of chunk c0 for group grp (blocks past the chunk repeat
+  // its last one: their values are never folded)
+  auto load_step = [&](W (&dst)[2][kDecRT], int c0, int grp) {
+    const int cn = min(kDecCh, nb - c0);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int t = 0; t < kDecRT; ++t) cur[i][t] = Tile::load(rows[t], min(wave + 4 * i, cn - 1), g);
-  }
+      for (int t = 0; t < kDecRT; ++t) dst[i][t] = Tile::load(row_of(grp, t), c0 + min(wave + 4 * i, cn - 1), g);
+  };
+  W cur[2][kDecRT], nxt[2][kDecRT];
+  load_step(cur, 0, 0);
   for (int c0 = 0; c0 < nb; c0 += kDecCh) {
     const int cn = min(kDecCh, nb - c0);
     // 1. the chunk's activations into LDS (rows >= M repeat row M - 1, blocks >= cn repeat the
@@ -266,53 +273,54 @@ __device__ __forceinline__ void mdec_rows(const uint8_t* w, long long row_bytes,
       const int bb = tid >> 4, r = tid & 15;
       Ad[tid] = act.d[(size_t)min(r, M - 1) * nb + c0 + min(bb, cn - 1)];
     }
-    // 2. weights of the next chunk
-    const int c1 = c0 + kDecCh;
-    if (c1 < nb) {
-      const int cn1 = min(kDecCh, nb - c1);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int t = 0; t < kDecRT; ++t) nxt[i][t] = Tile::load(rows[t], c1 + min(wave + 4 * i, cn1 - 1), g);
-    }
-    __syncthreads();
-    // 3. this wave's blocks, both tiles: values into LDS
     const ActTile A{Aq, Ab, kDecQStride, kDecBStride};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int bb = wave + 4 * i;
-      if (bb < cn) {
-        const typename Tile::F f = Tile::frag(A, bb, 0, ln, g);
+    for (int grp = 0; grp < kGroups; ++grp) {
+      // 2. the next step's weights: the next group of this chunk, or the first of the next chunk
+      const bool more = grp + 1 < kGroups || c0 + kDecCh < nb;
+      if (more) load_step(nxt, grp + 1 < kGroups ? c0 : c0 + kDecCh, grp + 1 < kGroups ? grp + 1 : 0);
+      __syncthreads();  // the chunk is in LDS; the previous step's fold has read Tp
+      // 3. this wave's blocks, every tile of the group: values into LDS
 #pragma unroll
-        for (int t = 0; t < kDecRT; ++t) {
-          const typename Tile::P pp = Tile::prep(cur[i][t], g);
-          Tile::value(pp, f, g, [&](int e, float v, float dd) {
-            Tp[t][bb][4 * g + e][ln] = v;
-            if (g == 0 && e == 0) Dp[t][bb][ln] = dd;
-          });
+      for (int i = 0; i < 2; ++i) {
+        const int bb = wave + 4 * i;
+        if (bb < cn) {
+          const typename Tile::F f = Tile::frag(A, bb, 0, ln, g);
+#pragma unroll
+          for (int t = 0; t < kDecRT; ++t) {
+            const typename Tile::P pp = Tile::prep(cur[i][t], g);
+            Tile::value(pp, f, g, [&](int e, float v, float dd) {
+              Tp[t][bb][4 * g + e][ln] = v;
+              if (g == 0 && e == 0) Dp[t][bb][ln] = dd;
+            });
+          }
         }
       }
+      __syncthreads();
+      // 4. fold the chunk's blocks in order: thread -> outputs (tile, m, n) of the group
+#pragma unroll
+      for (int k = 0; k < kOut; ++k) {
+        const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15, n = idx & 15;
+        for (int bb = 0; bb < cn; ++bb)
+          acc[grp][k] = Tile::fold(acc[grp][k], Ad[bb * 16 + m], Tp[t][bb][m][n], Dp[t][bb][n]);
+      }
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int t = 0; t < kDecRT; ++t) cur[i][t] = nxt[i][t];
+      }
     }
-    __syncthreads();
-    // 4. fold the chunk's blocks in order: thread -> outputs (tile, m, n)
+    __syncthreads();  // every fold has read Ad and Tp before the next chunk is staged
+  }
+#pragma unroll
+  for (int grp = 0; grp < kGroups; ++grp)
 #pragma unroll
     for (int k = 0; k < kOut; ++k) {
-      const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15, n = idx & 15;
-      for (int bb = 0; bb < cn; ++bb) acc[k] = Tile::fold(acc[k], Ad[bb * 16 + m], Tp[t][bb][m][n], Dp[t][bb][n]);
+      const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15;
+      const int n = n0 + 16 * (kDecRT * grp + t) + (idx & 15);
+      if (m < M && n < N) y.put((size_t)m * ldy + n, acc[grp][k]);
     }
-    __syncthreads();
-    if (c1 < nb) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int t = 0; t < kDecRT; ++t) cur[i][t] = nxt[i][t];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < kOut; ++k) {
-    const int idx = tid + 256 * k, t = idx >> 8, m = (idx >> 4) & 15, n = n0 + 16 * t + (idx & 15);
-    if (m < M && n < N) y.put((size_t)m * ldy + n, acc[k]);
-  }
 }
 
 template <int TYPE, int kDecRT>
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(256) void mdec_kernel(const uint8_t* w, long long r
 // Two waves per SIMD asked of the compiler: the chunk loop left to itself took Q6_K to 272 VGPRs
 // (one workgroup per CU instead of two; the down projection ran 1.5x longer), with the bound it
 // fits 206 VGPRs with no scratch (Q8_0 227, Q4_K 202).
-template <int TYPE, int kDecRT>
+template <int TYPE, int kDecRT, int kGroups>
 __global__ __launch_bounds__(256, 2) void moe_dec_kernel(const uint8_t* w, long long row_bytes,
                                                       long long expert_stride, Act act,
                                                       const int32_t* __restrict__ offsets,
@@ -346,8 +354,8 @@ __global__ __launch_bounds__(256, 2) void moe_dec_kernel(const uint8_t* w, long 
     a.q = act.q + (size_t)p0 * act.k;
     a.d = act.d + (size_t)p0 * act.nb;
     a.bsums = act.bsums + (size_t)p0 * act.nb * 16;
-    mdec_rows<TYPE, kDecRT>(w + (size_t)e * expert_stride, row_bytes, a, y.at((size_t)p0 * ldy), ldy,
-                            M, N, blockIdx.x, gridDim.x);
+    mdec_rows<TYPE, kDecRT, kGroups>(w + (size_t)e * expert_stride, row_bytes, a, y.at((size_t)p0 * ldy),
+                                     ldy, M, N, blockIdx.x, gridDim.x);
     __syncthreads();  // the next chunk rewrites the LDS tiles this one read
   }
 }
@@ -403,16 +411,38 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
     return -1;
   const int chunks = (max_rows + 15) / 16;
   if (chunks > 65535) return -1;
-  auto go = [&](auto kern, int rt) {
-    const int tiles = (n_rows + 16 * rt - 1) / (16 * rt);
-    hipLaunchKernelGGL(kern, dim3(tiles, n_experts, chunks), dim3(256), 0, stream, w, row_bytes,
-                       expert_stride, act, offsets, total_rows, y, ldy, n_rows);
+  // Tile groups per workgroup (each group's chunk of activations staged once for all of them):
+  // the most of 4, 2, 1 that still gives two workgroups per CU (Q8_0 at most 2: four spill).
+  // Measured on MI355X, eager forward of 8 experts top 2 (4096 x 14336; Q4_K gate / up, Q6_K
+  // down), the same bits: 16 tokens 498 vs 523 us, 128 tokens 1146 vs 1364; with four groups
+  // forced, 40 small experts at 16 tokens lost (214 vs 204 us) to the smaller grid.
+  auto go = [&](auto k1, auto k2, auto k4, int rt, int gmax) {
+    const long long want = 2LL * cu_count();
+    const int t1 = (n_rows + 16 * rt - 1) / (16 * rt);
+    auto grid_of = [&](int gs) { return (long long)((t1 + gs - 1) / gs) * n_experts * chunks; };
+    const int gs = gmax >= 4 && grid_of(4) >= want ? 4 : gmax >= 2 && grid_of(2) >= want ? 2 : 1;
+    const dim3 grid((t1 + gs - 1) / gs, n_experts, chunks);
+    if (gs == 4)
+      hipLaunchKernelGGL(k4, grid, dim3(256), 0, stream, w, row_bytes, expert_stride, act, offsets,
+                         total_rows, y, ldy, n_rows);
+    else if (gs == 2)
+      hipLaunchKernelGGL(k2, grid, dim3(256), 0, stream, w, row_bytes, expert_stride, act, offsets,
+                         total_rows, y, ldy, n_rows);
+    else
+      hipLaunchKernelGGL(k1, grid, dim3(256), 0, stream, w, row_bytes, expert_stride, act, offsets,
+                         total_rows, y, ldy, n_rows);
     return 0;
   };
   switch (type) {
-    case T_Q4_K: return go(moe_dec_kernel<T_Q4_K, 2>, 2);
-    case T_Q8_0: return go(moe_dec_kernel<T_Q8_0, 2>, 2);
-    case T_Q6_K: return go(moe_dec_kernel<T_Q6_K, 1>, 1);
+    case T_Q4_K:
+      return go(moe_dec_kernel<T_Q4_K, 2, 1>, moe_dec_kernel<T_Q4_K, 2, 2>,
+                moe_dec_kernel<T_Q4_K, 2, 4>, 2, 4);
+    case T_Q8_0:  // k4 is never taken (gmax 2): the two-group form stands in
+      return go(moe_dec_kernel<T_Q8_0, 2, 1>, moe_dec_kernel<T_Q8_0, 2, 2>,
+                moe_dec_kernel<T_Q8_0, 2, 2>, 2, 2);
+    case T_Q6_K:
+      return go(moe_dec_kernel<T_Q6_K, 1, 1>, moe_dec_kernel<T_Q6_K, 1, 2>,
+                moe_dec_kernel<T_Q6_K, 1, 4>, 1, 4);
     default: return -1;
   }
 }

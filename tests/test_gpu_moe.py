@@ -76,6 +76,31 @@ def test_grouped_rows_match_oracle(gpu, oracle, ggml_type, n, k, ci) -> None:
     assert_bit_exact(got.cpu().numpy(), want, "Q8_K given")
 
 
+# Expert matrices large enough for the launcher to stage each activation chunk once for two or
+# four groups of weight tiles per workgroup (it takes the most that still gives two workgroups per
+# CU; Q8_0 at most two), N past a whole group, an expert past 16 rows and an empty one.
+GROUPED_LARGE = [(D.Q4_K, 8200, 1024, [3, 0, 5, 16, 1, 17, 2, 4]),
+                 (D.Q6_K, 4100, 2048, [3, 0, 5, 16, 1, 17, 2, 4]),
+                 (D.Q8_0, 8200, 512, [3, 0, 5, 16, 1, 17, 2, 4]),
+                 (D.Q4_K, 4096, 1024, [2, 7, 1, 0, 9, 3, 16, 5])]
+
+
+@pytest.mark.parametrize("case", range(len(GROUPED_LARGE)))
+def test_grouped_rows_large_experts_match_oracle(gpu, oracle, case) -> None:
+    t, n, k, counts = GROUPED_LARGE[case]
+    n_experts, n_rows = len(counts), sum(counts)
+    w = expert_weights(t, n_experts, n, k, seed=70 + case)
+    x = S.activations(n_rows, k, seed=80 + case)
+    off = offsets_of(counts)
+    got = gpu.matmul_moe(t, torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(),
+                         torch.from_numpy(off).cuda(), max(counts), n, k).cpu().numpy()
+    rows = np.unique(np.concatenate([np.arange(0, n, 37), np.arange(n - 40, n)]))
+    for e in range(n_experts):
+        if counts[e]:
+            want = oracle.gemm(t, w[e][rows], x[off[e]:off[e + 1]], len(rows), k)
+            assert_bit_exact(got[off[e]:off[e + 1]][:, rows], want, f"expert {e}")
+
+
 def test_grouped_rows_with_loose_bound(gpu, oracle) -> None:
     """max_rows_per_expert above every expert's count (the module passes n_tokens): the extra
     16-row chunks find no rows and exit."""
