@@ -16,7 +16,7 @@ from collections.abc import Callable
 import torch
 from torch import nn
 
-from .gemm import HipGemm
+from .gemm import HipGemm, q8k_bytes
 
 
 def route_pairs(top_k_idx: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, torch.Tensor,
@@ -52,6 +52,9 @@ def combine_in_expert_order(contrib: torch.Tensor, order: torch.Tensor, top_k_id
     for r in range(top_k):
         out += by_pair.index_select(0, rows[:, r])
     return out
+
+
+_IQ4_XS = 23  # float activations: no Q8_K blocks
 
 
 def _is_silu(fn) -> bool:
@@ -108,10 +111,32 @@ class HipPackedMoEExperts(nn.Module):
         # names twice (the reference computes both slots) gets its extra rows by the kernel's loop
         bound = n_tokens
         gt, ut, dt = self.types
-        gate = g.matmul_moe(gt, self.gate_packed, xs, offsets, bound, self.ffn_len, n_embd)
-        up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd)
-        act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
-        down = g.matmul_moe(dt, self.down_packed, act, offsets, bound, n_embd, self.ffn_len)
+        n_pairs, dev = xs.shape[0], x.device
+        if n_pairs > 0 and _IQ4_XS not in (gt, ut) and xs.dtype in (torch.float32, torch.bfloat16):
+            # gate and up share one Q8_K quantization of the pairs' rows (the same blocks each
+            # call would write: bfloat16 values are widened exactly first)
+            wsx = torch.empty(q8k_bytes(n_pairs, n_embd), dtype=torch.uint8, device=dev)
+            g.quantize_into(xs, wsx)
+            gate = g.matmul_moe(gt, self.gate_packed, None, offsets, bound, self.ffn_len, n_embd,
+                                workspace=wsx, out=torch.empty((n_pairs, self.ffn_len),
+                                                               dtype=torch.float32, device=dev))
+            up = g.matmul_moe(ut, self.up_packed, None, offsets, bound, self.ffn_len, n_embd,
+                              workspace=wsx, out=torch.empty((n_pairs, self.ffn_len),
+                                                             dtype=torch.float32, device=dev))
+        else:
+            gate = g.matmul_moe(gt, self.gate_packed, xs, offsets, bound, self.ffn_len, n_embd)
+            up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd)
+        if n_pairs > 0 and dt != _IQ4_XS and self.dtype == torch.bfloat16 and \
+                _is_silu(self.activation):
+            # F.silu(gate) * up with torch's bfloat16 steps and the down projection's Q8_K blocks of
+            # exactly that tensor in one launch (as the one-token path does)
+            _, wsa = g.silu_mul_q8k(gate.to(self.dtype), up.to(self.dtype), want_out=False)
+            down = g.matmul_moe(dt, self.down_packed, None, offsets, bound, n_embd, self.ffn_len,
+                                workspace=wsa, out=torch.empty((n_pairs, n_embd),
+                                                               dtype=torch.float32, device=dev))
+        else:
+            act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
+            down = g.matmul_moe(dt, self.down_packed, act, offsets, bound, n_embd, self.ffn_len)
         if self._fused_combine(top_k_weights):
             # down row of pair p = its place in the sorted order
             rows = torch.empty_like(order)
