@@ -227,6 +227,19 @@ int mxa_gemm_moe_pairs_bf16(int ggml_type, const void *w, long long expert_strid
                             int out_features, int in_features, void *workspace,
                             size_t workspace_bytes, void *stream);
 
+/* Routing of MoE (token, slot) pairs by expert, one launch and no host sync: ids (n_tokens,
+ * top_k) DEVICE expert ids, int32 (ids_int64 = 0) or int64 (1), clamped into [0, n_experts).
+ * Writes DEVICE int32 arrays: offsets (n_experts + 1; offsets[e] = the pairs of experts below e),
+ * pair_tok (n_tokens * top_k: the token of each pair in expert order, tokens ascending within an
+ * expert: a stable sort), rows (n_tokens * top_k: the place of pair t * top_k + k in that order)
+ * and, unless NULL, ids32 (the ids converted to int32 as torch converts them). n_experts <= 256
+ * and n_tokens * top_k <= 2^20, else -1. The routing of `QuantizedMoEExperts.forward`
+ * (app/architectures/moe_experts.py:81-88: `top_k_idx.unique().tolist()`, then the tokens of each
+ * expert by `(top_k_idx == e).nonzero()`), as the grouped launches and the combine take it. */
+int mxa_moe_route(const void *ids, int ids_int64, int n_tokens, int top_k, int n_experts,
+                  int32_t *offsets, int32_t *pair_tok, int32_t *rows, int32_t *ids32,
+                  void *stream);
+
 /* Routing-weighted combine of MoE expert outputs, one launch: out (n_tokens, n_embd) fp32, row t =
  * the sum over token t's top_k slots k, in ascending expert id ids[t * top_k + k] (a DEVICE int32
  * array; equal ids in slot order), of down[r] * weights[t * top_k + k] with r = rows[t * top_k +

@@ -28,6 +28,7 @@ EXPORTS = (
     "mxa_gemm_moe",
     "mxa_gemm_moe_pairs",
     "mxa_gemm_moe_pairs_bf16",
+    "mxa_moe_route",
     "mxa_moe_combine",
     "mxa_gemm_multi",
     "mxa_gemm_multi_q8k",
@@ -98,6 +99,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_gemm_moe_pairs.restype = _i
     lib.mxa_gemm_moe_pairs_bf16.argtypes = [_i, _vp, _ll, _i, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_moe_pairs_bf16.restype = _i
+    lib.mxa_moe_route.argtypes = [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]
+    lib.mxa_moe_route.restype = _i
     lib.mxa_moe_combine.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]
     lib.mxa_moe_combine.restype = _i
     lib.mxa_gemm_multi.argtypes = [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]

@@ -449,6 +449,15 @@ int mxa_gemm_moe_pairs_bf16(int ggml_type, const void* w, long long expert_strid
   return check_launch();
 }
 
+int mxa_moe_route(const void* ids, int ids_int64, int n_tokens, int top_k, int n_experts,
+                  int32_t* offsets, int32_t* pair_tok, int32_t* rows, int32_t* ids32,
+                  void* stream) {
+  if (mxa::launch_moe_route(ids, ids_int64 != 0, n_tokens, top_k, n_experts, offsets, pair_tok,
+                            rows, ids32, (hipStream_t)stream) != 0)
+    return MXA_ERR_UNSUPPORTED;
+  return check_launch();
+}
+
 int mxa_moe_combine(const float* down, const int32_t* rows, const int32_t* ids,
                     const float* weights, int n_tokens, int top_k, int n_embd, int round_bf16,
                     float* out, void* stream) {

@@ -217,6 +217,13 @@ int launch_moe_lpb(int type, const uint8_t* w, long long row_bytes, long long ex
 // + k], slots in ascending ids[t top_k + k] (ties in slot order), bf16 != 0: each down value
 // rounded to bfloat16 first. top_k <= kMoeMaxTopK; -1 otherwise.
 constexpr int kMoeMaxTopK = 16;
+// MoE routing (one workgroup, stable counting sort): up to kMoeRouteMaxExperts experts and
+// kMoeRouteMaxPairs (token, slot) pairs; -1 otherwise.
+constexpr int kMoeRouteMaxExperts = 256;
+constexpr int kMoeRouteMaxPairs = 1 << 20;
+int launch_moe_route(const void* ids, bool ids64, int n_tokens, int top_k, int n_experts,
+                     int32_t* offsets, int32_t* pair_tok, int32_t* rows, int32_t* ids32,
+                     hipStream_t stream);
 int launch_moe_combine(const float* down, const int32_t* rows, const int32_t* ids,
                        const float* weights, int n_tokens, int top_k, int n_embd, int bf16,
                        float* out, hipStream_t stream);

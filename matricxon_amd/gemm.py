@@ -545,6 +545,40 @@ class HipGemm:
         self._calls += 1
         return out
 
+    MOE_ROUTE_MAX_EXPERTS = 256
+    MOE_ROUTE_MAX_PAIRS = 1 << 20
+
+    def moe_route(self, top_k_idx: torch.Tensor, num_experts: int
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        """The routing of MoE (token, slot) pairs in one launch (`mxa_moe_route`), no host sync:
+        (offsets (num_experts + 1,), pair_tok (n_pairs,), rows (n_tokens, top_k), ids32 (n_tokens,
+        top_k)), all int32 on top_k_idx's device. `pair_tok` lists each pair's token in expert
+        order (tokens ascending within an expert: a stable sort of the flattened ids clamped into
+        [0, num_experts)), `rows[t, k]` is the place of pair (t, k) in that order, `offsets`
+        delimits each expert's pairs and `ids32` is top_k_idx converted to int32. `top_k_idx`:
+        (n_tokens, top_k) int32 or int64 on the device; num_experts <= MOE_ROUTE_MAX_EXPERTS and
+        n_tokens * top_k <= MOE_ROUTE_MAX_PAIRS (else ValueError)."""
+        _require_device_tensor("top_k_idx", top_k_idx)
+        if top_k_idx.dim() != 2 or top_k_idx.dtype not in (torch.int32, torch.int64):
+            raise ValueError("top_k_idx must be an int32 or int64 (n_tokens, top_k) tensor")
+        n_tokens, top_k = top_k_idx.shape
+        if not (1 <= num_experts <= self.MOE_ROUTE_MAX_EXPERTS) or n_tokens < 1 or top_k < 1 or \
+                n_tokens * top_k > self.MOE_ROUTE_MAX_PAIRS:
+            raise ValueError(f"mxa_moe_route takes 1..{self.MOE_ROUTE_MAX_EXPERTS} experts and "
+                             f"1..{self.MOE_ROUTE_MAX_PAIRS} pairs")
+        ids = top_k_idx.contiguous()
+        device = ids.device
+        offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=device)
+        pair_tok = torch.empty(n_tokens * top_k, dtype=torch.int32, device=device)
+        rows = torch.empty((n_tokens, top_k), dtype=torch.int32, device=device)
+        ids32 = torch.empty((n_tokens, top_k), dtype=torch.int32, device=device)
+        status = self._lib.mxa_moe_route(ids.data_ptr(), int(ids.dtype == torch.int64), n_tokens,
+                                         top_k, int(num_experts), offsets.data_ptr(),
+                                         pair_tok.data_ptr(), rows.data_ptr(), ids32.data_ptr(),
+                                         _stream(device))
+        self._check(status, "mxa_moe_route", 0)
+        return offsets, pair_tok, rows, ids32
+
     def moe_combine(self, down: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                     rows: torch.Tensor | None = None, round_bf16: bool = False) -> torch.Tensor:
         """The weighted combine of MoE expert outputs in one launch (`mxa_moe_combine`): row t of

@@ -103,8 +103,16 @@ class HipPackedMoEExperts(nn.Module):
             out = self._one_token(x, top_k_weights, top_k_idx)
             if out is not None:
                 return out
-        order, offsets, pair_tok = route_pairs(top_k_idx, self.num_experts)
         g = self._gemm
+        fused = self._fused_combine(top_k_weights)
+        if fused and self.num_experts <= g.MOE_ROUTE_MAX_EXPERTS and \
+                0 < n_tokens * top_k <= g.MOE_ROUTE_MAX_PAIRS and \
+                top_k_idx.dtype in (torch.int32, torch.int64):
+            # one launch: the sort, each pair's token and place, the ids as int32 for the combine
+            order = None
+            offsets, pair_tok, rows, ids32 = g.moe_route(top_k_idx, self.num_experts)
+        else:
+            order, offsets, pair_tok = route_pairs(top_k_idx, self.num_experts)
         # the reference casts x to the layer dtype before each matmul (device_packed.py:54)
         xs = x.to(self.dtype).index_select(0, pair_tok)  # each pair's token, by expert
         # the launch is sized for one row per token and expert; an expert that a token's routing
@@ -137,7 +145,9 @@ class HipPackedMoEExperts(nn.Module):
         else:
             act = self.activation(gate.to(self.dtype)) * up.to(self.dtype)
             down = g.matmul_moe(dt, self.down_packed, act, offsets, bound, n_embd, self.ffn_len)
-        if self._fused_combine(top_k_weights):
+        if order is None:
+            return self._combine(down, rows, ids32, top_k_weights).to(x.dtype)
+        if fused:
             # down row of pair p = its place in the sorted order
             rows = torch.empty_like(order)
             rows[order] = torch.arange(order.numel(), device=order.device)

@@ -134,6 +134,29 @@ def test_grouped_rows_past_the_bound(gpu, oracle) -> None:
                              oracle.gemm(t, w[e], x[off[e]:off[e + 1]], n, k), f"expert {e}")
 
 
+# (n_tokens, top_k, n_experts, id dtype): decode and batched routings, more than one chunk of 1024
+# pairs, more distinct experts than a wave has lanes, ids outside the range, int32 ids
+ROUTE_CASES = [(1, 2, 8, torch.int64), (16, 8, 40, torch.int64), (300, 6, 256, torch.int64),
+               (2000, 4, 64, torch.int32), (5, 3, 1, torch.int64), (1030, 1, 7, torch.int32)]
+
+
+@pytest.mark.parametrize("case", range(len(ROUTE_CASES)))
+def test_route_kernel_matches_route_pairs(gpu, case) -> None:
+    """mxa_moe_route against the torch steps of route_pairs (a stable argsort of the clamped ids):
+    the same offsets, each sorted pair's token, each pair's place and the ids as int32."""
+    n_tokens, top_k, n_experts, dtype = ROUTE_CASES[case]
+    g = torch.Generator().manual_seed(case)
+    ids = torch.randint(-2, n_experts + 2, (n_tokens, top_k), generator=g).to(dtype).cuda()
+    offsets, pair_tok, rows, ids32 = gpu.moe_route(ids, n_experts)
+    order, want_off, want_tok = route_pairs(ids, n_experts)
+    assert torch.equal(offsets.cpu(), want_off.cpu())
+    assert torch.equal(pair_tok.cpu().long(), want_tok.cpu())
+    want_rows = torch.empty_like(order)
+    want_rows[order] = torch.arange(order.numel(), device=order.device)
+    assert torch.equal(rows.cpu().long().reshape(-1), want_rows.cpu())
+    assert torch.equal(ids32.cpu(), ids.cpu().to(torch.int32))
+
+
 def test_route_pairs_on_device_matches_host() -> None:
     idx = torch.tensor([[3, 0], [1, 3], [0, 2], [3, 1]], device="cuda")
     order, offsets, pair_tok = route_pairs(idx, 5)
