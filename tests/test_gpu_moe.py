@@ -101,6 +101,24 @@ def test_grouped_rows_large_experts_match_oracle(gpu, oracle, case) -> None:
             assert_bit_exact(got[off[e]:off[e + 1]][:, rows], want, f"expert {e}")
 
 
+@pytest.mark.parametrize("ggml_type", TYPES)
+def test_grouped_rows_many_per_expert_match_oracle(gpu, oracle, ggml_type) -> None:
+    """Bounds past 32 rows per expert take 64-row chunks through the prefill tile body: experts
+    with 0, 1, 63 / 64 / 65 and 150 rows (three chunks), N past a whole 128-row tile."""
+    counts = [0, 150, 3, 70, 0, 64, 65, 1, 63]
+    n, k = 700, 512
+    n_experts, n_rows = len(counts), sum(counts)
+    w = expert_weights(ggml_type, n_experts, n, k, seed=90 + ggml_type)
+    x = S.activations(n_rows, k, seed=91)
+    off = offsets_of(counts)
+    got = gpu.matmul_moe(ggml_type, torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(),
+                         torch.from_numpy(off).cuda(), max(counts), n, k).cpu().numpy()
+    for e in range(n_experts):
+        if counts[e]:
+            want = oracle.gemm(ggml_type, w[e], x[off[e]:off[e + 1]], n, k)
+            assert_bit_exact(got[off[e]:off[e + 1]], want, f"expert {e}")
+
+
 def test_grouped_rows_with_loose_bound(gpu, oracle) -> None:
     """max_rows_per_expert above every expert's count (the module passes n_tokens): the extra
     16-row chunks find no rows and exit."""
