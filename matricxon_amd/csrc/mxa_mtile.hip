@@ -451,23 +451,34 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
   // weight tile once per 64 rows instead of once per 16 (measured on MI355X, eager forward at
   // 128 tokens, the same bits: 8 experts top 2, 4096 x 14336, 607 vs 1058 us; 40 experts top 8,
   // 1536 x 512, 99-113 vs 176 us; at 16 tokens both forms tie)
-  constexpr int kMoeMtileMinRows = 32;
-  if (max_rows > kMoeMtileMinRows) {
-    constexpr int MT = 4, NT = 1, WV = 8, kRows = 16 * MT, kWgRows = 16 * NT * WV;
-    const dim3 grid((n_rows + kWgRows - 1) / kWgRows, n_experts, (max_rows + kRows - 1) / kRows);
-    auto go_mt = [&](auto kern) {
-      allow_lds((const void*)kern, 2 * kMtBuf<MT>);
-      hipLaunchKernelGGL(kern, grid, dim3(64 * WV), 2 * kMtBuf<MT>, stream, w, row_bytes,
-                         expert_stride, act, offsets, total_rows, y, ldy, n_rows);
+  // Up to 32 rows, expert matrices of 4096 rows and more take 16-row chunks through the same body
+  // (64 weight rows per 4-wave workgroup): same box, forward only, 8 experts top 2 (4096 x 14336),
+  // 8 / 16 / 24 / 32 tokens 404 / 392 / 406 / 410 vs 443 / 429 / 441 / 445 us on the decode tile;
+  // the 40 small experts (512 and 1536 rows) tie or lose, so they keep the decode tile.
+  constexpr int kMoeMtileMinRows = 32, kMoeSmallTileMinN = 4096;
+  // mt activation tiles and `waves` waves of 16 weight rows per workgroup
+  auto go_mt = [&](auto k_q4, auto k_q8, auto k_q6, int mt, int waves, int lds) {
+    const int rows = 16 * mt, wg_rows = 16 * waves;
+    const dim3 grid((n_rows + wg_rows - 1) / wg_rows, n_experts, (max_rows + rows - 1) / rows);
+    auto run = [&](auto kern) {
+      allow_lds((const void*)kern, lds);
+      hipLaunchKernelGGL(kern, grid, dim3(64 * waves), lds, stream, w, row_bytes, expert_stride,
+                         act, offsets, total_rows, y, ldy, n_rows);
       return 0;
     };
     switch (type) {
-      case T_Q4_K: return go_mt(moe_mtile_kernel<T_Q4_K, MT, NT, WV>);
-      case T_Q8_0: return go_mt(moe_mtile_kernel<T_Q8_0, MT, NT, WV>);
-      case T_Q6_K: return go_mt(moe_mtile_kernel<T_Q6_K, MT, NT, WV>);
+      case T_Q4_K: return run(k_q4);
+      case T_Q8_0: return run(k_q8);
+      case T_Q6_K: return run(k_q6);
       default: return -1;
     }
-  }
+  };
+  if (max_rows > kMoeMtileMinRows)
+    return go_mt(moe_mtile_kernel<T_Q4_K, 4, 1, 8>, moe_mtile_kernel<T_Q8_0, 4, 1, 8>,
+                 moe_mtile_kernel<T_Q6_K, 4, 1, 8>, 4, 8, 2 * kMtBuf<4>);
+  if (n_rows >= kMoeSmallTileMinN)
+    return go_mt(moe_mtile_kernel<T_Q4_K, 1, 1, 4>, moe_mtile_kernel<T_Q8_0, 1, 1, 4>,
+                 moe_mtile_kernel<T_Q6_K, 1, 1, 4>, 1, 4, 2 * kMtBuf<1>);
   // Tile groups per workgroup (each group's chunk of activations staged once for all of them):
   // the most of 4, 2, 1 that still gives two workgroups per CU (Q8_0 at most 2: four spill).
   // Measured on MI355X, eager forward of 8 experts top 2 (4096 x 14336; Q4_K gate / up, Q6_K

@@ -76,13 +76,17 @@ def test_grouped_rows_match_oracle(gpu, oracle, ggml_type, n, k, ci) -> None:
     assert_bit_exact(got.cpu().numpy(), want, "Q8_K given")
 
 
-# Expert matrices large enough for the launcher to stage each activation chunk once for two or
-# four groups of weight tiles per workgroup (it takes the most that still gives two workgroups per
-# CU; Q8_0 at most two), N past a whole group, an expert past 16 rows and an empty one.
+# Expert matrices of 4096 rows and more at bounds up to 32 rows (16-row chunks through the prefill
+# tile body), and mid-sized ones over many experts, for which the decode tile stages each
+# activation chunk once for two or four groups of weight tiles per workgroup (the most that still
+# gives two workgroups per CU; Q8_0 at most two); N past a whole tile, an empty expert, one past
+# 16 rows.
+_MANY = [int(c) for c in np.random.default_rng(5).integers(0, 4, 40)]
 GROUPED_LARGE = [(D.Q4_K, 8200, 1024, [3, 0, 5, 16, 1, 17, 2, 4]),
                  (D.Q6_K, 4100, 2048, [3, 0, 5, 16, 1, 17, 2, 4]),
                  (D.Q8_0, 8200, 512, [3, 0, 5, 16, 1, 17, 2, 4]),
-                 (D.Q4_K, 4096, 1024, [2, 7, 1, 0, 9, 3, 16, 5])]
+                 (D.Q4_K, 4096, 1024, [2, 7, 1, 0, 9, 3, 16, 5]),
+                 (D.Q4_K, 4000, 256, _MANY), (D.Q8_0, 3000, 256, _MANY), (D.Q6_K, 3000, 512, _MANY)]
 
 
 @pytest.mark.parametrize("case", range(len(GROUPED_LARGE)))
