@@ -206,24 +206,65 @@ __global__ __launch_bounds__(64 * WAVES) void mtile_kernel(const uint8_t* w, lon
                                   blockIdx.y);
 }
 
-// Grouped MoE projection for many rows per expert: as moe_dec_kernel below (expert e =
-// blockIdx.y, its rows [offsets[e], offsets[e + 1]) clamped into [0, total_rows)), but chunk
-// blockIdx.z of 16 MT rows through the row-tiled body, so that a weight tile is read once per
-// 16 MT rows of its expert instead of once per 16. The host gives the grid a chunk for every 16 MT
-// rows of its bound; a workgroup whose chunk is empty exits (one chunk per workgroup: a loop over
-// chunks made the Q6_K body spill).
+// Grouped MoE projection on the row-tiled body: every expert's rows [offsets[e], offsets[e + 1])
+// (clamped into [0, total_rows), as moe_dec_kernel below clamps them) are cut into chunks of 16 MT
+// rows, and workgroup z of the grid's third dimension takes item z of the list of (expert, chunk)
+// pairs, experts in order, so a weight tile is read once per 16 MT rows of its expert instead of
+// once per 16. Every wave finds its item from the offset table (lane l counts the chunks of
+// experts 4 l .. 4 l + 3, a wave prefix sum locates item z), so the list covers every row whatever
+// the routing: an expert that a token names twice has more rows than tokens, and the host sizes
+// the grid by n_experts + ceil(total_rows / (16 MT)), which bounds the list's length. A workgroup
+// past the list's end exits. n_experts <= 256. (One chunk per workgroup: a loop over chunks made
+// the Q6_K body spill.)
 template <int TYPE, int MT, int NT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void moe_mtile_kernel(const uint8_t* w, long long row_bytes,
                                                                long long expert_stride, Act act,
                                                                const int32_t* __restrict__ offsets,
-                                                               int total_rows, YOut y,
+                                                               int n_experts, int total_rows, YOut y,
                                                                long long ldy, int N) {
   constexpr int kRows = 16 * MT;
-  const int e = blockIdx.y;
-  const int begin = min(max(offsets[e], 0), total_rows);
-  const int end = min(max(offsets[e + 1], begin), total_rows);
-  const int p0 = begin + kRows * (int)blockIdx.z;
-  if (p0 >= end) return;  // uniform over the workgroup, before any barrier
+  const int item = blockIdx.z, lane = threadIdx.x & 63;
+  auto span = [&](int e, int& b, int& en) {
+    b = min(max(offsets[e], 0), total_rows);
+    en = min(max(offsets[e + 1], b), total_rows);
+  };
+  int cnt[4], lane_sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * lane + j;
+    int c = 0;
+    if (e < n_experts) {
+      int b, en;
+      span(e, b, en);
+      c = (en - b + kRows - 1) / kRows;
+    }
+    cnt[j] = c;
+    lane_sum += c;
+  }
+  int incl = lane_sum;  // inclusive prefix over the lanes
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  const bool mine = item >= incl - lane_sum && item < incl;
+  const uint64_t owner_mask = __ballot(mine);
+  if (owner_mask == 0) return;  // past the list: uniform over the workgroup, before any barrier
+  int e_sel = 0, c_sel = 0;
+  if (mine) {
+    int r = item - (incl - lane_sum);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (r >= 0 && r < cnt[j]) e_sel = 4 * lane + j, c_sel = r;
+      r -= cnt[j];
+    }
+  }
+  const int owner = __builtin_ctzll(owner_mask);
+  const int e = __builtin_amdgcn_readlane(e_sel, owner);
+  const int c = __builtin_amdgcn_readlane(c_sel, owner);
+  int begin, end;
+  span(e, begin, end);
+  const int p0 = begin + kRows * c;
   const int M = min(kRows, end - p0);
   Act a = act;
   a.q = act.q + (size_t)p0 * act.k;
@@ -456,14 +497,15 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
   // 8 / 16 / 24 / 32 tokens 404 / 392 / 406 / 410 vs 443 / 429 / 441 / 445 us on the decode tile;
   // the 40 small experts (512 and 1536 rows) tie or lose, so they keep the decode tile.
   constexpr int kMoeMtileMinRows = 32, kMoeSmallTileMinN = 4096;
-  // mt activation tiles and `waves` waves of 16 weight rows per workgroup
+  // mt activation tiles and `waves` waves of 16 weight rows per workgroup; the grid's third
+  // dimension bounds the (expert, chunk) list whatever the per-expert counts
   auto go_mt = [&](auto k_q4, auto k_q8, auto k_q6, int mt, int waves, int lds) {
     const int rows = 16 * mt, wg_rows = 16 * waves;
-    const dim3 grid((n_rows + wg_rows - 1) / wg_rows, n_experts, (max_rows + rows - 1) / rows);
+    const dim3 grid((n_rows + wg_rows - 1) / wg_rows, 1, n_experts + (total_rows + rows - 1) / rows);
     auto run = [&](auto kern) {
       allow_lds((const void*)kern, lds);
       hipLaunchKernelGGL(kern, grid, dim3(64 * waves), lds, stream, w, row_bytes, expert_stride,
-                         act, offsets, total_rows, y, ldy, n_rows);
+                         act, offsets, n_experts, total_rows, y, ldy, n_rows);
       return 0;
     };
     switch (type) {
@@ -473,10 +515,11 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
       default: return -1;
     }
   };
-  if (max_rows > kMoeMtileMinRows)
+  const bool list_fits = n_experts <= 256 && n_experts + (total_rows + 15) / 16 <= 65535;
+  if (list_fits && max_rows > kMoeMtileMinRows)
     return go_mt(moe_mtile_kernel<T_Q4_K, 4, 1, 8>, moe_mtile_kernel<T_Q8_0, 4, 1, 8>,
                  moe_mtile_kernel<T_Q6_K, 4, 1, 8>, 4, 8, 2 * kMtBuf<4>);
-  if (n_rows >= kMoeSmallTileMinN)
+  if (list_fits && n_rows >= kMoeSmallTileMinN)
     return go_mt(moe_mtile_kernel<T_Q4_K, 1, 1, 4>, moe_mtile_kernel<T_Q8_0, 1, 1, 4>,
                  moe_mtile_kernel<T_Q6_K, 1, 1, 4>, 1, 4, 2 * kMtBuf<1>);
   // Tile groups per workgroup (each group's chunk of activations staged once for all of them):

@@ -139,17 +139,24 @@ def test_grouped_rows_with_loose_bound(gpu, oracle) -> None:
                              oracle.gemm(t, w[e], x[off[e]:off[e + 1]], n, k), f"expert {e}")
 
 
-def test_grouped_rows_past_the_bound(gpu, oracle) -> None:
+# (type, N, K, bound, counts): the decode tile (its chunks loop), the 64-row prefill body (bound
+# past 32) and the 16-row one (N >= 4096), each with experts past the bound
+PAST_BOUND = [(D.Q6_K, 256, 1024, 16, [40, 0, 3, 33]), (D.Q4_K, 300, 512, 40, [130, 0, 3, 81]),
+              (D.Q6_K, 4100, 256, 16, [40, 0, 3, 33]), (D.Q8_0, 4100, 256, 20, [70, 1, 0, 45])]
+
+
+@pytest.mark.parametrize("case", range(len(PAST_BOUND)))
+def test_grouped_rows_past_the_bound(gpu, oracle, case) -> None:
     """max_rows_per_expert below an expert's count (a token routed twice to one expert gives it
-    more rows than tokens): the launch's chunks loop until every row is computed."""
-    counts = [40, 0, 3, 33]
-    n, k, t = 256, 1024, D.Q6_K
+    more rows than tokens): every row is still computed (the decode tile's chunks loop; the
+    prefill-body forms take their (expert, chunk) list from the offsets)."""
+    t, n, k, bound, counts = PAST_BOUND[case]
     w = expert_weights(t, len(counts), n, k, seed=7)
     x = S.activations(sum(counts), k, seed=8)
     off = offsets_of(counts)
     out = torch.full((sum(counts), n), float("nan"), dtype=torch.float32, device="cuda")
     got = gpu.matmul_moe(t, torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(),
-                         torch.from_numpy(off).cuda(), 16, n, k, out=out).cpu().numpy()
+                         torch.from_numpy(off).cuda(), bound, n, k, out=out).cpu().numpy()
     for e in range(len(counts)):
         if counts[e]:
             assert_bit_exact(got[off[e]:off[e + 1]],
@@ -272,7 +279,20 @@ def test_module_repeated_expert_in_a_tokens_routing(dtype) -> None:
     types = (D.Q4_K, D.Q4_K, D.Q6_K)
     n_tokens = 20
     mod, per_expert = build_experts(types, 4, 512, 256, dtype, seed=31)
-    x = torch.from_numpy(S.activations(n_tokens, 512, seed=32)).cuda().to(dtype)
+    _check_repeated_routing(mod, per_expert, n_tokens, 512)
+
+
+@pytest.mark.parametrize("n_tokens,ffn", [(40, 256), (20, 4096)])
+def test_module_repeated_expert_past_the_bound_on_prefill_tiles(n_tokens, ffn) -> None:
+    """The same repeated routing where the grouped launch takes the prefill tile body: a bound
+    past 32 rows (64-row chunks) and a 4096-row expert matrix (16-row chunks)."""
+    types = (D.Q4_K, D.Q4_K, D.Q6_K)
+    mod, per_expert = build_experts(types, 4, 512, ffn, torch.bfloat16, seed=34)
+    _check_repeated_routing(mod, per_expert, n_tokens, 512)
+
+
+def _check_repeated_routing(mod, per_expert, n_tokens: int, n_embd: int) -> None:
+    x = torch.from_numpy(S.activations(n_tokens, n_embd, seed=32)).cuda().to(mod.dtype)
     tidx = torch.full((n_tokens, 2), 2, dtype=torch.int64, device="cuda")
     tidx[::7] = 1
     tw = torch.rand(n_tokens, 2, generator=torch.Generator().manual_seed(33)).cuda()
