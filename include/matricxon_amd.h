@@ -202,6 +202,16 @@ int mxa_gemm_moe(int ggml_type, const void *w, long long expert_stride, int n_ex
                  float *y, int out_features, int in_features, void *workspace,
                  size_t workspace_bytes, void *stream);
 
+/* mxa_gemm_moe writing bfloat16 y (2-byte aligned): each output the float32 result rounded to
+ * nearest even as torch's cast rounds it, so the layer's bfloat16 gate and up projections need no
+ * separate cast launch. No counterpart in the reference's C library: its MoE experts on the GPU
+ * run in the layer's bfloat16 (app/architectures/moe_experts.py:81-88 through
+ * device_packed.py:53-63). */
+int mxa_gemm_moe_bf16(int ggml_type, const void *w, long long expert_stride, int n_experts,
+                      const float *x, const int32_t *offsets, int n_rows, int max_rows_per_expert,
+                      void *y, int out_features, int in_features, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
 /* One token's routed experts (MoE decode), one launch: pair p of n_pairs multiplies expert
  * ids[p] (a DEVICE int32 array; ids outside [0, n_experts) are clamped) at w + ids[p] *
  * expert_stride (out_features x row bytes) by activation row p of x (x_rows == n_pairs) or by the

@@ -26,6 +26,7 @@ EXPORTS = (
     "mxa_gemv_f32",
     "mxa_gemm_q8k",
     "mxa_gemm_moe",
+    "mxa_gemm_moe_bf16",
     "mxa_gemm_moe_pairs",
     "mxa_gemm_moe_pairs_bf16",
     "mxa_moe_route",
@@ -95,6 +96,8 @@ def load() -> ctypes.CDLL:
     lib.mxa_gemm_q8k.restype = _i
     lib.mxa_gemm_moe.argtypes = [_i, _vp, _ll, _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_moe.restype = _i
+    lib.mxa_gemm_moe_bf16.argtypes = [_i, _vp, _ll, _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp, _sz, _vp]
+    lib.mxa_gemm_moe_bf16.restype = _i
     lib.mxa_gemm_moe_pairs.argtypes = [_i, _vp, _ll, _i, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _sz, _vp]
     lib.mxa_gemm_moe_pairs.restype = _i
     lib.mxa_gemm_moe_pairs_bf16.argtypes = [_i, _vp, _ll, _i, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _sz, _vp]

@@ -351,12 +351,14 @@ int mxa_gemm_q8k_bf16(int ggml_type, const void* w, void* y, int n_tokens, int o
                        in_features, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_experts,
-                 const float* x, const int32_t* offsets, int n_rows, int max_rows_per_expert,
-                 float* y, int out_features, int in_features, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+namespace {
+
+int gemm_moe_core(int ggml_type, const void* w, long long expert_stride, int n_experts,
+                  const float* x, const int32_t* offsets, int n_rows, int max_rows_per_expert,
+                  mxa::YOut y, int out_features, int in_features, void* workspace,
+                  size_t workspace_bytes, void* stream) {
   if (!mxa_supports(ggml_type, in_features) || w == nullptr || offsets == nullptr ||
-      y == nullptr || n_experts < 1 || n_rows < 1 || out_features < 1 ||
+      (y.v & ~(uintptr_t)1) == 0 || n_experts < 1 || n_rows < 1 || out_features < 1 ||
       max_rows_per_expert < 1 || !aligned(w, 4) || !aligned(x, 16) || !aligned(workspace, 16))
     return MXA_ERR_UNSUPPORTED;
   // every expert's weight starts as aligned as mxa_gemm asks of its w
@@ -367,7 +369,7 @@ int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_ex
     if (x == nullptr) return MXA_ERR_UNSUPPORTED;
     const mxa::Act act = make_act(x, nullptr, in_features);
     if (mxa::launch_moe_lpb(ggml_type, (const uint8_t*)w, rb, expert_stride, n_experts, act,
-                            offsets, n_rows, min(max_rows_per_expert, n_rows), mxa::YOut::f32(y),
+                            offsets, n_rows, min(max_rows_per_expert, n_rows), y,
                             out_features, out_features, (hipStream_t)stream) != 0)
       return MXA_ERR_UNSUPPORTED;
     return check_launch();
@@ -379,10 +381,32 @@ int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_ex
   if (x != nullptr) mxa::launch_quantize_q8k(x, buf, n_rows, in_features, s);
   const mxa::Act act = make_act(x, &buf, in_features);
   if (mxa::launch_moe_dec(ggml_type, (const uint8_t*)w, rb, expert_stride, n_experts, act,
-                          offsets, n_rows, min(max_rows_per_expert, n_rows), mxa::YOut::f32(y),
+                          offsets, n_rows, min(max_rows_per_expert, n_rows), y,
                           out_features, out_features, s) != 0)
     return MXA_ERR_UNSUPPORTED;
   return check_launch();
+}
+
+}  // namespace
+
+int mxa_gemm_moe(int ggml_type, const void* w, long long expert_stride, int n_experts,
+                 const float* x, const int32_t* offsets, int n_rows, int max_rows_per_expert,
+                 float* y, int out_features, int in_features, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (y == nullptr) return MXA_ERR_UNSUPPORTED;
+  return gemm_moe_core(ggml_type, w, expert_stride, n_experts, x, offsets, n_rows,
+                       max_rows_per_expert, mxa::YOut::f32(y), out_features, in_features,
+                       workspace, workspace_bytes, stream);
+}
+
+int mxa_gemm_moe_bf16(int ggml_type, const void* w, long long expert_stride, int n_experts,
+                      const float* x, const int32_t* offsets, int n_rows, int max_rows_per_expert,
+                      void* y, int out_features, int in_features, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  if (y == nullptr || !aligned(y, 2)) return MXA_ERR_UNSUPPORTED;
+  return gemm_moe_core(ggml_type, w, expert_stride, n_experts, x, offsets, n_rows,
+                       max_rows_per_expert, mxa::YOut::bf16(y), out_features, in_features,
+                       workspace, workspace_bytes, stream);
 }
 
 int mxa_gemm_moe_pairs(int ggml_type, const void* w, long long expert_stride, int n_experts,

@@ -444,15 +444,17 @@ class HipGemm:
     def matmul_moe(self, ggml_type: int, experts: torch.Tensor, x: torch.Tensor | None,
                    offsets: torch.Tensor, max_rows_per_expert: int, out_features: int,
                    in_features: int, workspace: torch.Tensor | None = None,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
         """Grouped projection of packed MoE experts (`mxa_gemm_moe`), one launch for all of
         them: `experts` (n_experts, out_features, row_bytes) uint8 on the device; rows
         [offsets[e], offsets[e + 1]) of `x` (n_rows, in_features) go through expert e
         (`offsets`: int32 on the device, n_experts + 1 ascending values from 0 to n_rows, so no
         host sync). x None: `workspace` already holds the Q8_K activations of the n_rows rows.
         Returns (n_rows, out_features) float32; each row equals `matmul` of that row alone bit
-        for bit. Replaces the per-expert calls of QuantizedMoEExperts.forward
-        (app/architectures/moe_experts.py:81-88)."""
+        for bit. `out_dtype` bfloat16 writes the result as bfloat16, each value the float32
+        result rounded as torch's cast rounds it (`mxa_gemm_moe_bf16`). Replaces the per-expert
+        calls of QuantizedMoEExperts.forward (app/architectures/moe_experts.py:81-88)."""
         ggml_type = int(ggml_type)
         _require_device_tensor("experts", experts)
         device = experts.device
@@ -475,23 +477,26 @@ class HipGemm:
             n_rows = out.shape[0] if out is not None else -1
             if n_rows < 0:
                 raise ValueError("matmul_moe on a prequantized workspace needs `out` (n_rows rows)")
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"out_dtype must be float32 or bfloat16, not {out_dtype}")
         if out is None:
-            out = torch.empty((n_rows, out_features), dtype=torch.float32, device=device)
-        elif out.shape != (n_rows, out_features) or out.dtype != torch.float32 or \
+            out = torch.empty((n_rows, out_features), dtype=out_dtype, device=device)
+        elif out.shape != (n_rows, out_features) or out.dtype != out_dtype or \
                 not out.is_contiguous() or out.device != device:
-            raise ValueError("out must be a contiguous float32 (n_rows, out_features) tensor")
+            raise ValueError(f"out must be a contiguous {out_dtype} (n_rows, out_features) tensor")
         if n_rows == 0:
             return out
         if workspace is None and ggml_type != 23:  # IQ4_XS multiplies the float rows: none
             workspace = torch.empty(q8k_bytes(n_rows, in_features), dtype=torch.uint8,
                                     device=device)
-        status = self._lib.mxa_gemm_moe(
+        name = "mxa_gemm_moe_bf16" if out_dtype == torch.bfloat16 else "mxa_gemm_moe"
+        status = getattr(self._lib, name)(
             ggml_type, experts.data_ptr(), rb * out_features, n_experts,
             None if x32 is None else x32.data_ptr(), offsets.data_ptr(), n_rows,
             max(1, min(int(max_rows_per_expert), n_rows)), out.data_ptr(), out_features,
             in_features, None if workspace is None else workspace.data_ptr(),
             0 if workspace is None else workspace.numel(), _stream(device))
-        self._check(status, "mxa_gemm_moe", ggml_type)
+        self._check(status, name, ggml_type)
         self._calls += 1
         return out
 

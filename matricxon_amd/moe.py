@@ -120,6 +120,9 @@ class HipPackedMoEExperts(nn.Module):
         bound = n_tokens
         gt, ut, dt = self.types
         n_pairs, dev = xs.shape[0], x.device
+        # a bfloat16 layer's projections return bfloat16 (device_packed.py:53-58): the launches
+        # write gate and up rounded as that cast rounds them
+        gu = torch.bfloat16 if self.dtype == torch.bfloat16 else torch.float32
         if n_pairs > 0 and _IQ4_XS not in (gt, ut) and xs.dtype in (torch.float32, torch.bfloat16):
             # gate and up share one Q8_K quantization of the pairs' rows (the same blocks each
             # call would write: bfloat16 values are widened exactly first)
@@ -127,13 +130,17 @@ class HipPackedMoEExperts(nn.Module):
             g.quantize_into(xs, wsx)
             gate = g.matmul_moe(gt, self.gate_packed, None, offsets, bound, self.ffn_len, n_embd,
                                 workspace=wsx, out=torch.empty((n_pairs, self.ffn_len),
-                                                               dtype=torch.float32, device=dev))
+                                                               dtype=gu, device=dev),
+                                out_dtype=gu)
             up = g.matmul_moe(ut, self.up_packed, None, offsets, bound, self.ffn_len, n_embd,
                               workspace=wsx, out=torch.empty((n_pairs, self.ffn_len),
-                                                             dtype=torch.float32, device=dev))
+                                                             dtype=gu, device=dev),
+                              out_dtype=gu)
         else:
-            gate = g.matmul_moe(gt, self.gate_packed, xs, offsets, bound, self.ffn_len, n_embd)
-            up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd)
+            gate = g.matmul_moe(gt, self.gate_packed, xs, offsets, bound, self.ffn_len, n_embd,
+                                out_dtype=gu)
+            up = g.matmul_moe(ut, self.up_packed, xs, offsets, bound, self.ffn_len, n_embd,
+                              out_dtype=gu)
         if n_pairs > 0 and dt != _IQ4_XS and self.dtype == torch.bfloat16 and \
                 _is_silu(self.activation):
             # F.silu(gate) * up with torch's bfloat16 steps and the down projection's Q8_K blocks of

@@ -308,6 +308,36 @@ def test_module_rejects_types_without_a_kernel() -> None:
         HipPackedMoEExperts(z, z, z, 13, 13, 13, 256, 256, F.silu)
 
 
+# the grouped launch's bodies: the 16-row decode tile (small bounds, 40 experts), the 64-row
+# prefill tile (bounds past 32) and, for IQ4_XS, the float-row kernel
+GROUPED_BF16 = [(D.Q4_K, 512, 1024, COUNTS[0]), (D.Q6_K, 300, 2048, COUNTS[0]),
+                (D.Q8_0, 700, 512, [0, 150, 3, 70, 0, 64, 65, 1, 63]),
+                (D.Q4_K, 700, 512, [0, 150, 3, 70, 0, 64, 65, 1, 63]),
+                (D.Q4_K, 4000, 256, _MANY), (D.IQ4_XS, 512, 1024, COUNTS[0])]
+
+
+@pytest.mark.parametrize("case", range(len(GROUPED_BF16)))
+def test_grouped_bf16_equal_the_float32_result_cast(gpu, case) -> None:
+    """`mxa_gemm_moe_bf16` writes each output as the float32 launch's value rounded by torch's
+    cast, bit for bit, on float rows and on prequantized Q8_K blocks (x None)."""
+    t, n, k, counts = GROUPED_BF16[case]
+    n_experts, n_rows = len(counts), sum(counts)
+    w = torch.from_numpy(expert_weights(t, n_experts, n, k, seed=200 + case)).cuda()
+    x = torch.from_numpy(S.activations(n_rows, k, seed=210 + case)).cuda()
+    off = torch.from_numpy(offsets_of(counts)).cuda()
+    want = gpu.matmul_moe(t, w, x, off, max(counts), n, k)
+    got = gpu.matmul_moe(t, w, x, off, max(counts), n, k, out_dtype=torch.bfloat16)
+    assert got.dtype == torch.bfloat16 and got.shape == want.shape
+    assert torch.equal(got.view(torch.int16), want.to(torch.bfloat16).view(torch.int16))
+    if t != D.IQ4_XS:
+        ws = torch.empty(q8k_bytes(n_rows, k), dtype=torch.uint8, device="cuda")
+        gpu.quantize_into(x, ws)
+        pre = gpu.matmul_moe(t, w, None, off, max(counts), n, k, workspace=ws,
+                             out=torch.empty((n_rows, n), dtype=torch.bfloat16, device="cuda"),
+                             out_dtype=torch.bfloat16)
+        assert torch.equal(pre.view(torch.int16), got.view(torch.int16))
+
+
 @pytest.mark.parametrize("n,k", [(512, 1024), (300, 2048)])
 @pytest.mark.parametrize("ci", range(len(COUNTS)))
 def test_grouped_iq4_xs_rows_equal_single_rows(gpu, n, k, ci) -> None:
