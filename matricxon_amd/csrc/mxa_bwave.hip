@@ -449,6 +449,11 @@ __global__ __launch_bounds__(512) void bwave_multi_kernel(BwSegs segs, uint32_t 
                                  ldy, wg - sg.wg0);
 }
 
+template <int C>
+constexpr int ncw_of(int nb) {
+  return (nb + C - 1) / C;  // waves per workgroup: C blocks of each row per wave
+}
+
 // The resident geometry of R rows per workgroup of nb-block rows: the pack word and its LDS bytes;
 // false when the rows need the ring form or do not fit.
 template <int TYPE, int C>
@@ -478,14 +483,12 @@ bool bw_resident(int nb, int R, int depth, uint32_t* pack, int* lds) {
   return true;
 }
 
+// The launch geometry of R rows per workgroup of nb-block rows at `depth` tiles in flight: the
+// pack word, the LDS bytes and whether the rows take the ring form; false when they fit neither.
 template <int TYPE, int C>
-int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
-              int N, int depth, hipStream_t stream) {
+bool bw_plan(int nb, int R, int depth, uint32_t* pack, int* lds, bool* ring) {
   constexpr int TB = kBwBlockBytes<TYPE>;
   constexpr int kStage = a_stage_bytes<TYPE>(C);
-  const int nb = act.nb;
-  const int ncu = cu_count();
-  const int R = (int)((N + (long long)ncu - 1) / ncu);
   const int T = (R + 15) / 16;
   const int ncw = (nb + C - 1) / C;
   // the widest row piece of any wave, in 16-byte chunks, made odd (bank spread of the 16 rows)
@@ -498,33 +501,94 @@ int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, lon
   const int ncp = (16 * rs + 63) / 64;
   const int slot_bytes = 16 * rs * 16;
   // values [C][16][16] and d [C][16] fit a slot; the scales of a row in four 16-byte loads
-  if (ncp > kBwMaxCopies || ncw > 16 || nb % 4 != 0 || (C * 256 + C * 16) * 4 > slot_bytes ||
-      R > 0xFFF || rs > 0xFF || ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF)
-    return -1;
+  if (R < 1 || ncp > kBwMaxCopies || ncw > 16 || nb % 4 != 0 ||
+      (C * 256 + C * 16) * 4 > slot_bytes || R > 0xFFF || rs > 0xFF)
+    return false;
   // Resident: every tile's slot stays in LDS, the operands' staging area in the last two tiles'
   // slots when those are requested only after the operands are read (T - 2 >= D), else an area
   // of its own.
   int D = max(1, min(depth, min(T, 15)));
   const bool in_slots = T - 2 >= D && 2 * slot_bytes >= kStage;
   const int lds_res = ncw * T * slot_bytes + (in_slots ? 0 : ncw * kStage);
-  bool ring = T > kBwMaxTiles || lds_res > kBwLds;
-  int lds = lds_res;
-  if (ring) {
+  *ring = T > kBwMaxTiles || lds_res > kBwLds;
+  *lds = lds_res;
+  if (*ring) {
     // S = D + 1 slots per wave and the value ring; the staging area from slot index D on
     for (D = min(depth, 15); D >= 1; --D) {
-      lds = (D + 1) * ncw * slot_bytes + 2 * kBwValBytes;
-      if (lds <= kBwLds && ncw * kStage <= ncw * slot_bytes + 2 * kBwValBytes) break;
+      *lds = (D + 1) * ncw * slot_bytes + 2 * kBwValBytes;
+      if (*lds <= kBwLds && ncw * kStage <= ncw * slot_bytes + 2 * kBwValBytes) break;
     }
-    if (D < 1) return -1;
+    if (D < 1) return false;
   }
-  const uint32_t pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24 |
-                        (uint32_t)(!ring && in_slots) << 29;
+  *pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24 |
+          (uint32_t)(!*ring && in_slots) << 29;
+  return true;
+}
+
+template <int TYPE, int C>
+int launch_bw(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
+              int N, int depth, hipStream_t stream) {
+  const int nb = act.nb;
+  const int ncu = cu_count();
+  const int R = (int)((N + (long long)ncu - 1) / ncu);
+  uint32_t pack;
+  int lds;
+  bool ring;
+  if (ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF || !bw_plan<TYPE, C>(nb, R, depth, &pack, &lds, &ring))
+    return -1;
   const uint32_t packm = (uint32_t)M | (uint32_t)nb << 8;
   auto kern = ring ? bwave_kernel<TYPE, C, true> : bwave_kernel<TYPE, C, false>;
   allow_lds((const void*)kern, kBwLds);
   const int grid = (int)((N + (long long)R - 1) / R);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * ncw), lds, stream, w, pack, packm, N,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * ncw_of<C>(nb)), lds, stream, w, pack, packm, N,
                      (int)row_bytes, act.q, act.bsums, act.d, y, (int)ldy);
+  return 0;
+}
+
+// Grouped MoE experts: rows [offsets[e], offsets[e + 1]) of the activations (clamped into
+// [0, total_rows)) go through expert e, whose weight starts at w + e * expert_stride. The rows are
+// cut into 16-row chunks, and workgroup wg = blockIdx.x % wpe of item blockIdx.x / wpe of the
+// (expert, chunk) list runs the batched-decode body on its R rows of that expert's weight for the
+// chunk; a workgroup past the list's end exits. (One chunk per workgroup, so an expert that a
+// token names twice, with more rows than tokens, is still covered: a loop over chunks spilled.)
+template <int TYPE, int C, bool RING>
+__global__ __launch_bounds__(C == 1 ? 1024 : 512) void moe_bwave_kernel(
+    const uint8_t* __restrict__ w, long long expert_stride, uint32_t pack, int nb, int N,
+    int row_bytes, const int8_t* q, const int16_t* bsums, const float* d,
+    const int32_t* __restrict__ offsets, int n_experts, int total_rows, YOut y, int ldy, int wpe) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  int e, p0, m;
+  if (!moe_chunk_item(offsets, n_experts, total_rows, 16, (int)blockIdx.x / wpe, e, p0, m)) return;
+  bwave_rows<TYPE, C, RING>(smem, w + (size_t)e * expert_stride, pack,
+                            (uint32_t)m | (uint32_t)nb << 8, N, row_bytes,
+                            q + (size_t)p0 * nb * QK, bsums + (size_t)p0 * nb * 16,
+                            d + (size_t)p0 * nb, y.at((long long)p0 * ldy), ldy,
+                            (int)blockIdx.x % wpe);
+}
+
+template <int TYPE, int C>
+int launch_moe_bw(const uint8_t* w, long long row_bytes, long long expert_stride, int n_experts,
+                  const Act& act, const int32_t* offsets, int total_rows, YOut y, long long ldy,
+                  int N, int depth, hipStream_t stream) {
+  const int nb = act.nb;
+  // at most min(n_experts, total_rows) experts have rows: their workgroups fill the CUs
+  const long long busy = min(n_experts, total_rows);
+  const int R = (int)((N * busy + cu_count() - 1) / cu_count());
+  uint32_t pack;
+  int lds;
+  bool ring;
+  if (ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF || !bw_plan<TYPE, C>(nb, R, depth, &pack, &lds, &ring))
+    return -1;
+  // the list has at most n_experts + ceil(total_rows / 16) items (each expert's last chunk may
+  // be partial)
+  const int wpe = (N + R - 1) / R;
+  const long long items = n_experts + (total_rows + 15LL) / 16;
+  if (wpe * items > 0x7FFFFFFF) return -1;
+  auto kern = ring ? moe_bwave_kernel<TYPE, C, true> : moe_bwave_kernel<TYPE, C, false>;
+  allow_lds((const void*)kern, kBwLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(wpe * items)), dim3(64 * ncw_of<C>(nb)), lds, stream,
+                     w, expert_stride, pack, nb, N, (int)row_bytes, act.q, act.bsums, act.d,
+                     offsets, n_experts, total_rows, y, (int)ldy, wpe);
   return 0;
 }
 
@@ -814,6 +878,23 @@ int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act
     case T_Q4_K: return launch_bw<T_Q4_K, 2>(w, row_bytes, act, y, ldy, m_rows, n_rows, kDepth, stream);
     case T_Q6_K: return launch_bw<T_Q6_K, 2>(w, row_bytes, act, y, ldy, m_rows, n_rows, kDepth, stream);
     case T_Q8_0: return launch_bw<T_Q8_0, 1>(w, row_bytes, act, y, ldy, m_rows, n_rows, kDepth, stream);
+    default: return -1;
+  }
+}
+
+int launch_moe_bwave(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                     int n_experts, const Act& act, const int32_t* offsets, int total_rows,
+                     YOut y, long long ldy, int n_rows, hipStream_t stream) {
+  if (act.q == nullptr || act.nb > 16 || n_experts < 1 || n_experts > 256 || total_rows < 1 ||
+      n_rows < 1)
+    return -1;
+  if ((((uintptr_t)w | (uintptr_t)row_bytes | (uintptr_t)expert_stride) & 15) != 0) return -1;
+  // the depth and blocks per wave of the single-matrix launch above
+  constexpr int kDepth = 2;
+  switch (type) {
+    case T_Q4_K: return launch_moe_bw<T_Q4_K, 2>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, kDepth, stream);
+    case T_Q6_K: return launch_moe_bw<T_Q6_K, 2>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, kDepth, stream);
+    case T_Q8_0: return launch_moe_bw<T_Q8_0, 1>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, kDepth, stream);
     default: return -1;
   }
 }

@@ -239,4 +239,58 @@ __device__ __forceinline__ int xcd_tile(int wg, int n_wg) {
   return x * q + (x < r ? x : r) + k;
 }
 
+// Item `item` of a grouped MoE launch's (expert, chunk) work list: the rows [offsets[e],
+// offsets[e + 1]) of expert e (clamped into [0, total_rows)) cut into chunks of `rows`, experts in
+// order. One wave-wide prefix sum locates it (lane l counts the chunks of experts 4 l .. 4 l + 3,
+// so n_experts <= 256): its expert e, first row p0 and row count m (1 .. rows). False past the
+// list's end. Every lane of the wave must call it; the results are uniform over the wave.
+__device__ __forceinline__ bool moe_chunk_item(const int32_t* __restrict__ offsets, int n_experts,
+                                               int total_rows, int rows, int item, int& e,
+                                               int& p0, int& m) {
+  const int lane = threadIdx.x & 63;
+  auto span = [&](int x, int& b, int& en) {
+    b = min(max(offsets[x], 0), total_rows);
+    en = min(max(offsets[x + 1], b), total_rows);
+  };
+  int cnt[4], lane_sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int x = 4 * lane + j;
+    int c = 0;
+    if (x < n_experts) {
+      int b, en;
+      span(x, b, en);
+      c = (en - b + rows - 1) / rows;
+    }
+    cnt[j] = c;
+    lane_sum += c;
+  }
+  int incl = lane_sum;  // inclusive prefix over the lanes
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  const bool mine = item >= incl - lane_sum && item < incl;
+  const uint64_t owner_mask = __ballot(mine);
+  if (owner_mask == 0) return false;
+  int e_sel = 0, c_sel = 0;
+  if (mine) {
+    int r = item - (incl - lane_sum);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (r >= 0 && r < cnt[j]) e_sel = 4 * lane + j, c_sel = r;
+      r -= cnt[j];
+    }
+  }
+  const int owner = __builtin_ctzll(owner_mask);
+  e = __builtin_amdgcn_readlane(e_sel, owner);
+  const int c = __builtin_amdgcn_readlane(c_sel, owner);
+  int begin, end;
+  span(e, begin, end);
+  p0 = begin + rows * c;
+  m = min(rows, end - p0);
+  return true;
+}
+
 }  // namespace mxa

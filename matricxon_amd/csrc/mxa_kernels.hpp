@@ -245,6 +245,13 @@ int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act
 // take the group.
 int launch_bwave_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
                        hipStream_t stream);
+// Grouped MoE experts on the batched-decode body (rows of up to 16 blocks): rows
+// [offsets[e], offsets[e + 1]) of the Q8_K activations through the expert at w + e *
+// expert_stride, in 16-row passes; -1 when the geometry does not fit (the caller takes another
+// grouped form).
+int launch_moe_bwave(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
+                     int n_experts, const Act& act, const int32_t* offsets, int total_rows,
+                     YOut y, long long ldy, int n_rows, hipStream_t stream);
 
 // Batched decode (m_rows <= 16, rows of up to 16 blocks) with the workgroup's whole weight share
 // resident in LDS, streamed in by copy waves while compute waves run the matrix cores

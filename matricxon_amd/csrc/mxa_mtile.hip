@@ -222,50 +222,9 @@ __global__ __launch_bounds__(64 * WAVES) void moe_mtile_kernel(const uint8_t* w,
                                                                const int32_t* __restrict__ offsets,
                                                                int n_experts, int total_rows, YOut y,
                                                                long long ldy, int N) {
-  constexpr int kRows = 16 * MT;
-  const int item = blockIdx.z, lane = threadIdx.x & 63;
-  auto span = [&](int e, int& b, int& en) {
-    b = min(max(offsets[e], 0), total_rows);
-    en = min(max(offsets[e + 1], b), total_rows);
-  };
-  int cnt[4], lane_sum = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = 4 * lane + j;
-    int c = 0;
-    if (e < n_experts) {
-      int b, en;
-      span(e, b, en);
-      c = (en - b + kRows - 1) / kRows;
-    }
-    cnt[j] = c;
-    lane_sum += c;
-  }
-  int incl = lane_sum;  // inclusive prefix over the lanes
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int v = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += v;
-  }
-  const bool mine = item >= incl - lane_sum && item < incl;
-  const uint64_t owner_mask = __ballot(mine);
-  if (owner_mask == 0) return;  // past the list: uniform over the workgroup, before any barrier
-  int e_sel = 0, c_sel = 0;
-  if (mine) {
-    int r = item - (incl - lane_sum);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (r >= 0 && r < cnt[j]) e_sel = 4 * lane + j, c_sel = r;
-      r -= cnt[j];
-    }
-  }
-  const int owner = __builtin_ctzll(owner_mask);
-  const int e = __builtin_amdgcn_readlane(e_sel, owner);
-  const int c = __builtin_amdgcn_readlane(c_sel, owner);
-  int begin, end;
-  span(e, begin, end);
-  const int p0 = begin + kRows * c;
-  const int M = min(kRows, end - p0);
+  int e, p0, M;
+  // past the list: uniform over the workgroup, before any barrier
+  if (!moe_chunk_item(offsets, n_experts, total_rows, 16 * MT, blockIdx.z, e, p0, M)) return;
   Act a = act;
   a.q = act.q + (size_t)p0 * act.k;
   a.d = act.d + (size_t)p0 * act.nb;
@@ -515,6 +474,12 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
       default: return -1;
     }
   };
+  // Up to 16 rows per expert, expert matrices of 4096 rows and more of up to 16 blocks take the
+  // batched-decode body, the CUs shared among the experts that can have rows
+  if (max_rows <= 16 && n_rows >= kMoeSmallTileMinN &&
+      launch_moe_bwave(type, w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y,
+                       ldy, n_rows, stream) == 0)
+    return 0;
   const bool list_fits = n_experts <= 256 && n_experts + (total_rows + 15) / 16 <= 65535;
   if (list_fits && max_rows > kMoeMtileMinRows)
     return go_mt(moe_mtile_kernel<T_Q4_K, 4, 1, 8>, moe_mtile_kernel<T_Q8_0, 4, 1, 8>,
