@@ -607,17 +607,16 @@ int launch_moe_bw(const uint8_t* w, long long row_bytes, long long expert_stride
 // oracle and the other decode kernels bit for bit. Every part starts on a 16-byte boundary of the
 // row (PB * block bytes a multiple of 16), so a wave's per-lane copy offsets serve every unit.
 template <int TYPE, int C>
-__global__ __launch_bounds__(512) void bwlong_kernel(const uint8_t* __restrict__ w, uint32_t pack,
-                                                     uint32_t packm, int N, int row_bytes,
-                                                     const int8_t* q, const int16_t* bsums,
-                                                     const float* d, YOut y, int ldy) {
+__device__ __forceinline__ void bwlong_rows(uint8_t* smem, const uint8_t* __restrict__ w,
+                                            uint32_t pack, uint32_t packm, int N, int row_bytes,
+                                            const int8_t* q, const int16_t* bsums, const float* d,
+                                            YOut y, int ldy, int wg) {
   using Tile = typename BwTileOf<TYPE>::T;
   using F = typename Tile::F;
   constexpr int TB = kBwBlockBytes<TYPE>;
   constexpr int kStageA = a_stage_bytes<TYPE>(C);
   constexpr int kStage = kStageA + 256;  // then the scales: row r's 16 bytes at 16 r
   constexpr int kNA = 4 * C + (TYPE != T_Q8_0 ? 1 : 0) + 1;  // staging copies of a unit
-  extern __shared__ __align__(16) uint8_t smem[];
 
   const int R = pack & 0xFFF, rs = (pack >> 12) & 0xFF, D = (pack >> 20) & 0xF;
   const int ncw = (pack >> 24) & 0x1F;
@@ -628,7 +627,7 @@ __global__ __launch_bounds__(512) void bwlong_kernel(const uint8_t* __restrict__
 
   const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r0 = (int)blockIdx.x * R;
+  const int r0 = wg * R;
   const int rows = min(R, N - r0);  // >= 1: the grid is ceil(N / R)
   const int T = (rows + 15) >> 4;
   const int PB = ncw * C, P = (nb + PB - 1) / PB, U = T * P;
@@ -767,29 +766,88 @@ __global__ __launch_bounds__(512) void bwlong_kernel(const uint8_t* __restrict__
 }
 
 template <int TYPE, int C>
-int launch_bwl(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
-               int N, int ncw, int depth, hipStream_t stream) {
+__global__ __launch_bounds__(512) void bwlong_kernel(const uint8_t* __restrict__ w, uint32_t pack,
+                                                     uint32_t packm, int N, int row_bytes,
+                                                     const int8_t* q, const int16_t* bsums,
+                                                     const float* d, YOut y, int ldy) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  bwlong_rows<TYPE, C>(smem, w, pack, packm, N, row_bytes, q, bsums, d, y, ldy, (int)blockIdx.x);
+}
+
+// The long-row body for grouped MoE experts, as moe_bwave_kernel runs the short-row one: item
+// blockIdx.x / wpe of the (expert, 16-row chunk) list, its rows of workgroup blockIdx.x % wpe.
+template <int TYPE, int C>
+__global__ __launch_bounds__(512) void moe_bwlong_kernel(
+    const uint8_t* __restrict__ w, long long expert_stride, uint32_t pack, int nb, int N,
+    int row_bytes, const int8_t* q, const int16_t* bsums, const float* d,
+    const int32_t* __restrict__ offsets, int n_experts, int total_rows, YOut y, int ldy, int wpe) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  int e, p0, m;
+  if (!moe_chunk_item(offsets, n_experts, total_rows, 16, (int)blockIdx.x / wpe, e, p0, m)) return;
+  bwlong_rows<TYPE, C>(smem, w + (size_t)e * expert_stride, pack, (uint32_t)m | (uint32_t)nb << 8,
+                       N, row_bytes, q + (size_t)p0 * nb * QK, bsums + (size_t)p0 * nb * 16,
+                       d + (size_t)p0 * nb, y.at((long long)p0 * ldy), ldy, (int)blockIdx.x % wpe);
+}
+
+// The long-row geometry of R rows per workgroup, ncw waves of C blocks per part, at `depth`
+// units in flight: the pack word and the LDS bytes; false when it does not fit.
+template <int TYPE, int C>
+bool bwl_plan(int nb, int R, int ncw, int depth, uint32_t* pack, int* lds) {
   constexpr int TB = kBwBlockBytes<TYPE>;
   constexpr int kStage = a_stage_bytes<TYPE>(C) + 256;
-  const int nb = act.nb, PB = ncw * C;
-  const int ncu = cu_count();
-  const int R = (int)((N + (long long)ncu - 1) / ncu);
+  const int PB = ncw * C;
   int nch = 0;  // the widest row piece of a wave within a part, in 16-byte chunks, made odd
   for (int wv = 0; wv < ncw; ++wv) nch = max(nch, ((wv + 1) * C * TB + 15) / 16 - (wv * C * TB) / 16);
   const int rs = nch | 1;
   const int ncp = (16 * rs + 63) / 64;
   const int slot_bytes = kStage + 16 * rs * 16;
   const int val_bytes = PB * (256 + 16 + 16) * 4;
-  if (nb <= 16 || nb > 255 || nb % 4 != 0 || (PB * TB) % 16 != 0 || PB > 16 || ncp > kBwMaxCopies ||
-      R > 0xFFF || rs > 0xFF || ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF)
-    return -1;
-  int D = min(depth, 15), lds = 0;
+  if (R < 1 || nb <= 16 || nb > 255 || nb % 4 != 0 || (PB * TB) % 16 != 0 || PB > 16 ||
+      ncp > kBwMaxCopies || R > 0xFFF || rs > 0xFF)
+    return false;
+  int D = min(depth, 15);
   for (; D >= 1; --D) {
-    lds = D * ncw * slot_bytes + 2 * val_bytes;
-    if (lds <= kBwLds) break;
+    *lds = D * ncw * slot_bytes + 2 * val_bytes;
+    if (*lds <= kBwLds) break;
   }
-  if (D < 1) return -1;
-  const uint32_t pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24;
+  if (D < 1) return false;
+  *pack = (uint32_t)R | (uint32_t)rs << 12 | (uint32_t)D << 20 | (uint32_t)ncw << 24;
+  return true;
+}
+
+template <int TYPE, int C>
+int launch_moe_bwl(const uint8_t* w, long long row_bytes, long long expert_stride, int n_experts,
+                   const Act& act, const int32_t* offsets, int total_rows, YOut y, long long ldy,
+                   int N, int ncw, int depth, hipStream_t stream) {
+  const int nb = act.nb;
+  // at most min(n_experts, total_rows) experts have rows: their workgroups fill the CUs
+  const long long busy = min(n_experts, total_rows);
+  const int R = (int)((N * busy + cu_count() - 1) / cu_count());
+  uint32_t pack;
+  int lds;
+  if (ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF || !bwl_plan<TYPE, C>(nb, R, ncw, depth, &pack, &lds))
+    return -1;
+  const int wpe = (N + R - 1) / R;
+  const long long items = n_experts + (total_rows + 15LL) / 16;
+  if (wpe * items > 0x7FFFFFFF) return -1;
+  auto kern = moe_bwlong_kernel<TYPE, C>;
+  allow_lds((const void*)kern, kBwLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(wpe * items)), dim3(64 * ncw), lds, stream, w,
+                     expert_stride, pack, nb, N, (int)row_bytes, act.q, act.bsums, act.d, offsets,
+                     n_experts, total_rows, y, (int)ldy, wpe);
+  return 0;
+}
+
+template <int TYPE, int C>
+int launch_bwl(const uint8_t* w, long long row_bytes, const Act& act, YOut y, long long ldy, int M,
+               int N, int ncw, int depth, hipStream_t stream) {
+  const int nb = act.nb;
+  const int ncu = cu_count();
+  const int R = (int)((N + (long long)ncu - 1) / ncu);
+  uint32_t pack;
+  int lds;
+  if (ldy > 0x7FFFFFFF || row_bytes > 0x7FFFFFFF || !bwl_plan<TYPE, C>(nb, R, ncw, depth, &pack, &lds))
+    return -1;
   const uint32_t packm = (uint32_t)M | (uint32_t)nb << 8;
   auto kern = bwlong_kernel<TYPE, C>;
   allow_lds((const void*)kern, kBwLds);
@@ -885,11 +943,19 @@ int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act
 int launch_moe_bwave(int type, const uint8_t* w, long long row_bytes, long long expert_stride,
                      int n_experts, const Act& act, const int32_t* offsets, int total_rows,
                      YOut y, long long ldy, int n_rows, hipStream_t stream) {
-  if (act.q == nullptr || act.nb > 16 || n_experts < 1 || n_experts > 256 || total_rows < 1 ||
-      n_rows < 1)
+  if (act.q == nullptr || n_experts < 1 || n_experts > 256 || total_rows < 1 || n_rows < 1)
     return -1;
   if ((((uintptr_t)w | (uintptr_t)row_bytes | (uintptr_t)expert_stride) & 15) != 0) return -1;
-  // the depth and blocks per wave of the single-matrix launch above
+  // the parts, depths and blocks per wave of the single-matrix launches above
+  if (act.nb > 16) {
+    constexpr int kLongDepth = 1;
+    switch (type) {
+      case T_Q4_K: return launch_moe_bwl<T_Q4_K, 1>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, 8, kLongDepth, stream);
+      case T_Q6_K: return launch_moe_bwl<T_Q6_K, 1>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, 8, kLongDepth, stream);
+      case T_Q8_0: return launch_moe_bwl<T_Q8_0, 1>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, 8, kLongDepth, stream);
+      default: return -1;
+    }
+  }
   constexpr int kDepth = 2;
   switch (type) {
     case T_Q4_K: return launch_moe_bw<T_Q4_K, 2>(w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y, ldy, n_rows, kDepth, stream);

@@ -245,7 +245,7 @@ int launch_bwave(int type, const uint8_t* w, long long row_bytes, const Act& act
 // take the group.
 int launch_bwave_multi(const DecodeSeg* seg, int count, const Act& act, long long ldy, int m_rows,
                        hipStream_t stream);
-// Grouped MoE experts on the batched-decode body (rows of up to 16 blocks): rows
+// Grouped MoE experts on the batched-decode bodies (short and long rows): rows
 // [offsets[e], offsets[e + 1]) of the Q8_K activations through the expert at w + e *
 // expert_stride, in 16-row passes; -1 when the geometry does not fit (the caller takes another
 // grouped form).

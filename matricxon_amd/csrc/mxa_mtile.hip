@@ -474,8 +474,8 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
       default: return -1;
     }
   };
-  // Up to 16 rows per expert, expert matrices of 4096 rows and more of up to 16 blocks take the
-  // batched-decode body, the CUs shared among the experts that can have rows
+  // Up to 16 rows per expert, expert matrices of 4096 rows and more take the batched-decode
+  // bodies (short and long rows), the CUs shared among the experts that can have rows
   if (max_rows <= 16 && n_rows >= kMoeSmallTileMinN &&
       launch_moe_bwave(type, w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y,
                        ldy, n_rows, stream) == 0)

@@ -90,7 +90,10 @@ GROUPED_LARGE = [(D.Q4_K, 8200, 1024, [3, 0, 5, 16, 1, 17, 2, 4]),
                  # up to 16 rows per expert on the batched-decode body: resident and ring forms
                  (D.Q6_K, 4100, 2048, [3, 0, 5, 16, 1, 12, 2, 4]),
                  (D.Q8_0, 8200, 1024, [16, 1, 0, 7, 9]),
-                 (D.Q4_K, 14336, 1024, [2, 7, 1, 0, 9, 3, 16, 5])]
+                 (D.Q4_K, 14336, 1024, [2, 7, 1, 0, 9, 3, 16, 5]),
+                 # long rows (more than 16 blocks) on the batched-decode body
+                 (D.Q6_K, 4096, 14336, [3, 0, 5, 16, 1, 12, 2, 4]),
+                 (D.Q4_K, 4100, 5120, [16, 2, 0, 9]), (D.Q8_0, 4096, 8192, [5, 16, 1])]
 
 
 @pytest.mark.parametrize("case", range(len(GROUPED_LARGE)))
@@ -144,13 +147,13 @@ def test_grouped_rows_with_loose_bound(gpu, oracle) -> None:
 
 
 # (type, N, K, bound, counts): the decode tile (its chunks loop), the 64-row prefill body (bound
-# past 32), the 16-row one (N >= 4096) and the batched-decode body (N >= 4096, bound <= 16,
-# resident and ring forms), each with experts past the bound
+# past 32), the 16-row one (N >= 4096) and the batched-decode bodies (N >= 4096, bound <= 16,
+# resident, ring and long-row forms), each with experts past the bound
 PAST_BOUND = [(D.Q6_K, 256, 1024, 16, [40, 0, 3, 33]), (D.Q4_K, 300, 512, 40, [130, 0, 3, 81]),
               (D.Q6_K, 4100, 256, 16, [40, 0, 3, 33]), (D.Q8_0, 4100, 256, 20, [70, 1, 0, 45]),
               (D.Q4_K, 4096, 1024, 16, [40, 0, 3, 17]),
               (D.Q6_K, 14336, 1024, 8, [20, 5, 0, 9, 1, 16, 3, 2]),
-              (D.Q8_0, 4096, 4096, 12, [16, 30, 0, 1])]
+              (D.Q8_0, 4096, 4096, 12, [16, 30, 0, 1]), (D.Q6_K, 4096, 5120, 16, [33, 2, 0, 17])]
 
 
 @pytest.mark.parametrize("case", range(len(PAST_BOUND)))
