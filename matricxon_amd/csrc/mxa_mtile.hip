@@ -474,12 +474,14 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
       default: return -1;
     }
   };
-  // Up to 64 rows per expert, expert matrices of 4096 rows and more take the batched-decode
+  // Up to 96 rows per expert, expert matrices of 4096 rows and more take the batched-decode
   // bodies (short and long rows) in 16-row chunks, the CUs shared among the experts that can have
   // rows. Measured on MI355X, eager forward of 8 experts top 2 (4096 x 14336), the same bits:
-  // 16 / 24 / 32 / 48 / 64 tokens 304 / 299 / 298 / 538 / 536 us against 395 / 415 / 414 / 571 /
-  // 596 on the prefill tile bodies (96 tokens: 607 either way, so larger bounds keep those).
-  constexpr int kMoeDecodeBodyMaxRows = 64;
+  // 16 / 24 / 32 / 48 / 64 / 80 / 96 tokens 304 / 299 / 298 / 538 / 536 / 558 / 545 us against
+  // 395 / 415 / 414 / 571 / 596 / 608 / 598 on the prefill tile bodies; at 112 / 128 tokens the
+  // decode bodies lose (786 / 794 vs 594 / 607 us: more 16-row chunks per expert), so larger bounds
+  // keep the prefill tile body.
+  constexpr int kMoeDecodeBodyMaxRows = 96;
   if (max_rows <= kMoeDecodeBodyMaxRows && n_rows >= kMoeSmallTileMinN &&
       launch_moe_bwave(type, w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y,
                        ldy, n_rows, stream) == 0)

@@ -94,8 +94,10 @@ GROUPED_LARGE = [(D.Q4_K, 8200, 1024, [3, 0, 5, 16, 1, 17, 2, 4]),
                  # long rows (more than 16 blocks) on the batched-decode body
                  (D.Q6_K, 4096, 14336, [3, 0, 5, 16, 1, 12, 2, 4]),
                  (D.Q4_K, 4100, 5120, [16, 2, 0, 9]), (D.Q8_0, 4096, 8192, [5, 16, 1]),
-                 # bounds up to 64: several 16-row chunks of one expert
-                 (D.Q6_K, 4096, 5120, [64, 0, 33, 1, 17]), (D.Q4_K, 4096, 1024, [48, 50, 3])]
+                 # bounds up to 96: several 16-row chunks of one expert; past 96 the prefill
+                 # tile body
+                 (D.Q6_K, 4096, 5120, [64, 0, 33, 1, 17]), (D.Q4_K, 4096, 1024, [48, 50, 3]),
+                 (D.Q4_K, 4096, 1024, [90, 5, 70]), (D.Q6_K, 4096, 1024, [100, 3, 0, 40])]
 
 
 @pytest.mark.parametrize("case", range(len(GROUPED_LARGE)))
