@@ -474,15 +474,18 @@ int launch_moe_dec(int type, const uint8_t* w, long long row_bytes, long long ex
       default: return -1;
     }
   };
-  // Up to 96 rows per expert, expert matrices of 4096 rows and more take the batched-decode
+  // Up to 96 rows per expert, expert matrices of 1024 rows and more take the batched-decode
   // bodies (short and long rows) in 16-row chunks, the CUs shared among the experts that can have
-  // rows. Measured on MI355X, eager forward of 8 experts top 2 (4096 x 14336), the same bits:
+  // rows. Measured on MI355X, eager forward of 64 experts top 8 (2048 x 1024) at 4 / 16 / 32 / 64
+  // tokens 100 / 171 / 188 / 204 us against 123 / 170 / 186 / 222 on the decode tile and prefill
+  // tile bodies, 16 experts top 4 (3072 x 2048) 104 / 97 / 109 / 166 against 135 / 131 / 140 /
+  // 178; 8 experts top 2 (4096 x 14336), the same bits:
   // 16 / 24 / 32 / 48 / 64 / 80 / 96 tokens 304 / 299 / 298 / 538 / 536 / 558 / 545 us against
   // 395 / 415 / 414 / 571 / 596 / 608 / 598 on the prefill tile bodies; at 112 / 128 tokens the
   // decode bodies lose (786 / 794 vs 594 / 607 us: more 16-row chunks per expert), so larger bounds
   // keep the prefill tile body.
-  constexpr int kMoeDecodeBodyMaxRows = 96;
-  if (max_rows <= kMoeDecodeBodyMaxRows && n_rows >= kMoeSmallTileMinN &&
+  constexpr int kMoeDecodeBodyMaxRows = 96, kMoeDecodeBodyMinN = 1024;
+  if (max_rows <= kMoeDecodeBodyMaxRows && n_rows >= kMoeDecodeBodyMinN &&
       launch_moe_bwave(type, w, row_bytes, expert_stride, n_experts, act, offsets, total_rows, y,
                        ldy, n_rows, stream) == 0)
     return 0;

@@ -97,7 +97,10 @@ GROUPED_LARGE = [(D.Q4_K, 8200, 1024, [3, 0, 5, 16, 1, 17, 2, 4]),
                  # bounds up to 96: several 16-row chunks of one expert; past 96 the prefill
                  # tile body
                  (D.Q6_K, 4096, 5120, [64, 0, 33, 1, 17]), (D.Q4_K, 4096, 1024, [48, 50, 3]),
-                 (D.Q4_K, 4096, 1024, [90, 5, 70]), (D.Q6_K, 4096, 1024, [100, 3, 0, 40])]
+                 (D.Q4_K, 4096, 1024, [90, 5, 70]), (D.Q6_K, 4096, 1024, [100, 3, 0, 40]),
+                 # expert matrices of 1024 to 4096 rows on the batched-decode bodies
+                 (D.Q4_K, 1024, 2048, [5, 0, 9, 16, 2]), (D.Q6_K, 2048, 1024, [3, 17, 1]),
+                 (D.Q8_0, 1500, 4096, [7, 0, 2]), (D.Q6_K, 3072, 5120, [2, 11, 0, 4])]
 
 
 @pytest.mark.parametrize("case", range(len(GROUPED_LARGE)))
