@@ -35,37 +35,26 @@ def _require_divisible(in_features: int) -> int:
     return in_features // _QK_K
 
 
-def _qgemv(ggml_type: int, x: torch.Tensor, raw: torch.Tensor, out_features: int,
-           in_features: int) -> torch.Tensor:
-    _require_divisible(in_features)
-    gemm = HipGemm.get()
-    packed = raw.reshape(out_features, gemm.row_bytes(ggml_type, in_features))
-    y = gemm.gemv_f32(ggml_type, packed, x.reshape(1, in_features), out_features, in_features)
-    return y.reshape(out_features)
+def _qgemv_of(ggml_type: int, name: str, weight: str):
+    """The reference-named GEMV for one type: (x, raw, out_features, in_features) -> y."""
+
+    def qgemv(x: torch.Tensor, raw: torch.Tensor, out_features: int,
+              in_features: int) -> torch.Tensor:
+        _require_divisible(in_features)
+        gemm = HipGemm.get()
+        packed = raw.reshape(out_features, gemm.row_bytes(ggml_type, in_features))
+        y = gemm.gemv_f32(ggml_type, packed, x.reshape(1, in_features), out_features, in_features)
+        return y.reshape(out_features)
+
+    qgemv.__name__ = qgemv.__qualname__ = name
+    qgemv.__doc__ = f"{weight} weight: y = x @ W.T, x in float32."
+    return qgemv
 
 
-def qgemv_q4_k(x: torch.Tensor, raw: torch.Tensor, out_features: int,
-               in_features: int) -> torch.Tensor:
-    """Q4_K weight (out_features rows of in_features / 256 144-byte blocks): y = x @ W.T."""
-    return _qgemv(_Q4_K, x, raw, out_features, in_features)
-
-
-def qgemv_q6_k(x: torch.Tensor, raw: torch.Tensor, out_features: int,
-               in_features: int) -> torch.Tensor:
-    """Q6_K weight (210-byte blocks of 256 values): y = x @ W.T."""
-    return _qgemv(_Q6_K, x, raw, out_features, in_features)
-
-
-def qgemv_q8_0(x: torch.Tensor, raw: torch.Tensor, out_features: int,
-               in_features: int) -> torch.Tensor:
-    """Q8_0 weight (34-byte blocks of 32 values): y = x @ W.T."""
-    return _qgemv(_Q8_0, x, raw, out_features, in_features)
-
-
-def qgemv_iq4_xs(x: torch.Tensor, raw: torch.Tensor, out_features: int,
-                 in_features: int) -> torch.Tensor:
-    """IQ4_XS weight (136-byte blocks of 256 values): y = x @ W.T."""
-    return _qgemv(_IQ4_XS, x, raw, out_features, in_features)
+qgemv_q4_k = _qgemv_of(_Q4_K, "qgemv_q4_k", "Q4_K (144-byte blocks of 256 values)")
+qgemv_q6_k = _qgemv_of(_Q6_K, "qgemv_q6_k", "Q6_K (210-byte blocks of 256 values)")
+qgemv_q8_0 = _qgemv_of(_Q8_0, "qgemv_q8_0", "Q8_0 (34-byte blocks of 32 values)")
+qgemv_iq4_xs = _qgemv_of(_IQ4_XS, "qgemv_iq4_xs", "IQ4_XS (136-byte blocks of 256 values)")
 
 
 GEMV_KERNELS: dict[int, tuple[callable, int]] = {
