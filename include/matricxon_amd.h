@@ -186,8 +186,8 @@ int mxa_gemm_q8k(int ggml_type, const void *w, const float *x, float *y, int n_t
  * rows [offsets[e], offsets[e + 1]) of x (n_rows, in_features) fp32, writing the same rows of
  * y (n_rows, out_features). `offsets` is a DEVICE int32 array of n_experts + 1 ascending values
  * from 0 to n_rows (the rows grouped by expert), so routing needs no host sync;
- * max_rows_per_expert sizes the launch (the rows an expert usually has, e.g. n_tokens); an
- * expert with more rows is still computed whole, by looping. x == NULL:
+ * max_rows_per_expert picks the launch's form (the rows an expert usually has, e.g. n_tokens);
+ * an expert with more rows is still computed whole, in more chunks. x == NULL:
  * `workspace` already holds the Q8_K activations of the n_rows rows (mxa_quantize_q8_k,
  * mxa_silu_mul_q8_k). workspace: mxa_quantize_q8_k's layout for n_rows rows. Each row equals
  * mxa_gemm of that row alone bit for bit. Q4_K, Q6_K, Q8_0; IQ4_XS multiplies the float rows of x
