@@ -262,6 +262,12 @@ MODULE_CASES = [
     ((D.Q6_K, D.Q6_K, D.Q4_K), 8, 256, 512, 1, 2, torch.float32),
     # one bfloat16 token through the fused steps, the down projection on 56-block rows
     ((D.Q4_K, D.Q4_K, D.Q6_K), 4, 1024, 14336, 1, 2, torch.bfloat16),
+    # batched-decode bodies for the grouped projections (experts of 1024 rows and more, bounds
+    # up to 96): OLMoE-like 64 experts top 8, long down rows, float32 and Q8_0 down
+    ((D.Q4_K, D.Q4_K, D.Q6_K), 64, 2048, 1024, 16, 8, torch.bfloat16),
+    ((D.Q4_K, D.Q4_K, D.Q6_K), 64, 2048, 1024, 64, 8, torch.bfloat16),
+    ((D.Q4_K, D.Q4_K, D.Q6_K), 8, 1024, 5120, 12, 2, torch.bfloat16),
+    ((D.Q6_K, D.Q6_K, D.Q8_0), 6, 2048, 1024, 20, 2, torch.float32),
 ]
 
 
