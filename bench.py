@@ -503,6 +503,7 @@ MOE_CASES = [
     # (name, n_experts, top_k, n_embd, ffn_len, types gate/up/down)
     ("mixtral-8x7b-like", 8, 2, 4096, 14336, (Q4_K, Q4_K, Q6_K)),
     ("granite-moe-3b-like", 40, 8, 1536, 512, (Q4_K, Q4_K, Q6_K)),
+    ("olmoe-1b-7b-like", 64, 8, 2048, 1024, (Q4_K, Q4_K, Q6_K)),
 ]
 
 
